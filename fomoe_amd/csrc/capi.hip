@@ -1,0 +1,451 @@
+// capi.hip — host side of the C-ABI declared in include/gpu.h.
+//
+// One context = one device, one stream, lazily grown scratch. Every launch is
+// argument-checked on the host against the shapes the kernels cover before
+// anything reaches the device.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "gpu.h"
+#include "kernels.h"
+
+using namespace fo;
+
+struct gpu_ctx {
+    int device = 0;
+    int n_cu = 0;
+    uint64_t hbm = 0;
+    char arch[64] = {0};
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::string err;
+
+    // scratch (device)
+    float *logits = nullptr;       // [1024]
+    unsigned *counter = nullptr;   // router completion counter
+    int32_t *ids = nullptr;        // [16]
+    float *weights = nullptr;      // [17]
+    uint8_t *xq_h = nullptr;       size_t xq_h_cap = 0;
+    uint8_t *xq_act = nullptr;     size_t xq_act_cap = 0;
+    float *act = nullptr;          size_t act_cap = 0;
+    float *act2 = nullptr;         size_t act2_cap = 0;
+    float *vec_in = nullptr;       size_t vec_in_cap = 0;
+    float *vec_out = nullptr;      size_t vec_out_cap = 0;
+    uint8_t *staging = nullptr;    size_t staging_cap = 0;
+    int last_k = 0;
+
+    // captured stack-decode graph
+    hipGraphExec_t graph_exec = nullptr;
+};
+
+static int fail(gpu_ctx *c, int code, const char *fmt, ...) {
+    if (c) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        c->err = buf;
+    }
+    return code;
+}
+
+#define HIPC(call)                                                                         \
+    do {                                                                                   \
+        hipError_t e_ = (call);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return fail(ctx, e_ == hipErrorInvalidValue ? -1 : -2, "%s: %s (%s:%d)", #call, \
+                        hipGetErrorString(e_), __FILE__, __LINE__);                        \
+    } while (0)
+
+// Grow a device scratch buffer to at least `need` bytes (never inside a
+// captured region: callers size everything first).
+template <typename Tp>
+static hipError_t ensure(Tp *&p, size_t &cap, size_t need) {
+    if (cap >= need) return hipSuccess;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    hipError_t e = hipMalloc((void **)&p, need);
+    if (e == hipSuccess) cap = need;
+    return e;
+}
+
+static bool kquant(int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K; }
+static bool matvec_type(int t) { return kquant(t) || t == GGML_TYPE_Q8_0; }
+
+extern "C" {
+
+gpu_ctx_t *gpu_init(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return nullptr;
+    gpu_ctx *c = new gpu_ctx();
+    c->device = 0;
+    hipDeviceProp_t prop;
+    if (hipSetDevice(0) != hipSuccess || hipGetDeviceProperties(&prop, 0) != hipSuccess) {
+        delete c;
+        return nullptr;
+    }
+    c->n_cu = prop.multiProcessorCount;
+    c->hbm = prop.totalGlobalMem;
+    snprintf(c->arch, sizeof c->arch, "%s", prop.gcnArchName);
+    bool ok = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) == hipSuccess &&
+              hipEventCreate(&c->ev0) == hipSuccess && hipEventCreate(&c->ev1) == hipSuccess &&
+              hipMalloc((void **)&c->logits, 1024 * sizeof(float)) == hipSuccess &&
+              hipMalloc((void **)&c->counter, 256) == hipSuccess &&
+              hipMalloc((void **)&c->ids, 64 * sizeof(int32_t)) == hipSuccess &&
+              hipMalloc((void **)&c->weights, 64 * sizeof(float)) == hipSuccess &&
+              hipMemset(c->counter, 0, 256) == hipSuccess &&
+              hipMemset(c->ids, 0, 64 * sizeof(int32_t)) == hipSuccess &&
+              hipDeviceSynchronize() == hipSuccess;
+    if (!ok) {
+        gpu_free(c);
+        return nullptr;
+    }
+    return c;
+}
+
+void gpu_free(gpu_ctx_t *c) {
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+    void *bufs[] = {c->logits, c->counter, c->ids, c->weights, c->xq_h, c->xq_act, c->act,
+                    c->act2, c->vec_in, c->vec_out, c->staging};
+    for (void *p : bufs)
+        if (p) (void)hipFree(p);
+    if (c->ev0) (void)hipEventDestroy(c->ev0);
+    if (c->ev1) (void)hipEventDestroy(c->ev1);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char *gpu_last_error(gpu_ctx_t *c) { return c ? c->err.c_str() : "null context"; }
+
+int gpu_device_info(gpu_ctx_t *ctx, int *n_cu, uint64_t *hbm, char *arch, int arch_len) {
+    if (!ctx) return -1;
+    if (n_cu) *n_cu = ctx->n_cu;
+    if (hbm) *hbm = ctx->hbm;
+    if (arch && arch_len > 0) snprintf(arch, (size_t)arch_len, "%s", ctx->arch);
+    return 0;
+}
+
+void *gpu_alloc(gpu_ctx_t *ctx, uint64_t bytes) {
+    if (!ctx || bytes == 0) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        fail(ctx, -2, "hipMalloc(%llu) failed", (unsigned long long)bytes);
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+
+void gpu_dealloc(gpu_ctx_t *ctx, void *p) {
+    if (ctx && p) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(p);
+    }
+}
+
+int gpu_upload(gpu_ctx_t *ctx, void *d, const void *h, uint64_t bytes) {
+    if (!ctx || (!d && bytes) || (!h && bytes)) return fail(ctx, -1, "gpu_upload: null pointer");
+    if (!bytes) return 0;
+    HIPC(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIPC(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int gpu_download(gpu_ctx_t *ctx, void *h, const void *d, uint64_t bytes) {
+    if (!ctx || (!d && bytes) || (!h && bytes)) return fail(ctx, -1, "gpu_download: null pointer");
+    if (!bytes) return 0;
+    HIPC(hipMemcpyAsync(h, d, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIPC(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int gpu_sync(gpu_ctx_t *ctx) {
+    if (!ctx) return -1;
+    HIPC(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int gpu_timer_start(gpu_ctx_t *ctx) {
+    if (!ctx) return -1;
+    HIPC(hipEventRecord(ctx->ev0, ctx->stream));
+    return 0;
+}
+
+float gpu_timer_stop(gpu_ctx_t *ctx) {
+    if (!ctx) return -1.f;
+    float ms = -1.f;
+    if (hipEventRecord(ctx->ev1, ctx->stream) != hipSuccess ||
+        hipEventSynchronize(ctx->ev1) != hipSuccess ||
+        hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1) != hipSuccess)
+        return -1.f;
+    return ms;
+}
+
+// ------------------------------------------------------------------ kernels
+int gpu_dequantize(gpu_ctx_t *ctx, int type, const void *src, float *dst, int64_t n) {
+    if (!ctx || !src || !dst || n <= 0) return fail(ctx, -1, "gpu_dequantize: bad argument");
+    const int bv = fomoe_block_values(type);
+    if (bv == 0 || n % bv) return fail(ctx, -1, "gpu_dequantize: type %d / n %lld", type, (long long)n);
+    HIPC(launch_dequant(type, (const uint8_t *)src, dst, n, ctx->stream));
+    return 0;
+}
+
+// Prepare the activation(s) of a matvec into ctx->xq_act.
+static int prep_x(gpu_ctx_t *ctx, int type, const float *x, uint64_t x_stride, int K, int n_vec,
+                  uint64_t &stride_out) {
+    const int gsz = gsz_of(type);
+    stride_out = xq_stride(K, gsz);
+    HIPC(ensure(ctx->xq_act, ctx->xq_act_cap, stride_out * (size_t)n_vec));
+    HIPC(launch_xprep(gsz, x, x_stride, K, n_vec, ctx->xq_act, stride_out, ctx->stream));
+    return 0;
+}
+
+int gpu_matvec_q_batched(gpu_ctx_t *ctx, int type, const void *W, uint64_t mat_stride, int n_mats,
+                         const float *x, uint64_t x_stride, float *y, uint64_t y_stride, int M, int K) {
+    if (!ctx || !W || !x || !y || M <= 0 || K <= 0 || n_mats <= 0)
+        return fail(ctx, -1, "gpu_matvec_q: bad argument");
+    if (!matvec_type(type)) return fail(ctx, -1, "gpu_matvec_q: unsupported type %d", type);
+    if (K % fomoe_block_values(type) || (kquant(type) && K % 256) || K > 16384)
+        return fail(ctx, -1, "gpu_matvec_q: K=%d not supported for type %d", K, type);
+    uint64_t xs = 0;
+    int rc = prep_x(ctx, type, x, x_stride, K, x_stride ? n_mats : 1, xs);
+    if (rc) return rc;
+    MatvecArgs a{(const uint8_t *)W, mat_stride, fomoe_row_bytes(type, K), ctx->xq_act,
+                 x_stride ? xs : 0, y, y_stride, n_mats, M, K};
+    HIPC(launch_matvec(type, a, ctx->stream, ctx->n_cu));
+    return 0;
+}
+
+int gpu_matvec_q(gpu_ctx_t *ctx, int type, const void *W, const float *x, float *y, int M, int K) {
+    return gpu_matvec_q_batched(ctx, type, W, 0, 1, x, 0, y, 0, M, K);
+}
+
+// ------------------------------------------------------------------ MoE
+static int check_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L) {
+    if (!L || !L->router || !L->experts) return fail(ctx, -1, "moe layer: null pointer");
+    if (L->n_embd <= 0 || L->n_embd % 256 || L->n_embd > 8192)
+        return fail(ctx, -1, "moe layer: n_embd %d (multiple of 256, <= 8192)", L->n_embd);
+    if (L->inter <= 0 || L->inter % 256 || L->inter > 8192)
+        return fail(ctx, -1, "moe layer: inter %d (multiple of 256, <= 8192)", L->inter);
+    if (L->n_experts <= 0 || L->n_experts > 1024 || L->k <= 0 || L->k > 16 || L->k > L->n_experts)
+        return fail(ctx, -1, "moe layer: n_experts %d / k %d", L->n_experts, L->k);
+    if (!matvec_type(L->gate_type) || L->up_type != L->gate_type || !matvec_type(L->down_type))
+        return fail(ctx, -1, "moe layer: types gate %d up %d down %d", L->gate_type, L->up_type,
+                    L->down_type);
+    const uint64_t gs = fomoe_row_bytes(L->gate_type, L->n_embd) * (uint64_t)L->inter;
+    const uint64_t ds = fomoe_row_bytes(L->down_type, L->inter) * (uint64_t)L->n_embd;
+    if (L->gate_size < gs || L->up_size < gs || L->expert_stride < L->gate_size + L->up_size + ds)
+        return fail(ctx, -1, "moe layer: blob sizes too small for the shapes");
+    if (L->shared && (L->shared_inter != L->inter || L->shared_gate_size < gs || L->shared_up_size < gs))
+        return fail(ctx, -1, "moe layer: shared expert must match the routed shape");
+    return 0;
+}
+
+// Size every scratch buffer a layer needs (outside any graph capture).
+static int size_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L) {
+    const int n_tot = L->k + (L->shared ? 1 : 0);
+    HIPC(ensure(ctx->xq_h, ctx->xq_h_cap, xq_stride(L->n_embd, gsz_of(L->gate_type))));
+    HIPC(ensure(ctx->act, ctx->act_cap, sizeof(float) * (size_t)n_tot * L->inter));
+    HIPC(ensure(ctx->xq_act, ctx->xq_act_cap, xq_stride(L->inter, gsz_of(L->down_type)) * (size_t)n_tot));
+    return 0;
+}
+
+static int enqueue_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float *in, float *out,
+                         int flags) {
+    const int H = L->n_embd, F = L->inter, n_tot = L->k + (L->shared ? 1 : 0);
+    const float *norm_w = (flags & GPU_MOE_NORM) ? L->norm_w : nullptr;
+    if ((flags & GPU_MOE_NORM) && !norm_w) return fail(ctx, -1, "moe layer: GPU_MOE_NORM without norm_w");
+    RouterArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, L->k,
+                  ctx->logits, ctx->counter, ctx->ids, ctx->weights, L->shared_gate_vec};
+    HIPC(launch_router(ra, ctx->xq_h, gsz_of(L->gate_type), ctx->stream));
+    const uint8_t *base = (const uint8_t *)L->experts, *sh = (const uint8_t *)L->shared;
+    GateUpArgs ga{ctx->ids, L->k, base, L->expert_stride, 0, L->gate_size, sh, 0,
+                  L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H), in, norm_w,
+                  L->eps, ctx->act};
+    HIPC(launch_gateup(L->gate_type, ga, ctx->xq_h, ctx->stream, ctx->n_cu));
+    const int gsz = gsz_of(L->down_type);
+    const uint64_t xs = xq_stride(F, gsz);
+    HIPC(launch_xprep(gsz, ctx->act, (uint64_t)F, F, n_tot, ctx->xq_act, xs, ctx->stream));
+    DownArgs da{ctx->ids, ctx->weights, L->k, base, L->expert_stride, L->gate_size + L->up_size,
+                sh, L->shared_gate_size + L->shared_up_size, ctx->act, H, F,
+                fomoe_row_bytes(L->down_type, F), (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out};
+    HIPC(launch_down(L->down_type, da, ctx->xq_act, xs, ctx->stream, ctx->n_cu));
+    return 0;
+}
+
+int gpu_moe_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float *in, float *out, int flags) {
+    if (!ctx || !in || !out) return fail(ctx, -1, "gpu_moe_layer: null pointer");
+    int rc = check_layer(ctx, L);
+    if (!rc) rc = size_layer(ctx, L);
+    if (!rc) rc = enqueue_layer(ctx, L, in, out, flags);
+    if (!rc) ctx->last_k = L->k;
+    return rc;
+}
+
+int gpu_moe_last_routing(gpu_ctx_t *ctx, int32_t *ids, float *w, float *shared_w) {
+    if (!ctx || ctx->last_k <= 0) return fail(ctx, -1, "no routing recorded");
+    float tmp[64];
+    HIPC(hipStreamSynchronize(ctx->stream));
+    if (ids) HIPC(hipMemcpy(ids, ctx->ids, sizeof(int32_t) * ctx->last_k, hipMemcpyDeviceToHost));
+    HIPC(hipMemcpy(tmp, ctx->weights, sizeof(float) * (ctx->last_k + 1), hipMemcpyDeviceToHost));
+    if (w) memcpy(w, tmp, sizeof(float) * ctx->last_k);
+    if (shared_w) *shared_w = tmp[ctx->last_k];
+    return 0;
+}
+
+int gpu_router_topk(gpu_ctx_t *ctx, const float *router, const float *bias, const float *x,
+                    const float *norm_w, float eps, int E, int H, int k, int32_t *ids, float *w) {
+    if (!ctx || !router || !x || !ids || !w) return fail(ctx, -1, "gpu_router_topk: null pointer");
+    if (E <= 0 || E > 1024 || k <= 0 || k > 16 || k > E || H <= 0 || H % 256 || H > 8192)
+        return fail(ctx, -1, "gpu_router_topk: E %d k %d H %d", E, k, H);
+    RouterArgs ra{router, bias, x, norm_w, eps, E, H, k, ctx->logits, ctx->counter, ids, w, nullptr};
+    HIPC(launch_router(ra, nullptr, 32, ctx->stream));
+    return 0;
+}
+
+int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_layers, float *x,
+                         int n_steps) {
+    if (!ctx || !layers || !x || n_layers <= 0 || n_steps < 0)
+        return fail(ctx, -1, "gpu_moe_stack_decode: bad argument");
+    for (int l = 0; l < n_layers; l++) {
+        int rc = check_layer(ctx, &layers[l]);
+        if (!rc) rc = size_layer(ctx, &layers[l]);
+        if (rc) return rc;
+        if (!layers[l].norm_w) return fail(ctx, -1, "gpu_moe_stack_decode: layer %d has no norm_w", l);
+    }
+    if (n_steps == 0) return 0;
+    if (ctx->graph_exec) {
+        (void)hipGraphExecDestroy(ctx->graph_exec);
+        ctx->graph_exec = nullptr;
+    }
+    HIPC(hipStreamSynchronize(ctx->stream));
+    HIPC(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    int rc = 0;
+    for (int l = 0; l < n_layers && !rc; l++)
+        rc = enqueue_layer(ctx, &layers[l], x, x, GPU_MOE_NORM | GPU_MOE_RESIDUAL);
+    hipGraph_t g = nullptr;
+    hipError_t ce = hipStreamEndCapture(ctx->stream, &g);
+    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+    if (ce != hipSuccess) return fail(ctx, -2, "graph capture failed: %s", hipGetErrorString(ce));
+    hipError_t ie = hipGraphInstantiate(&ctx->graph_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess) return fail(ctx, -2, "graph instantiate failed: %s", hipGetErrorString(ie));
+    for (int s = 0; s < n_steps; s++) HIPC(hipGraphLaunch(ctx->graph_exec, ctx->stream));
+    ctx->last_k = layers[n_layers - 1].k;
+    return 0;
+}
+
+// ------------------------------------------------------------------ legacy FFN
+// Reference gpu_kernels.hip:8385-8488: same argument checks and -1 fallbacks
+// (limits MAX_EXPERTS 10, MAX_N_EMBD 4096, MAX_INTERMEDIATE 2048,
+// MAX_EXPERT_STRIDE 12 MiB at gpu_kernels.hip:438-441).
+int gpu_expert_ffn(gpu_ctx_t *ctx, const float *h, void **expert_buffers, const float *scores,
+                   int n_experts, int n_embd, int inter, uint64_t gate_size, uint64_t up_size,
+                   uint64_t stride, int gate_type, int up_type, int down_type, float *ffn_out) {
+    if (!ctx) return -1;
+    if (n_experts > 10 || n_embd > 4096 || inter > 2048 || stride > 12ull * 1024 * 1024) return -1;
+    if (!kquant(gate_type) || !kquant(up_type) || !kquant(down_type)) return -1;
+    if (!h || !ffn_out || n_embd <= 0 || inter <= 0 || n_embd % 256 || inter % 256) return -1;
+    if (n_experts <= 0) {
+        memset(ffn_out, 0, sizeof(float) * (size_t)n_embd);
+        return 0;
+    }
+    if (!expert_buffers || !scores) return -1;
+    hipStream_t s = ctx->stream;
+    const int H = n_embd, F = inter, n = n_experts;
+    if (ensure(ctx->staging, ctx->staging_cap, (size_t)n * stride) != hipSuccess ||
+        ensure(ctx->vec_in, ctx->vec_in_cap, sizeof(float) * (size_t)H) != hipSuccess ||
+        ensure(ctx->vec_out, ctx->vec_out_cap, sizeof(float) * (size_t)H) != hipSuccess ||
+        ensure(ctx->act, ctx->act_cap, sizeof(float) * (size_t)n * F) != hipSuccess ||
+        ensure(ctx->act2, ctx->act2_cap, sizeof(float) * (size_t)n * F) != hipSuccess ||
+        ensure(ctx->xq_h, ctx->xq_h_cap, xq_stride(H, 16) + xq_stride(H, 32)) != hipSuccess ||
+        ensure(ctx->xq_act, ctx->xq_act_cap, xq_stride(F, 16) * (size_t)n) != hipSuccess)
+        return fail(ctx, -1, "gpu_expert_ffn: scratch allocation failed");
+    if (hipMemcpyAsync(ctx->vec_in, h, sizeof(float) * H, hipMemcpyHostToDevice, s) != hipSuccess)
+        return -1;
+    for (int e = 0; e < n; e++)
+        if (!expert_buffers[e] ||
+            hipMemcpyAsync(ctx->staging + (size_t)e * stride, expert_buffers[e], stride,
+                           hipMemcpyHostToDevice, s) != hipSuccess)
+            return -1;
+    if (hipMemcpyAsync(ctx->weights, scores, sizeof(float) * n, hipMemcpyHostToDevice, s) != hipSuccess)
+        return -1;
+    const uint64_t rb_g = fomoe_row_bytes(gate_type, H), rb_u = fomoe_row_bytes(up_type, H);
+    if (gate_type == up_type) {
+        const int gsz = gsz_of(gate_type);
+        if (launch_xprep(gsz, ctx->vec_in, 0, H, 1, ctx->xq_h, xq_stride(H, gsz), s) != hipSuccess) return -1;
+        GateUpArgs ga{nullptr, n, ctx->staging, stride, 0, gate_size, nullptr, 0, 0, F, H, rb_g,
+                      ctx->vec_in, nullptr, 0.f, ctx->act};
+        if (launch_gateup(gate_type, ga, ctx->xq_h, s, ctx->n_cu) != hipSuccess) return -1;
+    } else {
+        // gate and up in different formats: two batched matvecs + SiLU*up
+        uint8_t *xg = ctx->xq_h, *xu = ctx->xq_h + xq_stride(H, 16);
+        if (launch_xprep(gsz_of(gate_type), ctx->vec_in, 0, H, 1, xg, 0, s) != hipSuccess ||
+            launch_xprep(gsz_of(up_type), ctx->vec_in, 0, H, 1, xu, 0, s) != hipSuccess)
+            return -1;
+        MatvecArgs mg{ctx->staging, stride, rb_g, xg, 0, ctx->act, (uint64_t)F, n, F, H};
+        MatvecArgs mu{ctx->staging + gate_size, stride, rb_u, xu, 0, ctx->act2, (uint64_t)F, n, F, H};
+        if (launch_matvec(gate_type, mg, s, ctx->n_cu) != hipSuccess ||
+            launch_matvec(up_type, mu, s, ctx->n_cu) != hipSuccess ||
+            launch_silu_mul(ctx->act, ctx->act2, (int64_t)n * F, s) != hipSuccess)
+            return -1;
+    }
+    const int gsz = gsz_of(down_type);
+    const uint64_t xs = xq_stride(F, gsz);
+    if (launch_xprep(gsz, ctx->act, (uint64_t)F, F, n, ctx->xq_act, xs, s) != hipSuccess) return -1;
+    DownArgs da{nullptr, ctx->weights, n, ctx->staging, stride, gate_size + up_size, nullptr, 0,
+                ctx->act, H, F, fomoe_row_bytes(down_type, F), nullptr, ctx->vec_out};
+    if (launch_down(down_type, da, ctx->xq_act, xs, s, ctx->n_cu) != hipSuccess) return -1;
+    if (hipMemcpyAsync(ffn_out, ctx->vec_out, sizeof(float) * H, hipMemcpyDeviceToHost, s) != hipSuccess)
+        return -1;
+    if (hipStreamSynchronize(s) != hipSuccess) return -1;
+    return 0;
+}
+
+// ------------------------------------------------------------------ synthetic
+int gpu_synth_f32(gpu_ctx_t *ctx, uint64_t seed, uint64_t stream, float std, float *out, int64_t n) {
+    if (!ctx || !out || n <= 0) return fail(ctx, -1, "gpu_synth_f32: bad argument");
+    HIPC(launch_synth_f32(seed, stream, std, out, n, ctx->stream));
+    return 0;
+}
+
+int gpu_synth_quant(gpu_ctx_t *ctx, int type, uint64_t seed, uint64_t stream0, uint64_t step, float std,
+                    int64_t M, int64_t K, int n_mats, void *dst, uint64_t dst_stride) {
+    if (!ctx || !dst || M <= 0 || K <= 0 || K % 256 || n_mats <= 0)
+        return fail(ctx, -1, "gpu_synth_quant: bad argument");
+    if (!matvec_type(type)) return fail(ctx, -1, "gpu_synth_quant: type %d", type);
+    HIPC(launch_synth_quant(type, seed, stream0, step, std, M, K, n_mats, (uint8_t *)dst, dst_stride,
+                            ctx->stream));
+    return 0;
+}
+
+void gpu_synth_zipf_bias(uint64_t seed, uint64_t stream, int n, double s, float *bias) {
+    if (n <= 0 || !bias) return;
+    auto mix = [](uint64_t z) {
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    };
+    const uint64_t G = 0x9E3779B97F4A7C15ull;
+    const uint64_t key = mix(seed * G + mix(stream + 0x632BE59BD9B4E019ull));
+    std::vector<int> perm((size_t)n);
+    for (int i = 0; i < n; i++) perm[(size_t)i] = i;
+    for (int i = n - 1; i > 0; i--) {
+        const int j = (int)(mix(key + ((uint64_t)i + 1) * G) % (uint64_t)(i + 1));
+        std::swap(perm[(size_t)i], perm[(size_t)j]);
+    }
+    for (int r = 0; r < n; r++) bias[perm[(size_t)r]] = (float)(-s * log((double)(r + 1)));
+}
+
+}  // extern "C"

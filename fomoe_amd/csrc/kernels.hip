@@ -1,0 +1,612 @@
+// kernels.hip — gfx950 decode-path kernels: activation prep, batched quantized
+// matvec, router + softmax + top-k, fused gate/up/SiLU, down + weighted
+// combine, and the bit-exact dequantizer.
+//
+// Reference counterparts (replaced, not ported): gpu_kernels.hip
+// kernel_q4k_matvec_coop 1858, kernel_q6k_matvec_coop 1747,
+// kernel_q8_0_matvec_coop 1901, kernel_f32_matvec_coop 2127, kernel_softmax
+// 2668, kernel_top_k_parallel 2745, kernel_q4k_fused_gate_up_silu 1320,
+// kernel_q6k_matvec_per_expert 1261, kernel_weighted_sum 1631,
+// kernel_moe_output_residual 1647, kernel_silu_mul 1306.
+#include <float.h>
+
+#include "formats.h"
+#include "kernels.h"
+
+namespace fo {
+
+// ============================================================ activation prep
+// One thread per group of GSZ values: exponent from the group maximum, the
+// four balanced int8 limbs of X = round(x * 2^e), the scale 2^-e and the fp32
+// sum (layout in formats.h).
+template <int GSZ>
+__global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ x, uint64_t x_stride,
+                                               int K, int n_vec, uint8_t *__restrict__ xq,
+                                               uint64_t xq_stride) {
+    const int ng = K / GSZ;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (int64_t)ng * n_vec) return;
+    const int v = (int)(gid / ng), g = (int)(gid % ng);
+    const float *xp = x + (uint64_t)v * x_stride + (uint64_t)g * GSZ;
+    float vals[GSZ];
+    float M = 0.f, sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < GSZ; i += 4) {
+        float4 t = *(const float4 *)(xp + i);
+        vals[i] = t.x; vals[i + 1] = t.y; vals[i + 2] = t.z; vals[i + 3] = t.w;
+    }
+#pragma unroll
+    for (int i = 0; i < GSZ; i++) { M = fmaxf(M, fabsf(vals[i])); sum += vals[i]; }
+    int E = 0;
+    frexpf(M, &E);               // M < 2^E
+    int e = 30 - E;
+    if (e > 149) e = 149;        // keep 2^-e representable
+    const float scale = (M > 0.f) ? ldexpf(1.0f, -e) : 0.f;
+    uint32_t limb[kLimbs][GSZ / 4];
+#pragma unroll
+    for (int L = 0; L < kLimbs; L++)
+#pragma unroll
+        for (int k = 0; k < GSZ / 4; k++) limb[L][k] = 0;
+#pragma unroll
+    for (int i = 0; i < GSZ; i++) {
+        int X = (M > 0.f) ? __float2int_rn(ldexpf(vals[i], e)) : 0;
+#pragma unroll
+        for (int L = 0; L < kLimbs - 1; L++) {
+            const int b = (int)(int8_t)(X & 0xFF);
+            X = (X - b) >> 8;
+            limb[L][i / 4] |= (uint32_t)(b & 0xFF) << (8 * (i % 4));
+        }
+        limb[kLimbs - 1][i / 4] |= (uint32_t)(X & 0xFF) << (8 * (i % 4));
+    }
+    uint8_t *out = xq + (uint64_t)v * xq_stride;
+    uint32_t *lp = (uint32_t *)(out + (uint64_t)g * (kLimbs * GSZ));
+#pragma unroll
+    for (int L = 0; L < kLimbs; L++)
+#pragma unroll
+        for (int k = 0; k < GSZ / 4; k += 4)
+            *(uint4 *)(lp + L * (GSZ / 4) + k) =
+                make_uint4(limb[L][k], limb[L][k + 1], limb[L][k + 2], limb[L][k + 3]);
+    *(float2 *)(out + (uint64_t)K * 4 + (uint64_t)g * 8) = make_float2(scale, sum);
+}
+
+hipError_t launch_xprep(int gsz, const float *x, uint64_t x_stride, int K, int n_vec,
+                        uint8_t *xq, uint64_t xq_stride_b, hipStream_t s) {
+    if (K % gsz || n_vec <= 0) return hipErrorInvalidValue;
+    const int64_t n = (int64_t)(K / gsz) * n_vec;
+    const int blocks = (int)((n + 255) / 256);
+    if (gsz == 16) k_xprep<16><<<blocks, 256, 0, s>>>(x, x_stride, K, n_vec, xq, xq_stride_b);
+    else if (gsz == 32) k_xprep<32><<<blocks, 256, 0, s>>>(x, x_stride, K, n_vec, xq, xq_stride_b);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// ============================================================ lane state
+// A lane's slots: G lanes share one row (G = 64 when a row has >= 64 slots,
+// else the next power of two >= S) and P = 64/G rows are processed side by
+// side per pass; lane l owns slots (l % G) + G*u, u < U.
+template <int U, int G>
+struct Slots {
+    int slot[U];
+    bool ok[U];
+    FO_DEV void init(int lane, int S) {
+#pragma unroll
+        for (int u = 0; u < U; u++) { slot[u] = (lane % G) + G * u; ok[u] = slot[u] < S; }
+    }
+};
+
+// The prepared activation of a lane's slots, held in registers.
+template <int T, int U>
+struct XRegs {
+    typename Fmt<T>::X x[U];
+    template <int G>
+    FO_DEV void load(const Slots<U, G> &sl, const uint8_t *xq, int K) {
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (sl.ok[u]) {
+                int gi[Fmt<T>::NG];
+                Fmt<T>::groups(sl.slot[u], gi);
+                load_xslot(x[u], xq, K, gi);
+            }
+    }
+};
+
+template <int T, int U>
+struct RowRaw { typename Fmt<T>::Raw r[U]; };
+
+template <int T, int U, int G>
+FO_DEV void load_row(RowRaw<T, U> &rr, const uint8_t *row, const Slots<U, G> &sl) {
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (sl.ok[u]) rr.r[u] = Fmt<T>::load(row, sl.slot[u]);
+}
+
+template <int T, int U, int G>
+FO_DEV float dot_row(const RowRaw<T, U> &rr, const Slots<U, G> &sl, const XRegs<T, U> &X) {
+    float a = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (sl.ok[u]) a += Fmt<T>::dot(rr.r[u], sl.slot[u], X.x[u]);
+    return a;
+}
+
+// Contiguous share [t0, t1) of `total` tasks for wave w of nw.
+FO_DEV void wave_share(int64_t total, int w, int nw, int64_t &t0, int64_t &t1) {
+    t0 = total * w / nw;
+    t1 = total * (w + 1) / nw;
+}
+
+// ============================================================ batched matvec
+// y_m[r] = W_m[r,:] . x_m. Tasks are (matrix, block of P*R rows); each wave
+// takes a contiguous run of tasks and issues all loads of a task before any
+// arithmetic.
+template <int T, int U, int G, int R>
+__global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
+    constexpr int P = kWave / G, ROWS = P * R;
+    const int lane = threadIdx.x & 63, sub = lane / G;
+    const int w = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nw = (int)((gridDim.x * blockDim.x) >> 6);
+    const int S = a.K / Fmt<T>::SLOT;
+    const int64_t tpm = (a.M + ROWS - 1) / ROWS;
+    int64_t t0, t1;
+    wave_share(tpm * a.n_mats, w, nw, t0, t1);
+    Slots<U, G> L;
+    L.init(lane, S);
+    XRegs<T, U> X;
+    int64_t cur = -1;
+    for (int64_t t = t0; t < t1; t++) {
+        const int64_t m = t / tpm;
+        const int rb = (int)(t - m * tpm);
+        if (m != cur && (cur < 0 || a.x_stride)) X.load(L, a.xq + m * a.x_stride, a.K);
+        cur = m;
+        const uint8_t *W = a.W + m * a.mat_stride;
+        RowRaw<T, U> raw[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = min(rb * ROWS + r * P + sub, a.M - 1);
+            load_row(raw[r], W + (uint64_t)row * a.row_bytes, L);
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float v = group_sum<G>(dot_row(raw[r], L, X));
+            const int row = rb * ROWS + r * P + sub;
+            if ((lane % G) == 0 && row < a.M) a.y[m * a.y_stride + row] = v;
+        }
+    }
+}
+
+// Slot geometry of a K-wide row: lanes per row G and slots per lane U.
+static bool geometry(int type, int K, int &G, int &U) {
+    const int slot = (type == GGML_TYPE_Q8_0) ? 32 : 64;
+    if (K <= 0 || K % slot) return false;
+    if ((type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K || type == GGML_TYPE_Q6_K) && K % 256)
+        return false;
+    const int S = K / slot;
+    if (S >= 64) { G = 64; U = (S + 63) / 64; return U <= kMaxSlotsPerLane; }
+    G = 1;
+    while (G < S) G <<= 1;
+    U = 1;
+    return G >= 4;
+}
+
+static int waves_for(int64_t tasks, int n_cu, int per_cu) {
+    const int64_t cap = (int64_t)n_cu * per_cu;
+    return (int)(tasks < cap ? (tasks > 0 ? tasks : 1) : cap);
+}
+
+template <int T, int R>
+static hipError_t matvec_t(const MatvecArgs &a, hipStream_t s, int n_cu) {
+    int G, U;
+    if (!geometry(T, a.K, G, U)) return hipErrorInvalidValue;
+    const int P = 64 / G;
+    const int64_t tasks = (int64_t)((a.M + P * R - 1) / (P * R)) * a.n_mats;
+    const int blocks = (waves_for(tasks, n_cu, 16) + 3) / 4;
+#define FO_MV(GG, UU) \
+    if (G == GG && U == UU) { k_matvec<T, UU, GG, R><<<blocks, 256, 0, s>>>(a); return hipGetLastError(); }
+    FO_MV(64, 1) FO_MV(64, 2) FO_MV(64, 3) FO_MV(64, 4)
+    FO_MV(32, 1) FO_MV(16, 1) FO_MV(8, 1) FO_MV(4, 1)
+#undef FO_MV
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu) {
+    if (a.M <= 0 || a.n_mats <= 0) return hipErrorInvalidValue;
+    switch (type) {
+        case GGML_TYPE_Q4_K: return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
+        case GGML_TYPE_Q5_K: return matvec_t<GGML_TYPE_Q5_K, 2>(a, s, n_cu);
+        case GGML_TYPE_Q6_K: return matvec_t<GGML_TYPE_Q6_K, 2>(a, s, n_cu);
+        case GGML_TYPE_Q8_0: return matvec_t<GGML_TYPE_Q8_0, 2>(a, s, n_cu);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// ============================================================ router
+// Work-group of 4 waves, one router row per wave. The input is staged in LDS
+// (RMS-normalised when norm_w is set: h = x * (1/sqrt(mean(x^2)+eps)) * w, in
+// the operation order of reference src/tensor.c:175-184), each work-group
+// also writes its share of the prepared activation of h for the expert
+// kernels, and the last work-group to finish runs softmax, top-k and
+// renormalisation (reference src/inference.c:486-502, src/tensor.c:186-252).
+constexpr int kRouterMaxE = 1024;
+
+template <int UH>  // H = 256*UH; a lane holds 4*UH values of h
+__global__ __launch_bounds__(256) void k_router(RouterArgs a, uint8_t *__restrict__ xq_h, int gsz) {
+    extern __shared__ float sh[];  // H floats
+    __shared__ float red[4];
+    __shared__ int last;
+    const int H = a.H, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int i = tid * 4; i < H; i += 1024) *(float4 *)(sh + i) = *(const float4 *)(a.x + i);
+    __syncthreads();
+    if (a.norm_w) {
+        float ss = 0.f;
+        for (int i = tid; i < H; i += 256) ss += sh[i] * sh[i];
+        ss = wave_sum(ss);
+        if (lane == 0) red[wv] = ss;
+        __syncthreads();
+        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const float scale = 1.0f / sqrtf(tot / (float)H + a.eps);
+        __syncthreads();
+        for (int i = tid; i < H; i += 256) sh[i] = sh[i] * scale * a.norm_w[i];
+        __syncthreads();
+    }
+    // this work-group's share of the prepared activation of h
+    if (xq_h) {
+        const int ng = H / gsz, per = (ng + gridDim.x - 1) / gridDim.x;
+        for (int j = tid; j < per; j += 256) {
+            const int g = blockIdx.x * per + j;
+            if (g >= ng) break;
+            const float *xp = sh + g * gsz;
+            float M = 0.f, sum = 0.f;
+            for (int i = 0; i < gsz; i++) { M = fmaxf(M, fabsf(xp[i])); sum += xp[i]; }
+            int E = 0;
+            frexpf(M, &E);
+            int e = 30 - E;
+            if (e > 149) e = 149;
+            uint32_t *lp = (uint32_t *)(xq_h + (uint64_t)g * (kLimbs * gsz));
+            for (int k = 0; k < gsz / 4; k++) {
+                uint32_t lb[kLimbs] = {0, 0, 0, 0};
+                for (int b = 0; b < 4; b++) {
+                    int X = (M > 0.f) ? __float2int_rn(ldexpf(xp[4 * k + b], e)) : 0;
+                    for (int L = 0; L < kLimbs - 1; L++) {
+                        const int v = (int)(int8_t)(X & 0xFF);
+                        X = (X - v) >> 8;
+                        lb[L] |= (uint32_t)(v & 0xFF) << (8 * b);
+                    }
+                    lb[kLimbs - 1] |= (uint32_t)(X & 0xFF) << (8 * b);
+                }
+                for (int L = 0; L < kLimbs; L++) lp[L * (gsz / 4) + k] = lb[L];
+            }
+            *(float2 *)(xq_h + (uint64_t)H * 4 + (uint64_t)g * 8) =
+                make_float2((M > 0.f) ? ldexpf(1.0f, -e) : 0.f, sum);
+        }
+    }
+    // one row per wave
+    const int e = blockIdx.x * 4 + wv;
+    if (e < a.E) {
+        const float *row = a.W + (uint64_t)e * H;
+        float4 wv4[UH];
+#pragma unroll
+        for (int u = 0; u < UH; u++) wv4[u] = *((const float4 *)row + lane + 64 * u);
+        float acc = 0.f;
+#pragma unroll
+        for (int u = 0; u < UH; u++) {
+            const float4 hv = *(const float4 *)(sh + 4 * (lane + 64 * u));
+            acc = fmaf(wv4[u].x, hv.x, acc);
+            acc = fmaf(wv4[u].y, hv.y, acc);
+            acc = fmaf(wv4[u].z, hv.z, acc);
+            acc = fmaf(wv4[u].w, hv.w, acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) a.logits[e] = acc + (a.bias ? a.bias[e] : 0.f);
+    }
+    // last work-group: softmax, top-k, renormalise
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();
+        const unsigned prev = atomicAdd(a.counter, 1u);
+        last = (prev == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!last || wv != 0) return;
+    __threadfence();
+    constexpr int NV = kRouterMaxE / 64;
+    float v[NV];
+    float mx = -FLT_MAX;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = lane + 64 * j;
+        v[j] = (i < a.E) ? __hip_atomic_load(a.logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                         : -FLT_MAX;
+        mx = fmaxf(mx, v[j]);
+    }
+    mx = wave_max(mx);
+    float ls = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = lane + 64 * j;
+        v[j] = (i < a.E) ? expf(v[j] - mx) : 0.f;
+        ls += v[j];
+    }
+    const float inv = 1.0f / wave_sum(ls);
+#pragma unroll
+    for (int j = 0; j < NV; j++) v[j] = (lane + 64 * j < a.E) ? v[j] * inv : -FLT_MAX;
+    // top-k: k rounds of wave argmax, ties to the lowest index
+    float selv[16];
+    int seli[16];
+    for (int kk = 0; kk < a.k; kk++) {
+        float best = -FLT_MAX;
+        int bi = 0x7FFFFFFF;
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+            if (v[j] > best) { best = v[j]; bi = lane + 64 * j; }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(best, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+        }
+        if (bi < 0 || bi >= a.E) { bi = 0; best = 0.f; }  // non-finite logits: never index out of range
+        selv[kk] = best;
+        seli[kk] = bi;
+        if (lane == (bi & 63)) {
+#pragma unroll
+            for (int j = 0; j < NV; j++)
+                if (j == (bi >> 6)) v[j] = -FLT_MAX;
+        }
+    }
+    // shared-expert gate sigmoid(h . g)
+    float gate = 1.0f;
+    if (a.shared_gate_vec) {
+        float d = 0.f;
+        for (int i = lane; i < H; i += 64) d += sh[i] * a.shared_gate_vec[i];
+        d = wave_sum(d);
+        gate = 1.0f / (1.0f + expf(-d));
+    }
+    if (lane == 0) {
+        float ssum = 0.f;
+        for (int kk = 0; kk < a.k; kk++) ssum += selv[kk];
+        const float rinv = ssum > 0.f ? 1.0f / ssum : 1.0f;
+        for (int kk = 0; kk < a.k; kk++) {
+            a.ids[kk] = seli[kk];
+            a.weights[kk] = ssum > 0.f ? selv[kk] * rinv : selv[kk];
+        }
+        a.weights[a.k] = gate;
+        __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+hipError_t launch_router(const RouterArgs &a, uint8_t *xq_h, int gsz, hipStream_t s) {
+    if (a.E <= 0 || a.E > kRouterMaxE || a.k <= 0 || a.k > 16 || a.k > a.E || a.H % 256)
+        return hipErrorInvalidValue;
+    const int blocks = (a.E + 3) / 4;
+    const size_t lds = (size_t)a.H * 4;
+#define FO_RT(UU) \
+    if (a.H == 256 * UU) { k_router<UU><<<blocks, 256, lds, s>>>(a, xq_h, gsz); return hipGetLastError(); }
+    FO_RT(4) FO_RT(8) FO_RT(12) FO_RT(16) FO_RT(24) FO_RT(32)
+#undef FO_RT
+    return hipErrorInvalidValue;
+}
+
+// ============================================================ gate/up/SiLU
+// Tasks are (expert slot, block of P*R rows); gate and up rows of a task are
+// loaded together and act = silu(gate.h) * (up.h) (reference
+// src/inference.c:555-566 order: silu of gate, then multiply by up).
+template <int T, int U, int G, int R>
+__global__ __launch_bounds__(256) void k_gateup(GateUpArgs a, const uint8_t *__restrict__ xq_h) {
+    constexpr int P = kWave / G, ROWS = P * R;
+    const int lane = threadIdx.x & 63, sub = lane / G;
+    const int w = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nw = (int)((gridDim.x * blockDim.x) >> 6);
+    const int S = a.H / Fmt<T>::SLOT;
+    const int n_tot = a.n_sel + (a.shared ? 1 : 0);
+    const int tpe = (a.F + ROWS - 1) / ROWS;
+    int64_t t0, t1;
+    wave_share((int64_t)tpe * n_tot, w, nw, t0, t1);
+    if (t0 >= t1) return;
+    Slots<U, G> L;
+    L.init(lane, S);
+    XRegs<T, U> X;
+    X.load(L, xq_h, a.H);
+    for (int64_t t = t0; t < t1; t++) {
+        const int e = (int)(t / tpe), rb = (int)(t - (int64_t)e * tpe);
+        const uint8_t *blob;
+        uint64_t go, uo;
+        if (e < a.n_sel) {
+            const int id = a.ids ? a.ids[e] : e;
+            blob = a.base + (uint64_t)id * a.stride;
+            go = a.gate_off; uo = a.up_off;
+        } else {
+            blob = a.shared; go = a.sh_gate_off; uo = a.sh_up_off;
+        }
+        RowRaw<T, U> rg[R], ru[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = min(rb * ROWS + r * P + sub, a.F - 1);
+            load_row(rg[r], blob + go + (uint64_t)row * a.row_bytes, L);
+            load_row(ru[r], blob + uo + (uint64_t)row * a.row_bytes, L);
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float g = group_sum<G>(dot_row(rg[r], L, X));
+            const float u = group_sum<G>(dot_row(ru[r], L, X));
+            const int row = rb * ROWS + r * P + sub;
+            if ((lane % G) == 0 && row < a.F) a.act[(uint64_t)e * a.F + row] = (g / (1.0f + expf(-g))) * u;
+        }
+    }
+}
+
+template <int T, int R>
+static hipError_t gateup_t(const GateUpArgs &a, const uint8_t *xq_h, hipStream_t s, int n_cu) {
+    int G, U;
+    if (!geometry(T, a.H, G, U)) return hipErrorInvalidValue;
+    const int P = 64 / G, n_tot = a.n_sel + (a.shared ? 1 : 0);
+    const int64_t tasks = (int64_t)((a.F + P * R - 1) / (P * R)) * n_tot;
+    const int blocks = (waves_for(tasks, n_cu, 16) + 3) / 4;
+#define FO_GU(GG, UU) \
+    if (G == GG && U == UU) { k_gateup<T, UU, GG, R><<<blocks, 256, 0, s>>>(a, xq_h); return hipGetLastError(); }
+    FO_GU(64, 1) FO_GU(64, 2) FO_GU(32, 1) FO_GU(16, 1) FO_GU(8, 1) FO_GU(4, 1)
+#undef FO_GU
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gateup(int type, const GateUpArgs &a, const uint8_t *xq_h, hipStream_t s, int n_cu) {
+    if (a.F <= 0 || a.n_sel < 0 || a.n_sel + (a.shared ? 1 : 0) <= 0) return hipErrorInvalidValue;
+    switch (type) {
+        case GGML_TYPE_Q4_K: return gateup_t<GGML_TYPE_Q4_K, 2>(a, xq_h, s, n_cu);
+        case GGML_TYPE_Q5_K: return gateup_t<GGML_TYPE_Q5_K, 2>(a, xq_h, s, n_cu);
+        case GGML_TYPE_Q6_K: return gateup_t<GGML_TYPE_Q6_K, 2>(a, xq_h, s, n_cu);
+        case GGML_TYPE_Q8_0: return gateup_t<GGML_TYPE_Q8_0, 2>(a, xq_h, s, n_cu);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// ============================================================ down + combine
+// Tasks are blocks of P rows of the output; for each expert e (routed in rank
+// order, then shared) the wave loads NE experts' rows at a time and
+// accumulates weights[e] * down_e[row,:].act_e in the lanes before a single
+// group reduction per row; out = resid + sum (reference src/inference.c:
+// 574 vec_scaled_add in rank order, 595 shared add, 606 residual).
+template <int T, int U, int G, int NE>
+__global__ __launch_bounds__(256) void k_down(DownArgs a, const uint8_t *__restrict__ xq_act,
+                                              uint64_t xq_vstride) {
+    constexpr int P = kWave / G;
+    const int lane = threadIdx.x & 63, sub = lane / G;
+    const int w = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nw = (int)((gridDim.x * blockDim.x) >> 6);
+    const int S = a.F / Fmt<T>::SLOT;
+    const int n_tot = a.n_sel + (a.shared ? 1 : 0);
+    const int tasks = (a.H + P - 1) / P;
+    int64_t t0, t1;
+    wave_share(tasks, w, nw, t0, t1);
+    Slots<U, G> L;
+    L.init(lane, S);
+    for (int64_t t = t0; t < t1; t++) {
+        const int row_u = (int)t * P + sub;
+        const int row = min(row_u, a.H - 1);
+        float acc = 0.f;
+        for (int e0 = 0; e0 < n_tot; e0 += NE) {
+            RowRaw<T, U> raw[NE];
+#pragma unroll
+            for (int i = 0; i < NE; i++) {
+                const int e = e0 + i;
+                if (e < n_tot) {
+                    const uint8_t *m = (e < a.n_sel)
+                        ? a.base + (uint64_t)(a.ids ? a.ids[e] : e) * a.stride + a.down_off
+                        : a.shared + a.sh_down_off;
+                    load_row(raw[i], m + (uint64_t)row * a.row_bytes, L);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NE; i++) {
+                const int e = e0 + i;
+                if (e < n_tot) {
+                    XRegs<T, U> X;
+                    X.load(L, xq_act + (uint64_t)e * xq_vstride, a.F);
+                    acc = fmaf(a.weights[e], dot_row(raw[i], L, X), acc);
+                }
+            }
+        }
+        const float v = group_sum<G>(acc);
+        if ((lane % G) == 0 && row_u < a.H) a.out[row_u] = (a.resid ? a.resid[row_u] : 0.f) + v;
+    }
+}
+
+template <int T>
+static hipError_t down_t(const DownArgs &a, const uint8_t *xq_act, uint64_t xq_vstride, hipStream_t s,
+                         int n_cu) {
+    int G, U;
+    if (!geometry(T, a.F, G, U)) return hipErrorInvalidValue;
+    const int P = 64 / G;
+    const int64_t tasks = (a.H + P - 1) / P;
+    const int blocks = (waves_for(tasks, n_cu, 16) + 3) / 4;
+#define FO_DN(GG, UU) \
+    if (G == GG && U == UU) { k_down<T, UU, GG, 4><<<blocks, 256, 0, s>>>(a, xq_act, xq_vstride); return hipGetLastError(); }
+    FO_DN(64, 1) FO_DN(64, 2) FO_DN(32, 1) FO_DN(16, 1) FO_DN(8, 1) FO_DN(4, 1)
+#undef FO_DN
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_down(int type, const DownArgs &a, const uint8_t *xq_act, uint64_t xq_vstride,
+                       hipStream_t s, int n_cu) {
+    if (a.H <= 0 || a.n_sel < 0) return hipErrorInvalidValue;
+    switch (type) {
+        case GGML_TYPE_Q4_K: return down_t<GGML_TYPE_Q4_K>(a, xq_act, xq_vstride, s, n_cu);
+        case GGML_TYPE_Q5_K: return down_t<GGML_TYPE_Q5_K>(a, xq_act, xq_vstride, s, n_cu);
+        case GGML_TYPE_Q6_K: return down_t<GGML_TYPE_Q6_K>(a, xq_act, xq_vstride, s, n_cu);
+        case GGML_TYPE_Q8_0: return down_t<GGML_TYPE_Q8_0>(a, xq_act, xq_vstride, s, n_cu);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// ============================================================ dequantize
+// One thread per value, with the exact operation order of the reference
+// dequantizers (reference src/quant.c:82-105, 147-175, 216-247, 266-274,
+// 298-315); results are bit-identical (the products are exact, see the
+// oracle's pins).
+__global__ __launch_bounds__(256) void k_dequant(int type, const uint8_t *__restrict__ src,
+                                                 float *__restrict__ dst, int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float y = 0.f;
+    if (type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K) {
+        const int bb = type == GGML_TYPE_Q4_K ? 144 : 176;
+        const uint8_t *b = src + (i >> 8) * bb;
+        const int e = (int)(i & 255), g = e >> 6, hi = (e >> 5) & 1, l = e & 31;
+        const int j = 2 * g + hi;
+        const uint8_t *sc = b + 4;
+        int s6, m6;
+        if (j < 4) { s6 = sc[j] & 63; m6 = sc[j + 4] & 63; }
+        else { s6 = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4); m6 = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4); }
+        const float d = h2f(ld2(b)), dmin = h2f(ld2(b + 2));
+        const uint8_t *qs = b + (type == GGML_TYPE_Q4_K ? 16 : 48);
+        int q = hi ? (qs[32 * g + l] >> 4) : (qs[32 * g + l] & 0xF);
+        if (type == GGML_TYPE_Q5_K) q += ((b[16 + l] >> (2 * g + hi)) & 1) ? 16 : 0;
+        const float d1 = d * (float)s6, m1 = dmin * (float)m6;
+        y = d1 * (float)q - m1;
+    } else if (type == GGML_TYPE_Q6_K) {
+        const uint8_t *b = src + (i >> 8) * 210;
+        const int e = (int)(i & 255), n = e >> 7, r = e & 127, t = r >> 5, l = r & 31;
+        const uint8_t qlb = b[64 * n + l + ((t & 1) ? 32 : 0)];
+        const int lo = (t & 2) ? (qlb >> 4) : (qlb & 0xF);
+        const int hbits = (b[128 + 32 * n + l] >> (2 * t)) & 3;
+        const int q = (lo | (hbits << 4)) - 32;
+        const float d = h2f(ld2(b + 208));
+        y = d * (float)(int8_t)b[192 + (e >> 4)] * (float)q;
+    } else if (type == GGML_TYPE_Q8_0) {
+        const uint8_t *b = src + (i >> 5) * 34;
+        y = h2f(ld2(b)) * (float)(int8_t)b[2 + (i & 31)];
+    } else if (type == GGML_TYPE_MXFP4) {
+        const uint8_t *b = src + (i >> 5) * 17;
+        const int e = (int)(i & 31);
+        const int c = (e < 16) ? (b[1 + e] & 0xF) : (b[1 + e - 16] >> 4);
+        const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+        const float v = (c & 8) ? -mag[c & 7] : mag[c & 7];
+        const float s = (b[0] == 0xFF) ? 0.0f : ldexpf(1.0f, (int)b[0] - 127);
+        y = v * s;
+    } else if (type == GGML_TYPE_F16) {
+        y = h2f(ld2(src + 2 * i));
+    } else if (type == GGML_TYPE_BF16) {
+        y = __uint_as_float(ld2(src + 2 * i) << 16);
+    } else {
+        y = ((const float *)src)[i];
+    }
+    dst[i] = y;
+}
+
+hipError_t launch_dequant(int type, const uint8_t *src, float *dst, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipErrorInvalidValue;
+    k_dequant<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(type, src, dst, n);
+    return hipGetLastError();
+}
+
+__global__ void k_silu_mul(float *g, const float *u, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { const float v = g[i]; g[i] = (v / (1.0f + expf(-v))) * u[i]; }
+}
+
+hipError_t launch_silu_mul(float *g, const float *u, int64_t n, hipStream_t s) {
+    k_silu_mul<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(g, u, n);
+    return hipGetLastError();
+}
+
+}  // namespace fo

@@ -1,0 +1,155 @@
+/*
+ * gpu.h — C-ABI of libfomoe_gfx950.so, the MI355X (gfx950) implementation of
+ * fomoe's quantized MoE expert hot path.
+ *
+ * Drop-in part: gpu_ctx_t, gpu_init, gpu_free and gpu_expert_ffn keep the
+ * reference's signatures, ownership and -1 "fall back to CPU" semantics
+ * (reference include/gpu.h:10-16, 68-83; implementation
+ * src/gpu_kernels.hip:8385-8488), so src/inference.c:544 links unchanged.
+ *
+ * HBM-resident extensions (no reference counterpart; the reference copies
+ * every expert host-to-device per call, which defeats residency): explicit
+ * device pointers, int return codes (0 ok, -1 invalid argument / unsupported
+ * shape, -2 device error; the message is in gpu_last_error), never exit().
+ * All device work is ordered on the context's single stream; calls marked
+ * "async" return before the device finishes (use gpu_sync). A context is not
+ * re-entrant: one host thread per context, as in the reference.
+ */
+#ifndef FOMOE_GPU_H
+#define FOMOE_GPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct gpu_ctx gpu_ctx_t;
+
+/* ---------------------------------------------------------------- lifecycle
+ * gpu_init: select device 0, create the stream and scratch. NULL when no
+ * device is present (reference include/gpu.h:13; gpu_kernels.hip:3774-3777).
+ * gpu_free: release everything the context allocated (reference gpu.h:16). */
+gpu_ctx_t *gpu_init(void);
+void gpu_free(gpu_ctx_t *ctx);
+
+/* ---------------------------------------------------------------- legacy FFN
+ * Routed-expert FFN for host buffers (reference include/gpu.h:68-83):
+ *   ffn_out = sum_e expert_scores[e] * down_e(silu(gate_e.h) * (up_e.h))
+ * expert_buffers[e] points at a host blob gate | up | down (gate at 0, up at
+ * expert_gate_size, down at expert_gate_size + expert_up_size). Excludes the
+ * shared expert and the residual. Synchronous. Returns 0, or -1 for a NULL
+ * ctx, n_experts > 10, n_embd > 4096, expert_intermediate > 2048,
+ * expert_stride > 12 MiB, a gate/up/down type outside {Q4_K, Q5_K, Q6_K},
+ * or a device error (same limits as reference gpu_kernels.hip:438-441,
+ * 8393-8403). */
+int gpu_expert_ffn(gpu_ctx_t *ctx,
+                   const float *h,
+                   void **expert_buffers,
+                   const float *expert_scores,
+                   int n_experts,
+                   int n_embd,
+                   int expert_intermediate,
+                   uint64_t expert_gate_size,
+                   uint64_t expert_up_size,
+                   uint64_t expert_stride,
+                   int gate_type,
+                   int up_type,
+                   int down_type,
+                   float *ffn_out);
+
+/* ---------------------------------------------------------------- device memory */
+void *gpu_alloc(gpu_ctx_t *ctx, uint64_t bytes);               /* NULL on failure */
+void  gpu_dealloc(gpu_ctx_t *ctx, void *d_ptr);
+int   gpu_upload(gpu_ctx_t *ctx, void *d_dst, const void *h_src, uint64_t bytes);   /* sync */
+int   gpu_download(gpu_ctx_t *ctx, void *h_dst, const void *d_src, uint64_t bytes); /* sync */
+int   gpu_sync(gpu_ctx_t *ctx);
+/* n_cu, total HBM bytes and the gfx arch name of the context's device. */
+int   gpu_device_info(gpu_ctx_t *ctx, int *n_cu, uint64_t *hbm_bytes, char *arch, int arch_len);
+const char *gpu_last_error(gpu_ctx_t *ctx);
+
+/* ---------------------------------------------------------------- kernels (async)
+ * gpu_dequantize: d_dst[n] = dequantized values of d_src, bit-identical to
+ * reference src/quant.c dequantize_row_* (Q4_K, Q5_K, Q6_K, Q8_0, MXFP4, F16,
+ * BF16, F32).
+ * gpu_matvec_q: d_y[M] = W[M x K] . d_x[K] for quantized W (Q4_K, Q5_K, Q6_K:
+ * K % 256 == 0; Q8_0: K % 32 == 0), fp32 activations, exact integer products
+ * and fp32 accumulation (replaces reference mat_vec_mul, src/tensor.c:102-173,
+ * on the device).
+ * gpu_matvec_q_batched: the same for n_mats matrices W_m = d_W + m*mat_stride
+ * bytes, x_m = d_x + m*x_stride floats (0: one shared x), y_m = d_y +
+ * m*y_stride floats, in one launch. */
+int gpu_dequantize(gpu_ctx_t *ctx, int type, const void *d_src, float *d_dst, int64_t n);
+int gpu_matvec_q(gpu_ctx_t *ctx, int type, const void *d_W, const float *d_x, float *d_y,
+                 int M, int K);
+int gpu_matvec_q_batched(gpu_ctx_t *ctx, int type, const void *d_W, uint64_t mat_stride,
+                         int n_mats, const float *d_x, uint64_t x_stride, float *d_y,
+                         uint64_t y_stride, int M, int K);
+
+/* ---------------------------------------------------------------- MoE layer */
+typedef struct {
+    int n_embd;                 /* H */
+    int inter;                  /* F, routed-expert intermediate */
+    int n_experts;              /* E (<= 1024) */
+    int k;                      /* experts used per token (<= 16) */
+    int gate_type, up_type, down_type;
+    uint64_t gate_size, up_size, expert_stride;
+    const float *router;        /* device [E x H] fp32 */
+    const float *router_bias;   /* device [E] added to the logits, or NULL */
+    const void *experts;        /* device, E blobs gate|up|down, expert_stride apart */
+    const void *shared;         /* device shared-expert blob, or NULL */
+    int shared_inter;           /* must equal inter */
+    uint64_t shared_gate_size, shared_up_size;
+    const float *shared_gate_vec; /* device [H]: shared output *= sigmoid(h.v); NULL: 1 */
+    const float *norm_w;        /* device [H] RMSNorm weight, used with GPU_MOE_NORM */
+    float eps;
+} gpu_moe_layer_t;
+
+#define GPU_MOE_NORM     1  /* h = rms_norm(in) * norm_w before routing */
+#define GPU_MOE_RESIDUAL 2  /* out = in + ffn (else out = ffn); out may alias in */
+
+/* One MoE layer for one token, everything device-resident (async):
+ * router matvec, softmax, top-k (ties to the lowest index), renormalise,
+ * routed SwiGLU experts, shared expert, weighted combine (reference
+ * src/inference.c:481-606; gpu_kernels.hip 5514-5528, 7405-7435, 7740). */
+int gpu_moe_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *layer, const float *d_in,
+                  float *d_out, int flags);
+/* Routing of the most recent gpu_moe_layer call (sync): k ids, k weights
+ * and the shared-expert weight. */
+int gpu_moe_last_routing(gpu_ctx_t *ctx, int32_t *ids, float *weights, float *shared_weight);
+/* Router alone (async): d_ids[k], d_weights[k+1] (last = shared weight 1). */
+int gpu_router_topk(gpu_ctx_t *ctx, const float *d_router, const float *d_bias,
+                    const float *d_x, const float *d_norm_w, float eps, int n_experts,
+                    int n_embd, int k, int32_t *d_ids, float *d_weights);
+
+/* n_steps decode steps through n_layers layers, x <- x + moe_l(rms_norm(x))
+ * per layer, in place on d_x[n_embd]. The per-step launch sequence is
+ * captured once into a HIP graph and replayed. Async. */
+int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_layers,
+                         float *d_x, int n_steps);
+
+/* ---------------------------------------------------------------- synthetic data
+ * This build's own generator (no reference counterpart): counter-based
+ * SplitMix64 normals and this build's quantizers; bit-identical to the CPU
+ * generator in oracle/. Matrix m of a batch uses stream stream0 + m*step and
+ * lands at d_dst + m*dst_stride. K % 256 == 0. Async. */
+int gpu_synth_f32(gpu_ctx_t *ctx, uint64_t seed, uint64_t stream, float std, float *d_out,
+                  int64_t n);
+int gpu_synth_quant(gpu_ctx_t *ctx, int type, uint64_t seed, uint64_t stream0,
+                    uint64_t stream_step, float std, int64_t M, int64_t K, int n_mats,
+                    void *d_dst, uint64_t dst_stride);
+/* Host-side Zipf(s) router bias: bias[e] = -s*ln(rank(e)), rank a seeded
+ * permutation. */
+void gpu_synth_zipf_bias(uint64_t seed, uint64_t stream, int n, double s, float *h_bias);
+
+/* ---------------------------------------------------------------- timing
+ * Events on the context's stream: gpu_timer_start records, gpu_timer_stop
+ * records, waits and returns the elapsed milliseconds (< 0 on error). */
+int   gpu_timer_start(gpu_ctx_t *ctx);
+float gpu_timer_stop(gpu_ctx_t *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FOMOE_GPU_H */

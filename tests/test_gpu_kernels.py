@@ -1,0 +1,368 @@
+"""GPU parity: the gfx950 kernels against the CPU oracle, through the C-ABI.
+
+Bars: dequantization and synthetic generation bit-exact; matvec / router
+weights / FFN / MoE layer within parity_err <= 1e-3 (max per-element relative
+error with a 1e-3*||ref||_inf floor, fp32 accumulate on both sides); routing
+ids equal.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import fomoe_amd as FA
+import oracle as O
+from conftest import inf_rel, parity_err
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+TOL = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+# ------------------------------------------------------------------ synthetic generator
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0])
+def test_synth_quant_bit_exact(gpu, t):
+    say("synth", t)
+    M, K, n = 48, 1024, 3
+    rb = O.row_bytes(t, K) * M
+    stride = (rb + 255) // 256 * 256
+    d = gpu.alloc(stride * n)
+    gpu.synth_quant(t, 4, 1 << 24, 16, 0.02, M, K, n, d, stride)
+    got = gpu.download(d, np.uint8, stride * n).reshape(n, stride)[:, :rb]
+    for m in range(n):
+        want = O.synth_quant(t, 4, (1 << 24) + 16 * m, 0.02, M, K)
+        assert np.array_equal(got[m], want), (t, m)
+
+
+def test_synth_f32_bit_exact(gpu):
+    n = 100001
+    d = gpu.alloc(4 * n)
+    gpu.synth_f32(7, 3, 0.02, d, n)
+    got = gpu.download(d, np.float32, n)
+    assert np.array_equal(got.view(np.uint32), O.synth_f32(7, 3, 0.02, n).view(np.uint32))
+
+
+# ------------------------------------------------------------------ dequantization
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, O.MXFP4])
+def test_dequant_golden_bit_exact(gpu, t):
+    say("dequant", t)
+    raw, want = GOLD[f"deq_{t}_in"], GOLD[f"deq_{t}_out"]
+    got = gpu.dequantize(t, gpu.upload(raw), want.size)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_every_fp16_scale(gpu):
+    """Q8_0 blocks whose d runs through all 65536 fp16 codes (subnormal, inf,
+    NaN included): d*q for q in [-128, 127] must equal the oracle bit for bit."""
+    nb = 65536
+    b = np.zeros((nb, 34), np.uint8)
+    b[:, 0:2] = np.arange(nb, dtype=np.uint16).view(np.uint8).reshape(nb, 2)
+    q = (np.arange(32) * 8 - 128).astype(np.int8)
+    b[:, 2:] = q.view(np.uint8)
+    raw = b.ravel()
+    got = gpu.dequantize(O.Q8_0, gpu.upload(raw), nb * 32)
+    want = O.dequantize(O.Q8_0, raw, nb * 32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0])
+def test_dequant_synth_bit_exact(gpu, t):
+    W = O.synth_quant(t, 21, 5, 0.02, 64, 2048)
+    got = gpu.dequantize(t, gpu.upload(W), 64 * 2048)
+    want = O.dequantize(t, W, 64 * 2048)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ------------------------------------------------------------------ matvec
+def _matvec_case(gpu, t, M, K, wseed, xseed, std=0.02):
+    W = O.synth_quant(t, wseed, 0, std, M, K)
+    x = O.synth_f32(xseed, 0, 1.0, K)
+    dW, dx, dy = gpu.upload(W), gpu.upload(x), gpu.alloc(4 * M)
+    gpu.matvec(t, dW, dx, dy, M, K)
+    return gpu.download(dy, np.float32, M), O.mat_vec(t, W, x, M, K)
+
+
+@pytest.mark.parametrize("name,t,M,K,ws,xs", [
+    ("config1_q4k", O.Q4_K, 1024, 4096, 0, 1),
+    ("config2_q6k", O.Q6_K, 4096, 1024, 2, 3),
+    ("config2_q8_0", O.Q8_0, 4096, 1024, 2, 3),
+])
+def test_matvec_baseline_configs(gpu, name, t, M, K, ws, xs):
+    say("matvec", name)
+    got, want = _matvec_case(gpu, t, M, K, ws, xs)
+    e, r = parity_err(got, want), inf_rel(got, want)
+    say(f"  parity_err {e:.3e} inf_rel {r:.3e}")
+    assert e <= TOL
+    assert r < 1e-5
+
+
+@pytest.mark.parametrize("t,M,K", [
+    (O.Q4_K, 1, 256), (O.Q4_K, 3, 512), (O.Q4_K, 7, 1024), (O.Q4_K, 33, 2048), (O.Q4_K, 5, 3072),
+    (O.Q4_K, 9, 8192), (O.Q4_K, 2, 16384), (O.Q5_K, 17, 1024), (O.Q5_K, 8, 4096),
+    (O.Q6_K, 1, 256), (O.Q6_K, 11, 768), (O.Q6_K, 64, 3072), (O.Q6_K, 3, 16384),
+    (O.Q8_0, 1, 32), (O.Q8_0, 5, 96), (O.Q8_0, 19, 4096), (O.Q8_0, 2, 8192),
+])
+def test_matvec_shapes(gpu, t, M, K):
+    say("matvec shape", t, M, K)
+    got, want = _matvec_case(gpu, t, M, K, 1000 + M, 2000 + K)
+    assert parity_err(got, want) <= TOL
+
+
+def test_matvec_activation_extremes(gpu):
+    """Activations spanning many binades, exact zeros and a zero group: the
+    block-fixed-point path keeps fp32-level accuracy."""
+    t, M, K = O.Q4_K, 64, 4096
+    W = O.synth_quant(t, 31, 0, 0.02, M, K)
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(K) * np.exp2(rng.integers(-20, 20, K))).astype(np.float32)
+    x[:64] = 0.0
+    x[100:110] = 1e-30
+    dW, dx, dy = gpu.upload(W), gpu.upload(x), gpu.alloc(4 * M)
+    gpu.matvec(t, dW, dx, dy, M, K)
+    got = gpu.download(dy, np.float32, M)
+    ref = O.dequantize(t, W, M * K).reshape(M, K).astype(np.float64) @ x.astype(np.float64)
+    assert parity_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("t,M,K,per_x", [(O.Q4_K, 1024, 4096, False), (O.Q6_K, 4096, 1024, True),
+                                         (O.Q8_0, 256, 1024, True)])
+def test_matvec_batched(gpu, t, M, K, per_x):
+    say("batched", t, per_x)
+    n = 5
+    rb = O.row_bytes(t, K) * M
+    stride = (rb + 4095) // 4096 * 4096
+    dW = gpu.alloc(stride * n)
+    gpu.synth_quant(t, 8, 100, 1, 0.02, M, K, n, dW, stride)
+    xs = np.stack([O.synth_f32(9, m if per_x else 0, 1.0, K) for m in range(n)])
+    dx = gpu.upload(xs if per_x else xs[0])
+    dy = gpu.alloc(4 * M * n)
+    gpu.matvec_batched(t, dW, stride, n, dx, K if per_x else 0, dy, M, M, K)
+    got = gpu.download(dy, np.float32, M * n).reshape(n, M)
+    for m in range(n):
+        want = O.mat_vec(t, O.synth_quant(t, 8, 100 + m, 0.02, M, K), xs[m], M, K)
+        assert parity_err(got[m], want) <= TOL, m
+
+
+# ------------------------------------------------------------------ router
+@pytest.mark.parametrize("norm,bias", [(False, False), (True, True)])
+def test_router_topk(gpu, norm, bias):
+    say("router", norm, bias)
+    E, H, k = 512, 4096, 10
+    R_ = O.synth_f32(4, 3, 0.02, E * H)
+    x = O.synth_f32(4, 5, 1.0, H) * np.float32(1.7)
+    w = (1 + 0.1 * O.synth_f32(4, 7, 1.0, H)).astype(np.float32) if norm else None
+    b = O.zipf_bias(4, 6, E, 1.1) if bias else None
+    ids = gpu.alloc(4 * 16)
+    wts = gpu.alloc(4 * 17)
+    gpu.router_topk(gpu.upload(R_), gpu.upload(b) if bias else None, gpu.upload(x),
+                    gpu.upload(w) if norm else None, 1e-6, E, H, k, ids, wts)
+    gi = gpu.download(ids, np.int32, k)
+    gw = gpu.download(wts, np.float32, k + 1)
+    h = O.rms_norm(x, w, 1e-6) if norm else x
+    logits = O.mat_vec(O.F32, R_, h, E, H)
+    if bias:
+        logits = (logits + b).astype(np.float32)
+    p = O.softmax(logits)
+    oi, ov = O.top_k(p, k)
+    ow = (ov * np.float32(1.0 / ov.sum(dtype=np.float32))).astype(np.float32)
+    assert np.array_equal(gi, oi)
+    assert inf_rel(gw[:k], ow) < 1e-5 and gw[k] == 1.0
+
+
+# ------------------------------------------------------------------ MoE layer
+def _golden_moe_device(gpu):
+    s = GOLD["moe_seed"]
+    seed, E, k, H, F = (int(v) for v in s)
+    gs = F * O.row_bytes(O.Q4_K, H)
+    ds = H * O.row_bytes(O.Q6_K, F)
+    stride = 2 * gs + ds
+    router = O.synth_f32(seed, 3, 0.02, E * H)
+    h = O.synth_f32(seed, 5, 1.0, H)
+    experts = np.concatenate([np.concatenate([O.synth_quant(O.Q4_K, seed, (e << 4) | 0, 0.02, F, H),
+                                              O.synth_quant(O.Q4_K, seed, (e << 4) | 1, 0.02, F, H),
+                                              O.synth_quant(O.Q6_K, seed, (e << 4) | 2, 0.02, H, F)])
+                              for e in range(E + 1)])
+    dR, dE = gpu.upload(router), gpu.upload(experts)
+    L = FA.MoeLayer()
+    L.n_embd, L.inter, L.n_experts, L.k = H, F, E, k
+    L.gate_type, L.up_type, L.down_type = O.Q4_K, O.Q4_K, O.Q6_K
+    L.gate_size, L.up_size, L.expert_stride = gs, gs, stride
+    L.router, L.router_bias, L.experts = dR.ptr, None, dE.ptr
+    L.shared = dE.offset(E * stride)
+    L.shared_inter, L.shared_gate_size, L.shared_up_size = F, gs, gs
+    L.shared_gate_vec, L.norm_w, L.eps = None, None, 1e-6
+    return L, [dR, dE], h, (router, experts, gs, ds, E, k, H, F)
+
+
+def test_moe_layer_vs_reference_golden(gpu):
+    say("moe golden")
+    L, keep, h, _ = _golden_moe_device(gpu)
+    dh, dout = gpu.upload(h), gpu.alloc(4 * h.size)
+    gpu.moe_layer(L, dh, dout, 0)
+    out = gpu.download(dout, np.float32, h.size)
+    ids, w, sw = gpu.last_routing(L.k)
+    assert np.array_equal(ids, GOLD["moe_ids"])
+    assert inf_rel(w, GOLD["moe_w"]) < 1e-5 and sw == 1.0
+    e = parity_err(out, GOLD["moe_out"])
+    say(f"  parity_err {e:.3e}")
+    assert e <= TOL
+
+
+def test_moe_layer_norm_residual_gate(gpu):
+    """GPU_MOE_NORM | GPU_MOE_RESIDUAL with a shared-expert sigmoid gate,
+    in place (out aliases in), against the oracle layer."""
+    L, keep, h, (router, experts, gs, ds, E, k, H, F) = _golden_moe_device(gpu)
+    norm_w = (1 + 0.1 * O.synth_f32(3, 3, 1.0, H)).astype(np.float32)
+    gvec = O.synth_f32(3, 4, 0.05, H)
+    dn, dg = gpu.upload(norm_w), gpu.upload(gvec)
+    L.norm_w, L.shared_gate_vec = dn.ptr, dg.ptr
+    x = (h * np.float32(2.5)).astype(np.float32)
+    dx = gpu.upload(x)
+    gpu.moe_layer(L, dx, dx, FA.MOE_NORM | FA.MOE_RESIDUAL)
+    got = gpu.download(dx, np.float32, H)
+    from test_oracle import moe_desc
+    d = moe_desc(E, k, H, F, router, experts, gs, ds, shared_off=E * (2 * gs + ds), norm_w=norm_w, gvec=gvec)
+    want, oid, ow = O.moe_layer(d, x, O.MOE_NORM | O.MOE_RESIDUAL)
+    ids, w, sw = gpu.last_routing(k)
+    assert np.array_equal(ids, oid)
+    assert parity_err(got - x, want - x) <= TOL   # the FFN part, not just the residual
+    assert parity_err(got, want) <= TOL
+
+
+def test_moe_layer_config3_full(gpu):
+    """BASELINE config 3 at full size: 512 experts (Q4_K gate/up 1024x4096, Q6_K
+    down 4096x1024) + shared, top-10, generated in HBM; the oracle rebuilds the
+    router and only the selected experts on the CPU."""
+    from fomoe_amd import synthetic as S
+    say("moe config3 full")
+    shape = S.LayerShape()
+    layer = S.build_layer(gpu, shape, layer=0, seed=4, norm=False)
+    dh = S.hidden(gpu, shape.n_embd)
+    dout = gpu.alloc(4 * shape.n_embd)
+    gpu.moe_layer(layer.desc, dh, dout, 0)
+    out = gpu.download(dout, np.float32, shape.n_embd)
+    ids, w, sw = gpu.last_routing(shape.k)
+    E, H, F, k = shape.n_experts, shape.n_embd, shape.inter, shape.k
+    h = O.synth_f32(4, S.stream(0, 0, S.HIDDEN), 1.0, H)
+    assert np.array_equal(gpu.download(dh, np.float32, H), h)
+    router = O.synth_f32(4, S.stream(0, 0, S.ROUTER), 0.02, E * H)
+    p = O.softmax(O.mat_vec(O.F32, router, h, E, H))
+    oi, ov = O.top_k(p, k)
+    assert np.array_equal(ids, oi)
+    # sparse expert table: only the routed experts and the shared one are filled
+    stride = shape.stride
+    table = np.zeros((E + 1) * stride, np.uint8)
+    for e in list(oi) + [E]:
+        blob = np.concatenate([O.synth_quant(O.Q4_K, 4, S.stream(0, e, S.GATE), 0.02, F, H),
+                               O.synth_quant(O.Q4_K, 4, S.stream(0, e, S.UP), 0.02, F, H),
+                               O.synth_quant(O.Q6_K, 4, S.stream(0, e, S.DOWN), 0.02, H, F)])
+        table[e * stride:e * stride + blob.size] = blob
+        # the device holds the same bytes
+        dev = gpu.download(layer.desc.experts + e * stride, np.uint8, blob.size)
+        assert np.array_equal(dev, blob), e
+    from test_oracle import moe_desc
+    d = moe_desc(E, k, H, F, router, table, shape.gate_size, shape.down_size, shared_off=E * stride)
+    d.expert_stride = stride
+    want, _, ow = O.moe_layer(d, h, 0)
+    e = parity_err(out, want)
+    say(f"  parity_err {e:.3e} inf_rel {inf_rel(out, want):.3e}")
+    assert inf_rel(w, ow) < 1e-5
+    assert e <= TOL
+
+
+# ------------------------------------------------------------------ reference ABI
+def _ffn_blobs(E, H, F, seed, types=(O.Q4_K, O.Q4_K, O.Q6_K)):
+    gt, ut, dt = types
+    gs, us = F * O.row_bytes(gt, H), F * O.row_bytes(ut, H)
+    ds = H * O.row_bytes(dt, F)
+    blobs = [np.concatenate([O.synth_quant(gt, seed, (e << 4) | 0, 0.02, F, H),
+                             O.synth_quant(ut, seed, (e << 4) | 1, 0.02, F, H),
+                             O.synth_quant(dt, seed, (e << 4) | 2, 0.02, H, F)]) for e in range(E)]
+    return blobs, gs, us, gs + us + ds
+
+
+def _ffn_oracle(blobs, h, scores, H, F, gs, us, types):
+    gt, ut, dt = types
+    out = np.zeros(H, np.float32)
+    for b, s in zip(blobs, scores):
+        g = O.mat_vec(gt, b, h, F, H)
+        g = (g / (np.float32(1) + np.exp(-g))).astype(np.float32)
+        u = O.mat_vec(ut, b[gs:], h, F, H)
+        out = (out + s * O.mat_vec(dt, b[gs + us:], (g * u).astype(np.float32), H, F)).astype(np.float32)
+    return out
+
+
+@pytest.mark.parametrize("types,H,F,n", [((O.Q4_K, O.Q4_K, O.Q6_K), 4096, 1024, 10),
+                                         ((O.Q4_K, O.Q5_K, O.Q5_K), 1024, 512, 3),
+                                         ((O.Q6_K, O.Q6_K, O.Q4_K), 2048, 2048, 1)])
+def test_expert_ffn_reference_abi(gpu, types, H, F, n):
+    say("expert_ffn", types, H, F, n)
+    blobs, gs, us, stride = _ffn_blobs(n, H, F, 50 + n, types)
+    h = O.synth_f32(51, 0, 1.0, H)
+    scores = np.abs(O.synth_f32(52, 0, 1.0, n)).astype(np.float32)
+    scores /= scores.sum()
+    rc, out = gpu.expert_ffn(h, blobs, scores, H, F, gs, us, stride, *types)
+    assert rc == 0, gpu.last_error()
+    want = _ffn_oracle(blobs, h, scores, H, F, gs, us, types)
+    assert parity_err(out, want) <= TOL
+
+
+def test_expert_ffn_fallback_codes(gpu):
+    blobs, gs, us, stride = _ffn_blobs(1, 1024, 512, 7)
+    h = np.ones(1024, np.float32)
+    one = np.ones(1, np.float32)
+    # more than 10 experts, Q8_0, oversize dims -> -1 (use the CPU), no device work
+    assert gpu.expert_ffn(h, blobs * 11, np.ones(11, np.float32), 1024, 512, gs, us, stride,
+                          O.Q4_K, O.Q4_K, O.Q6_K)[0] == -1
+    assert gpu.expert_ffn(h, blobs, one, 1024, 512, gs, us, stride, O.Q8_0, O.Q4_K, O.Q6_K)[0] == -1
+    assert gpu.expert_ffn(h, blobs, one, 8192, 512, gs, us, stride, O.Q4_K, O.Q4_K, O.Q6_K)[0] == -1
+    assert gpu.expert_ffn(h, blobs, one, 1024, 4096, gs, us, stride, O.Q4_K, O.Q4_K, O.Q6_K)[0] == -1
+    assert gpu.expert_ffn(h, blobs, one, 1024, 512, gs, us, 13 << 20, O.Q4_K, O.Q4_K, O.Q6_K)[0] == -1
+    rc, out = gpu.expert_ffn(h, [], np.zeros(0, np.float32), 1024, 512, gs, us, stride,
+                             O.Q4_K, O.Q4_K, O.Q6_K)
+    assert rc == 0 and not out.any()
+
+
+# ------------------------------------------------------------------ decode stack
+def test_stack_decode_small_vs_oracle(gpu):
+    """Three layers with Zipf-biased routing, two steps of x <- x +
+    moe(rms_norm(x)) replayed from a captured graph, against the oracle."""
+    from fomoe_amd import synthetic as S
+    say("stack small")
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=16, k=4)
+    layers = [S.build_layer(gpu, shape, l, seed=11, zipf_s=1.1) for l in range(3)]
+    x0 = O.synth_f32(12, 0, 1.0, shape.n_embd)
+    dx = gpu.upload(x0)
+    gpu.stack_decode([L.desc for L in layers], dx, 2)
+    gpu.sync()
+    got = gpu.download(dx, np.float32, shape.n_embd)
+    E, H, F, k = shape.n_experts, shape.n_embd, shape.inter, shape.k
+    x = x0.copy()
+    from test_oracle import moe_desc
+    host = []
+    for l in range(3):
+        router = O.synth_f32(11, S.stream(l, 0, S.ROUTER), 0.02, E * H)
+        experts = np.zeros((E + 1) * shape.stride, np.uint8)
+        for e in range(E + 1):
+            blob = np.concatenate([O.synth_quant(O.Q4_K, 11, S.stream(l, e, S.GATE), 0.02, F, H),
+                                   O.synth_quant(O.Q4_K, 11, S.stream(l, e, S.UP), 0.02, F, H),
+                                   O.synth_quant(O.Q6_K, 11, S.stream(l, e, S.DOWN), 0.02, H, F)])
+            experts[e * shape.stride:e * shape.stride + blob.size] = blob
+        bias = O.zipf_bias(11, S.stream(l, 0, 6), E, 1.1)
+        norm_w = np.ones(H, np.float32)
+        d = moe_desc(E, k, H, F, router, experts, shape.gate_size, shape.down_size,
+                     shared_off=E * shape.stride, bias=bias, norm_w=norm_w)
+        d.expert_stride = shape.stride
+        host.append((d, router, experts, bias, norm_w))
+    for step in range(2):
+        for l in range(3):
+            x, _, _ = O.moe_layer(host[l][0], x, O.MOE_NORM | O.MOE_RESIDUAL)
+    e = parity_err(got, x)
+    say(f"  parity_err {e:.3e}")
+    assert e <= TOL
