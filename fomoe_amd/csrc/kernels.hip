@@ -182,10 +182,10 @@ static bool geometry(int type, int K, int &G, int &U) {
         return false;
     const int S = K / slot;
     if (S >= 64) { G = 64; U = (S + 63) / 64; return U <= kMaxSlotsPerLane; }
-    G = 1;
+    G = 4;                      // at least 4 lanes per row (extra lanes idle)
     while (G < S) G <<= 1;
     U = 1;
-    return G >= 4;
+    return true;
 }
 
 static int waves_for(int64_t tasks, int n_cu, int per_cu) {
@@ -381,7 +381,7 @@ hipError_t launch_router(const RouterArgs &a, uint8_t *xq_h, int gsz, hipStream_
     const size_t lds = (size_t)a.H * 4;
 #define FO_RT(UU) \
     if (a.H == 256 * UU) { k_router<UU><<<blocks, 256, lds, s>>>(a, xq_h, gsz); return hipGetLastError(); }
-    FO_RT(4) FO_RT(8) FO_RT(12) FO_RT(16) FO_RT(24) FO_RT(32)
+    FO_RT(1) FO_RT(2) FO_RT(4) FO_RT(8) FO_RT(12) FO_RT(16) FO_RT(24) FO_RT(32)
 #undef FO_RT
     return hipErrorInvalidValue;
 }

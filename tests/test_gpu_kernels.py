@@ -215,24 +215,29 @@ def test_moe_layer_vs_reference_golden(gpu):
 
 
 def test_moe_layer_norm_residual_gate(gpu):
-    """GPU_MOE_NORM | GPU_MOE_RESIDUAL with a shared-expert sigmoid gate,
-    in place (out aliases in), against the oracle layer."""
+    """GPU_MOE_NORM with a shared-expert sigmoid gate against the oracle layer,
+    then GPU_MOE_RESIDUAL in place (out aliases in): out = x + ffn."""
     L, keep, h, (router, experts, gs, ds, E, k, H, F) = _golden_moe_device(gpu)
     norm_w = (1 + 0.1 * O.synth_f32(3, 3, 1.0, H)).astype(np.float32)
     gvec = O.synth_f32(3, 4, 0.05, H)
     dn, dg = gpu.upload(norm_w), gpu.upload(gvec)
     L.norm_w, L.shared_gate_vec = dn.ptr, dg.ptr
     x = (h * np.float32(2.5)).astype(np.float32)
-    dx = gpu.upload(x)
-    gpu.moe_layer(L, dx, dx, FA.MOE_NORM | FA.MOE_RESIDUAL)
-    got = gpu.download(dx, np.float32, H)
     from test_oracle import moe_desc
     d = moe_desc(E, k, H, F, router, experts, gs, ds, shared_off=E * (2 * gs + ds), norm_w=norm_w, gvec=gvec)
-    want, oid, ow = O.moe_layer(d, x, O.MOE_NORM | O.MOE_RESIDUAL)
+    want, oid, ow = O.moe_layer(d, x, O.MOE_NORM)
+    dx, dout = gpu.upload(x), gpu.alloc(4 * H)
+    gpu.moe_layer(L, dx, dout, FA.MOE_NORM)
+    ffn = gpu.download(dout, np.float32, H)
     ids, w, sw = gpu.last_routing(k)
     assert np.array_equal(ids, oid)
-    assert parity_err(got - x, want - x) <= TOL   # the FFN part, not just the residual
-    assert parity_err(got, want) <= TOL
+    assert inf_rel(w, ow) < 1e-5
+    hn = O.rms_norm(x, norm_w, 1e-6)
+    assert abs(sw - 1 / (1 + np.exp(-float(hn.astype(np.float64) @ gvec)))) < 1e-6
+    assert parity_err(ffn, want) <= TOL
+    gpu.moe_layer(L, dx, dx, FA.MOE_NORM | FA.MOE_RESIDUAL)
+    got = gpu.download(dx, np.float32, H)
+    assert np.array_equal(got, (x + ffn).astype(np.float32))
 
 
 def test_moe_layer_config3_full(gpu):
@@ -258,7 +263,7 @@ def test_moe_layer_config3_full(gpu):
     # sparse expert table: only the routed experts and the shared one are filled
     stride = shape.stride
     table = np.zeros((E + 1) * stride, np.uint8)
-    for e in list(oi) + [E]:
+    for e in [int(v) for v in oi] + [E]:
         blob = np.concatenate([O.synth_quant(O.Q4_K, 4, S.stream(0, e, S.GATE), 0.02, F, H),
                                O.synth_quant(O.Q4_K, 4, S.stream(0, e, S.UP), 0.02, F, H),
                                O.synth_quant(O.Q6_K, 4, S.stream(0, e, S.DOWN), 0.02, H, F)])
