@@ -15,6 +15,7 @@
 #include "common.h"
 #include "gpu.h"
 #include "kernels.h"
+#include "moe.h"
 
 using namespace fo;
 
@@ -40,6 +41,7 @@ struct gpu_ctx {
     float *vec_out = nullptr;      size_t vec_out_cap = 0;
     uint8_t *staging = nullptr;    size_t staging_cap = 0;
     int last_k = 0;
+    bool last_fast = false;      // routing of the last layer came from the K1-K3 path
 
     // captured stack-decode graph
     hipGraphExec_t graph_exec = nullptr;
@@ -261,11 +263,44 @@ static int size_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L) {
     return 0;
 }
 
+// Shapes the three-kernel path (moe.hip) covers; others take the general path.
+static bool fast_layer(const gpu_moe_layer_t *L) {
+    const int dslot = L->down_type == GGML_TYPE_Q8_0 ? 32 : 64;
+    const int n_tot = L->k + (L->shared ? 1 : 0);
+    return L->n_embd % 512 == 0 && L->n_embd <= 8192 && L->inter / dslot <= 64 && n_tot <= 16;
+}
+
+static constexpr int kSharedW = 32;   // ctx->weights[32] holds the shared-expert weight
+
+static int enqueue_layer_fast(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float *in, float *out,
+                              int flags, const float *norm_w) {
+    const int H = L->n_embd, F = L->inter;
+    const int dg = gsz_of(L->down_type);
+    const uint64_t xs = xq_stride(F, dg);
+    const uint8_t *base = (const uint8_t *)L->experts, *sh = (const uint8_t *)L->shared;
+    float *shared_w = ctx->weights + kSharedW;
+    RouteArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, ctx->logits,
+                 ctx->xq_h, gsz_of(L->gate_type), L->shared_gate_vec, shared_w};
+    HIPC(launch_route(ra, ctx->stream));
+    ExpandArgs ea{ctx->logits, L->n_experts, L->k, ctx->ids, ctx->weights, base, L->expert_stride,
+                  L->gate_size, sh, L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H),
+                  ctx->xq_h, ctx->xq_act, xs, dg, nullptr};
+    HIPC(launch_expand(L->gate_type, ea, ctx->stream, ctx->n_cu));
+    ReduceArgs da{ctx->ids, ctx->weights, sh ? shared_w : nullptr, L->k, base, L->expert_stride,
+                  L->gate_size + L->up_size, sh, L->shared_gate_size + L->shared_up_size, F, H,
+                  fomoe_row_bytes(L->down_type, F), ctx->xq_act, xs,
+                  (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out};
+    HIPC(launch_reduce(L->down_type, da, ctx->stream, ctx->n_cu));
+    return 0;
+}
+
 static int enqueue_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float *in, float *out,
                          int flags) {
     const int H = L->n_embd, F = L->inter, n_tot = L->k + (L->shared ? 1 : 0);
     const float *norm_w = (flags & GPU_MOE_NORM) ? L->norm_w : nullptr;
     if ((flags & GPU_MOE_NORM) && !norm_w) return fail(ctx, -1, "moe layer: GPU_MOE_NORM without norm_w");
+    ctx->last_fast = fast_layer(L);
+    if (ctx->last_fast) return enqueue_layer_fast(ctx, L, in, out, flags, norm_w);
     RouterArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, L->k,
                   ctx->logits, ctx->counter, ctx->ids, ctx->weights, L->shared_gate_vec};
     HIPC(launch_router(ra, ctx->xq_h, gsz_of(L->gate_type), ctx->stream));
@@ -298,9 +333,9 @@ int gpu_moe_last_routing(gpu_ctx_t *ctx, int32_t *ids, float *w, float *shared_w
     float tmp[64];
     HIPC(hipStreamSynchronize(ctx->stream));
     if (ids) HIPC(hipMemcpy(ids, ctx->ids, sizeof(int32_t) * ctx->last_k, hipMemcpyDeviceToHost));
-    HIPC(hipMemcpy(tmp, ctx->weights, sizeof(float) * (ctx->last_k + 1), hipMemcpyDeviceToHost));
+    HIPC(hipMemcpy(tmp, ctx->weights, sizeof(float) * (kSharedW + 1), hipMemcpyDeviceToHost));
     if (w) memcpy(w, tmp, sizeof(float) * ctx->last_k);
-    if (shared_w) *shared_w = tmp[ctx->last_k];
+    if (shared_w) *shared_w = ctx->last_fast ? tmp[kSharedW] : tmp[ctx->last_k];
     return 0;
 }
 

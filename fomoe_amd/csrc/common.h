@@ -16,10 +16,11 @@ namespace fo {
 constexpr int kWave = 64;
 
 // Prepared-activation layout (see formats.h): K values in groups of gsz take
-// K*4 bytes of int8 limbs plus K/gsz float2 {scale, sum}.
+// K*3 bytes of int8 limbs (three per value) plus K/gsz float2 {scale, sum}.
 __host__ __device__ constexpr int gsz_of(int type) { return type == GGML_TYPE_Q6_K ? 16 : 32; }
+__host__ __device__ constexpr uint64_t xq_limb_bytes(int K) { return (uint64_t)K * 3; }
 __host__ __device__ constexpr uint64_t xq_bytes(int K, int gsz) {
-    return (uint64_t)K * 4 + (uint64_t)(K / gsz) * 8;
+    return xq_limb_bytes(K) + (uint64_t)(K / gsz) * 8;
 }
 // Per-vector stride of a prepared batch, rounded to 256 bytes.
 __host__ __device__ constexpr uint64_t xq_stride(int K, int gsz) {
@@ -44,6 +45,27 @@ FO_DEV uint4 ld16_stream(const uint8_t *p) {
     v.w = __builtin_nontemporal_load((const uint32_t *)p + 3);
     return v;
 }
+
+// Stage nbytes (a multiple of 16) from global memory into LDS with gfx950's
+// direct global->LDS loads (global_load_lds_dwordx4): every wave streams
+// 1 KiB pieces, all in flight at once, no VGPRs. The LDS buffer must have room
+// up to the next multiple of 1 KiB (the last piece's spare lanes re-read the
+// final 16 bytes into that padding). Completion: s_waitcnt vmcnt(0) and a
+// barrier, see stage_lds_wait().
+FO_DEV void stage_lds(uint8_t *lds_dst, const uint8_t *g, uint32_t nbytes, int wave, int nwaves) {
+    const int lane = threadIdx.x & 63;
+    for (uint32_t off = (uint32_t)wave * 1024u; off < nbytes; off += (uint32_t)nwaves * 1024u) {
+        const uint32_t o = off + (uint32_t)lane * 16u;
+        const uint8_t *src = g + (o < nbytes ? o : nbytes - 16u);
+        __builtin_amdgcn_global_load_lds((const void *)src,
+                                         (__attribute__((address_space(3))) void *)(lds_dst + off), 16, 0, 0);
+    }
+}
+FO_DEV void stage_lds_wait() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+}
+__host__ __device__ constexpr uint32_t lds_round(uint64_t n) { return (uint32_t)((n + 1023) & ~(uint64_t)1023); }
 
 // fp16 bits -> fp32 (exact; hardware conversion handles subnormals, inf, NaN)
 FO_DEV float h2f(uint32_t bits16) {

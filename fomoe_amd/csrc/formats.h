@@ -8,15 +8,15 @@
 // Arithmetic. At batch 1 a plain "byte -> float, fma" unpack costs ~5 VALU
 // instructions per Q4_K weight byte, which on gfx950 is as slow as HBM itself.
 // Instead the activation is held in block fixed point: each group of GSZ
-// values shares an exponent e, X = round(x * 2^e) with |X| < 2^30, split into
-// four balanced int8 limbs X = X0 + 2^8 X1 + 2^16 X2 + 2^24 X3. The weight
+// values shares an exponent e, X = round(x * 2^e) with |X| < 2^22, split into
+// three balanced int8 limbs X = X0 + 2^8 X1 + 2^16 X2. The weight
 // codes are small non-negative (or int8) integers, so
 //     sum_i q_i * X_i = sum_L 2^(8L) * sum_i q_i * X_{L,i}
 // is computed exactly with v_dot4c_i32_i8 (4 products per instruction) and
-// only the per-group combination and the scale application use fp32. X equals
-// x exactly for every value within 2^6 of the group maximum, and smaller values
-// carry an absolute error below 2^-31 of that maximum — far inside the fp32
-// rounding of the reference's own sum (reference src/quant.c:109-212).
+// only the per-group combination and the scale application use fp32. Each X
+// carries an absolute error of at most 2^-23 of the group maximum (2 ulp of
+// the largest value) — the size of the fp32 rounding the reference's own
+// sequential sum incurs (reference src/quant.c:109-212).
 //
 // Sub-block scales are applied once per sub-block: sum_i (d*sc*q_i - dmin*m)
 // * x_i = d*sc*sum_i q_i x_i - dmin*m*sum_i x_i; the group sums of x are
@@ -31,17 +31,17 @@
 
 namespace fo {
 
-constexpr int kLimbs = 4;
+constexpr int kLimbs = 3;
+constexpr int kFixBits = 22;   // |X| < 2^22: limbs X0, X1 in [-128,127], X2 in [-64,64]
 
 // Prepared activation of one group of GSZ values:
 //   limb dwords l[L][k] hold limb L of values 4k..4k+3 (one int8 each),
 //   scsum = {2^-e, sum of the group's fp32 values}.
 // In memory a vector of K values is [K/GSZ groups][kLimbs][GSZ/4] int32 limb
-// dwords followed by K/GSZ float2 {scale, sum}.
+// dwords followed by K/GSZ float2 {scale, sum} (xq_bytes in common.h).
 
 FO_DEV float combine(const int a[kLimbs]) {
-    float f = (float)a[3];
-    f = fmaf(f, 256.f, (float)a[2]);
+    float f = (float)a[2];
     f = fmaf(f, 256.f, (float)a[1]);
     return fmaf(f, 256.f, (float)a[0]);
 }
@@ -61,7 +61,7 @@ template <int NG, int GSZ> struct XSlot {
 // Load the groups gi[0..NG) of a prepared vector into registers.
 template <int NG, int GSZ>
 FO_DEV void load_xslot(XSlot<NG, GSZ> &x, const uint8_t *xq, int K, const int gi[NG]) {
-    const uint8_t *ss = xq + (uint64_t)K * 4;
+    const uint8_t *ss = xq + xq_limb_bytes(K);
 #pragma unroll
     for (int g = 0; g < NG; g++) {
         const uint8_t *p = xq + (uint64_t)gi[g] * (kLimbs * GSZ);
@@ -119,7 +119,7 @@ template <> struct Fmt<GGML_TYPE_Q4_K> {
     }
     static FO_DEV float dot(const Raw &r, int s, const X &x) {
         const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-        int a0[kLimbs] = {0, 0, 0, 0}, a1[kLimbs] = {0, 0, 0, 0};
+        int a0[kLimbs] = {}, a1[kLimbs] = {};
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
@@ -151,7 +151,7 @@ template <> struct Fmt<GGML_TYPE_Q5_K> {
         const int g = s & 3;
         const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
         const uint32_t h[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
-        int a0[kLimbs] = {0, 0, 0, 0}, a1[kLimbs] = {0, 0, 0, 0};
+        int a0[kLimbs] = {}, a1[kLimbs] = {};
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const uint32_t hb = h[k] >> (2 * g);
@@ -233,7 +233,7 @@ template <> struct Fmt<GGML_TYPE_Q8_0> {
     static FO_DEV void groups(int s, int gi[NG]) { gi[0] = s; }
     static FO_DEV float dot(const Raw &r, int, const X &x) {
         const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-        int a[kLimbs] = {0, 0, 0, 0};
+        int a[kLimbs] = {};
 #pragma unroll
         for (int k = 0; k < 8; k++)
 #pragma unroll

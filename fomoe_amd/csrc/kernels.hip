@@ -39,7 +39,7 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ x, uint
     for (int i = 0; i < GSZ; i++) { M = fmaxf(M, fabsf(vals[i])); sum += vals[i]; }
     int E = 0;
     frexpf(M, &E);               // M < 2^E
-    int e = 30 - E;
+    int e = kFixBits - E;
     if (e > 149) e = 149;        // keep 2^-e representable
     const float scale = (M > 0.f) ? ldexpf(1.0f, -e) : 0.f;
     uint32_t limb[kLimbs][GSZ / 4];
@@ -66,7 +66,7 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ x, uint
         for (int k = 0; k < GSZ / 4; k += 4)
             *(uint4 *)(lp + L * (GSZ / 4) + k) =
                 make_uint4(limb[L][k], limb[L][k + 1], limb[L][k + 2], limb[L][k + 3]);
-    *(float2 *)(out + (uint64_t)K * 4 + (uint64_t)g * 8) = make_float2(scale, sum);
+    *(float2 *)(out + xq_limb_bytes(K) + (uint64_t)g * 8) = make_float2(scale, sum);
 }
 
 hipError_t launch_xprep(int gsz, const float *x, uint64_t x_stride, int K, int n_vec,
@@ -259,11 +259,11 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a, uint8_t *__restric
             for (int i = 0; i < gsz; i++) { M = fmaxf(M, fabsf(xp[i])); sum += xp[i]; }
             int E = 0;
             frexpf(M, &E);
-            int e = 30 - E;
+            int e = kFixBits - E;
             if (e > 149) e = 149;
             uint32_t *lp = (uint32_t *)(xq_h + (uint64_t)g * (kLimbs * gsz));
             for (int k = 0; k < gsz / 4; k++) {
-                uint32_t lb[kLimbs] = {0, 0, 0, 0};
+                uint32_t lb[kLimbs] = {};
                 for (int b = 0; b < 4; b++) {
                     int X = (M > 0.f) ? __float2int_rn(ldexpf(xp[4 * k + b], e)) : 0;
                     for (int L = 0; L < kLimbs - 1; L++) {
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a, uint8_t *__restric
                 }
                 for (int L = 0; L < kLimbs; L++) lp[L * (gsz / 4) + k] = lb[L];
             }
-            *(float2 *)(xq_h + (uint64_t)H * 4 + (uint64_t)g * 8) =
+            *(float2 *)(xq_h + xq_limb_bytes(H) + (uint64_t)g * 8) =
                 make_float2((M > 0.f) ? ldexpf(1.0f, -e) : 0.f, sum);
         }
     }

@@ -1,0 +1,70 @@
+// moe.h — argument blocks of the three-kernel MoE layer (moe.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fo {
+
+// K1: logits[E] = router . h (+ bias), h = rms_norm(x) * norm_w (norm_w NULL:
+// h = x); writes the prepared h (groups of gsz) and *shared_w = sigmoid(h.v)
+// (1 when shared_gate_vec is NULL).
+struct RouteArgs {
+    const float *router, *bias, *x, *norm_w;
+    float eps;
+    int E, H;
+    float *logits;
+    uint8_t *xq_h;
+    int gsz;
+    const float *shared_gate_vec;
+    float *shared_w;
+};
+
+// K2: top-k of logits, then act_e = silu(gate_e . h) * (up_e . h) for the k
+// routed experts (blob = base + id*stride: gate at 0, up at gate_size) and the
+// shared expert (gate at 0, up at sh_gate_size), written in prepared form
+// (groups of down_gsz) at xq_act + e*xq_vstride, and as fp32 to act if set.
+// Work-group 0 writes ids[k] / weights[k].
+struct ExpandArgs {
+    const float *logits;
+    int E, k;
+    int32_t *ids;
+    float *weights;
+    const uint8_t *base;
+    uint64_t stride, gate_size;
+    const uint8_t *shared;
+    uint64_t sh_gate_size;
+    int F, H;
+    uint64_t row_bytes;
+    const uint8_t *xq_h;
+    uint8_t *xq_act;
+    uint64_t xq_vstride;
+    int down_gsz;
+    float *act;
+};
+
+// K3: out[i] = (resid ? resid[i] : 0) + sum_e w_e * down_e[i,:] . act_e over
+// the k routed experts in rank order, then the shared expert (weight
+// *shared_w, or 1 when NULL).
+struct ReduceArgs {
+    const int32_t *ids;
+    const float *weights;
+    const float *shared_w;
+    int k;
+    const uint8_t *base;
+    uint64_t stride, down_off;
+    const uint8_t *shared;
+    uint64_t sh_down_off;
+    int F, H;
+    uint64_t row_bytes;
+    const uint8_t *xq_act;
+    uint64_t xq_vstride;
+    const float *resid;
+    float *out;
+};
+
+hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+hipError_t launch_expand(int gate_type, const ExpandArgs &a, hipStream_t s, int n_cu);
+hipError_t launch_reduce(int down_type, const ReduceArgs &a, hipStream_t s, int n_cu);
+
+}  // namespace fo

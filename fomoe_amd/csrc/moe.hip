@@ -1,0 +1,434 @@
+// moe.hip — the batch-1 MoE layer as three kernels with no device-scope
+// atomics (on MI355X an agent-scope atomic serialises at ~10 ns, so a 256-WG
+// "last block" handshake costs more than a kernel boundary in a graph):
+//
+//   K1 k_route   router logits = W_r . rms_norm(x) (+ bias); the prepared
+//                (block-fixed-point) activation of h for the experts; the
+//                shared-expert gate sigmoid(h . v).
+//   K2 k_expand  every work-group recomputes top-k + renormalisation from the
+//                logits (a few hundred VALU instructions, cheaper than any
+//                grid-wide handshake), then streams gate/up rows of the routed
+//                experts and the shared expert; each task covers one activation
+//                group of rows, so the WG writes silu(g)*u straight into the
+//                prepared form the down projection consumes.
+//   K3 k_reduce  down projection of all selected experts for a block of output
+//                rows with every expert's prepared activation staged in LDS once
+//                per WG; the weighted combine and the residual are summed in
+//                registers in a fixed order (deterministic).
+//
+// Semantics follow reference src/inference.c:481-606 (router, softmax, top-k,
+// renormalise, SwiGLU experts, scaled add in rank order, shared expert with
+// optional sigmoid gate, residual); the reference GPU kernels replaced are
+// gpu_kernels.hip kernel_f32_matvec_coop 2127, kernel_softmax 2668,
+// kernel_top_k_parallel 2745, kernel_q4k_fused_gate_up_silu 1320,
+// kernel_q4k_fused_gus_mw 1474, kernel_q6k_matvec_per_expert 1261,
+// kernel_moe_output_residual 1647 and kernel_dot_sigmoid_scale 3648.
+#include <float.h>
+
+#include "formats.h"
+#include "moe.h"
+
+namespace fo {
+
+// ------------------------------------------------------------ wave primitives
+template <int CTRL>
+FO_DEV float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+FO_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false); }
+
+// Maximum over the 64 lanes, returned in every lane: butterflies inside quads,
+// half-row and row mirrors (16-lane maxima), then the four row maxima.
+FO_DEV float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));   // row_mirror
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+FO_DEV int wave_min_dpp(int v) {
+    v = min(v, dpp_i<0xB1>(v));
+    v = min(v, dpp_i<0x4E>(v));
+    v = min(v, dpp_i<0x141>(v));
+    v = min(v, dpp_i<0x140>(v));
+    const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return min(min(a, b), min(c, d));
+}
+FO_DEV float wave_sum_dpp(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Top-k of E logits (<= 1024) with ties to the lowest index — the order of
+// reference src/tensor.c:226-252 applied to softmax(logits), which is
+// monotone — and the renormalised weights exp(l_i - l_max) / sum over the
+// selection (= softmax then renormalise, reference src/inference.c:488-502).
+// Executed by one wave; results in ids[k], w[k].
+constexpr int kMaxE = 1024, kMaxK = 16;
+FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *ids, float *w) {
+    constexpr int NV = kMaxE / 64;
+    const int lane = threadIdx.x & 63;
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = lane + 64 * j;
+        v[j] = (64 * j < E && i < E) ? logits[i] : -FLT_MAX;
+    }
+    const int nv = (E + 63) / 64;
+    float sel_v[kMaxK];
+    int sel_i[kMaxK];
+    for (int kk = 0; kk < k; kk++) {
+        float lb = -FLT_MAX;
+        int lj = 0;
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+            if (j < nv && v[j] > lb) { lb = v[j]; lj = j; }
+        const float m = wave_max_dpp(lb);
+        const uint64_t ball = __ballot(lb == m);
+        int idx;
+        if (__popcll(ball) == 1) {
+            const int wl = __ffsll((unsigned long long)ball) - 1;
+            idx = 64 * __builtin_amdgcn_readlane(lj, wl) + wl;
+        } else {
+            idx = wave_min_dpp(lb == m ? 64 * lj + lane : 0x7FFFFFFF);
+        }
+        if (idx < 0 || idx >= E) idx = 0;   // non-finite logits: never index outside the table
+        sel_v[kk] = m;
+        sel_i[kk] = idx;
+        if (lane == (idx & 63)) {
+#pragma unroll
+            for (int j = 0; j < NV; j++)
+                if (j == (idx >> 6)) v[j] = -FLT_MAX;
+        }
+    }
+    if (lane == 0) {
+        const float mx = sel_v[0];
+        float e[kMaxK], s = 0.f;
+        for (int kk = 0; kk < k; kk++) { e[kk] = expf(sel_v[kk] - mx); s += e[kk]; }
+        const float inv = 1.0f / s;
+        for (int kk = 0; kk < k; kk++) { ids[kk] = sel_i[kk]; w[kk] = e[kk] * inv; }
+    }
+}
+
+// Prepare one group of G values held one per lane in lanes [0, G) of a wave
+// (G = 16 or 32): exponent from the group maximum, four balanced int8 limbs
+// per value packed four values per dword, {2^-e, fp32 sum}. Layout as in
+// formats.h. `dst` points at the vector's limb area, `ss` at its {scale,sum}
+// area, g is the group index.
+template <int G>
+FO_DEV void prep_group_lanes(float val, int g, uint8_t *__restrict__ dst, uint8_t *__restrict__ ss) {
+    const int lane = threadIdx.x & 63;
+    float a = fabsf(val), s = val;
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) {
+        a = fmaxf(a, __shfl_xor(a, o, 64));
+        s += __shfl_xor(s, o, 64);
+    }
+    int E = 0;
+    frexpf(a, &E);
+    int e = kFixBits - E;
+    if (e > 149) e = 149;
+    int X = (a > 0.f) ? __float2int_rn(ldexpf(val, e)) : 0;
+    uint32_t limb[kLimbs];
+#pragma unroll
+    for (int L = 0; L < kLimbs - 1; L++) {
+        const int b = (int)(int8_t)(X & 0xFF);
+        X = (X - b) >> 8;
+        limb[L] = (uint32_t)(b & 0xFF);
+    }
+    limb[kLimbs - 1] = (uint32_t)(X & 0xFF);
+    // gather bytes of lanes 4q..4q+3 into lane 4q
+#pragma unroll
+    for (int L = 0; L < kLimbs; L++) {
+        const uint32_t b1 = (uint32_t)__shfl_down((int)limb[L], 1, 64);
+        const uint32_t b2 = (uint32_t)__shfl_down((int)limb[L], 2, 64);
+        const uint32_t b3 = (uint32_t)__shfl_down((int)limb[L], 3, 64);
+        limb[L] = limb[L] | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+    if (lane < G && (lane & 3) == 0) {
+        uint32_t *p = (uint32_t *)(dst + (uint64_t)g * (kLimbs * G));
+#pragma unroll
+        for (int L = 0; L < kLimbs; L++) p[L * (G / 4) + (lane >> 2)] = limb[L];
+    }
+    if (lane == 0) *(float2 *)(ss + (uint64_t)g * 8) = make_float2(a > 0.f ? ldexpf(1.0f, -e) : 0.f, s);
+}
+
+// ============================================================ K1: route
+// WG of 256 threads = 4 waves; WG b handles router rows 2b, 2b+1, each split
+// over two waves (half of H each). The weight loads are issued before the
+// norm so their latency overlaps it.
+template <int UH>  // H = 512*UH; a lane holds UH float4 of one half-row
+__global__ __launch_bounds__(256) void k_route(RouteArgs a) {
+    extern __shared__ float sh[];             // h [H]
+    __shared__ float part[4];
+    __shared__ float red[4];
+    const int H = a.H, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int row = 2 * blockIdx.x + (wv >> 1), half = wv & 1;
+    float4 wr[UH];
+    const bool has_row = row < a.E;
+    if (has_row) {
+        const float4 *rp = (const float4 *)(a.router + (uint64_t)row * H) + half * (H / 8);
+#pragma unroll
+        for (int u = 0; u < UH; u++) wr[u] = rp[lane + 64 * u];
+    }
+    float *shw = sh + lds_round((uint64_t)H * 4) / 4;   // norm weight
+    stage_lds((uint8_t *)sh, (const uint8_t *)a.x, (uint32_t)H * 4, wv, 4);
+    if (a.norm_w) stage_lds((uint8_t *)shw, (const uint8_t *)a.norm_w, (uint32_t)H * 4, wv, 4);
+    stage_lds_wait();
+    if (a.norm_w) {
+        float ss = 0.f;
+        for (int i = tid; i < H; i += 256) ss += sh[i] * sh[i];
+        ss = wave_sum_dpp(ss);
+        if (lane == 0) red[wv] = ss;
+        __syncthreads();
+        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const float scale = 1.0f / sqrtf(tot / (float)H + a.eps);
+        __syncthreads();
+        for (int i = tid; i < H; i += 256) sh[i] = sh[i] * scale * shw[i];
+        __syncthreads();
+    }
+    // this WG's share of the prepared h (groups of a.gsz values, one wave each)
+    if (a.xq_h) {
+        const int ng = H / a.gsz;
+        const int per = (ng + gridDim.x - 1) / gridDim.x;
+        for (int j = wv; j < per; j += 4) {
+            const int g = blockIdx.x * per + j;
+            if (g >= ng) break;
+            const float val = lane < a.gsz ? sh[g * a.gsz + lane] : 0.f;
+            if (a.gsz == 16) prep_group_lanes<16>(val, g, a.xq_h, a.xq_h + xq_limb_bytes(H));
+            else prep_group_lanes<32>(val, g, a.xq_h, a.xq_h + xq_limb_bytes(H));
+        }
+    }
+    // shared-expert gate
+    if (blockIdx.x == 0 && wv == 0 && a.shared_w) {
+        float g = 1.0f;
+        if (a.shared_gate_vec) {
+            float d = 0.f;
+            for (int i = lane; i < H; i += 64) d += sh[i] * a.shared_gate_vec[i];
+            d = wave_sum_dpp(d);
+            g = 1.0f / (1.0f + expf(-d));
+        }
+        if (lane == 0) *a.shared_w = g;
+    }
+    float acc = 0.f;
+    if (has_row) {
+        const float *hp = sh + half * (H / 2);
+#pragma unroll
+        for (int u = 0; u < UH; u++) {
+            const float4 hv = *(const float4 *)(hp + 4 * (lane + 64 * u));
+            acc = fmaf(wr[u].x, hv.x, acc);
+            acc = fmaf(wr[u].y, hv.y, acc);
+            acc = fmaf(wr[u].z, hv.z, acc);
+            acc = fmaf(wr[u].w, hv.w, acc);
+        }
+        acc = wave_sum_dpp(acc);
+    }
+    if (lane == 0) part[wv] = acc;
+    __syncthreads();
+    if (tid < 2) {
+        const int r = 2 * blockIdx.x + tid;
+        if (r < a.E) a.logits[r] = (part[2 * tid] + part[2 * tid + 1]) + (a.bias ? a.bias[r] : 0.f);
+    }
+}
+
+hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
+    if (a.E <= 0 || a.E > kMaxE || a.H % 512 || a.H > 8192) return hipErrorInvalidValue;
+    const int blocks = (a.E + 1) / 2;
+    const size_t lds = 2 * (size_t)lds_round((uint64_t)a.H * 4);
+#define FO_K1(U) if (a.H == 512 * U) { k_route<U><<<blocks, 256, lds, s>>>(a); return hipGetLastError(); }
+    FO_K1(1) FO_K1(2) FO_K1(3) FO_K1(4) FO_K1(6) FO_K1(8) FO_K1(12) FO_K1(16)
+#undef FO_K1
+    return hipErrorInvalidValue;
+}
+
+// ============================================================ K2: expand
+// One work-group of 4 waves per task (expert slot e, block of TR rows, TR =
+// the activation-group size of the down projection); the grid is all tasks at
+// once (k=10 + shared, F=1024, TR=16: 704 WGs, all resident), and every wave
+// issues all its weight loads before any arithmetic, so the layer's whole
+// gate/up traffic is in flight together. Routed WGs first compute top-k (wave
+// 0) while the other waves stage the prepared h in LDS; the shared expert's
+// WGs skip the top-k. The TR results meet in LDS and wave 0 writes them in
+// prepared form for K3 (and as fp32 when a.act is set).
+template <int T, int TR, int G, int U>
+__global__ __launch_bounds__(256, 3) void k_expand(ExpandArgs a) {
+    using F = Fmt<T>;
+    constexpr int P = kWave / G;                        // rows side by side per pass
+    constexpr int PASS = (TR + 4 * P - 1) / (4 * P);    // passes per wave
+    extern __shared__ uint8_t lds[];                    // prepared h
+    __shared__ int s_ids[kMaxK];
+    __shared__ float s_w[kMaxK];
+    __shared__ float s_act[TR];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, sub = lane / G;
+    const int H = a.H, F_ = a.F;
+    const int tpe = F_ / TR;
+    const int e = blockIdx.x / tpe, rb = blockIdx.x - e * tpe;
+    const bool routed = e < a.k;
+    const uint64_t xqb = xq_bytes(H, F::GSZ);
+    if (routed && wv == 0) {
+        wave_topk(a.logits, a.E, a.k, s_ids, s_w);
+        if (blockIdx.x == 0 && lane == 0)
+            for (int i = 0; i < a.k; i++) { a.ids[i] = s_ids[i]; a.weights[i] = s_w[i]; }
+    } else {
+        stage_lds(lds, a.xq_h, (uint32_t)xqb, routed ? wv - 1 : wv, routed ? 3 : 4);
+    }
+    stage_lds_wait();
+    const uint8_t *blob;
+    uint64_t uo;
+    if (routed) { blob = a.base + (uint64_t)s_ids[e] * a.stride; uo = a.gate_size; }
+    else { blob = a.shared; uo = a.sh_gate_size; }
+    // slots past S mirror the last slot (valid addresses) and contribute 0
+    const int S = H / F::SLOT;
+    int slot[U];
+    float live[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int sl = (lane % G) + G * u;
+        slot[u] = min(sl, S - 1);
+        live[u] = sl < S ? 1.f : 0.f;
+    }
+    typename F::Raw rg[PASS][U], ru[PASS][U];
+#pragma unroll
+    for (int p = 0; p < PASS; p++) {
+        const int rl = p * 4 * P + wv * P + sub;
+        const int row = rb * TR + min(rl, TR - 1);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            rg[p][u] = F::load(blob + (uint64_t)row * a.row_bytes, slot[u]);
+            ru[p][u] = F::load(blob + uo + (uint64_t)row * a.row_bytes, slot[u]);
+        }
+    }
+    typename F::X X[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        int gi[F::NG];
+        F::groups(slot[u], gi);
+        load_xslot(X[u], lds, H, gi);
+    }
+#pragma unroll
+    for (int p = 0; p < PASS; p++) {
+        float g = 0.f, v = 0.f;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            g = fmaf(live[u], F::dot(rg[p][u], slot[u], X[u]), g);
+            v = fmaf(live[u], F::dot(ru[p][u], slot[u], X[u]), v);
+        }
+        g = group_sum<G>(g);
+        v = group_sum<G>(v);
+        const int rl = p * 4 * P + wv * P + sub;
+        if ((lane % G) == 0 && rl < TR) s_act[rl] = (g / (1.0f + expf(-g))) * v;
+    }
+    __syncthreads();
+    if (wv == 0) {
+        const float val = lane < TR ? s_act[lane] : 0.f;
+        uint8_t *dst = a.xq_act + (uint64_t)e * a.xq_vstride;
+        prep_group_lanes<TR>(val, rb, dst, dst + xq_limb_bytes(F_));
+        if (a.act && lane < TR) a.act[(uint64_t)e * F_ + rb * TR + lane] = val;
+    }
+}
+
+hipError_t launch_expand(int type, const ExpandArgs &a, hipStream_t s, int n_cu) {
+    (void)n_cu;
+    const int slot = type == GGML_TYPE_Q8_0 ? 32 : 64;
+    const int TR = a.down_gsz;
+    if (a.k <= 0 || a.k > kMaxK || a.E <= 0 || a.E > kMaxE || a.F <= 0 || a.F % TR || a.H % slot ||
+        (TR != 16 && TR != 32))
+        return hipErrorInvalidValue;
+    const int S = a.H / slot;
+    int G = 4, U = 1;
+    while (G < S && G < 64) G <<= 1;
+    if (S > 64) U = (S + 63) / 64;
+    if (U > 2) return hipErrorInvalidValue;
+    const int n_tot = a.k + (a.shared ? 1 : 0);
+    const size_t lds = lds_round(xq_bytes(a.H, type == GGML_TYPE_Q6_K ? 16 : 32));
+    const int grid = a.F / TR * n_tot;
+#define FO_K2(TT, RR, GG, UU) \
+    if (type == TT && TR == RR && G == GG && U == UU) { k_expand<TT, RR, GG, UU><<<grid, 256, lds, s>>>(a); return hipGetLastError(); }
+#define FO_K2T(TT) \
+    FO_K2(TT, 16, 64, 1) FO_K2(TT, 16, 64, 2) FO_K2(TT, 16, 32, 1) FO_K2(TT, 16, 16, 1) FO_K2(TT, 16, 8, 1) FO_K2(TT, 16, 4, 1) \
+    FO_K2(TT, 32, 64, 1) FO_K2(TT, 32, 64, 2) FO_K2(TT, 32, 32, 1) FO_K2(TT, 32, 16, 1) FO_K2(TT, 32, 8, 1) FO_K2(TT, 32, 4, 1)
+    FO_K2T(GGML_TYPE_Q4_K) FO_K2T(GGML_TYPE_Q5_K) FO_K2T(GGML_TYPE_Q6_K) FO_K2T(GGML_TYPE_Q8_0)
+#undef FO_K2T
+#undef FO_K2
+    return hipErrorInvalidValue;
+}
+
+// ============================================================ K3: reduce
+// One work-group per block of RB = P*RP output rows with one wave per
+// selected expert (routed in rank order, then shared): the wave keeps its
+// expert's prepared activation in registers for RP passes of P rows (G lanes
+// per row), so it is fetched once per RB rows; every wave issues all its
+// weight loads before any arithmetic. Per-expert row sums meet in LDS and
+// out = resid + sum_e w_e * dot_e is summed in that fixed order.
+template <int T, int G, int RP>
+__global__ __launch_bounds__(1024) void k_reduce(ReduceArgs a) {
+    using F = Fmt<T>;
+    constexpr int P = kWave / G, RB = P * RP;
+    __shared__ float part[kMaxK + 1][RB];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, sub = lane / G;
+    const int n_tot = a.k + (a.shared ? 1 : 0);
+    const int S = a.F / F::SLOT;
+    const int slot = min(lane % G, S - 1);          // lanes past S mirror the last slot ...
+    const float live = (lane % G) < S ? 1.f : 0.f;  // ... and contribute nothing
+    const int row0 = blockIdx.x * RB;
+    if (wv < n_tot) {
+        const uint8_t *m = (wv < a.k) ? a.base + (uint64_t)a.ids[wv] * a.stride + a.down_off
+                                      : a.shared + a.sh_down_off;
+        typename F::Raw raw[RP];
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            const int row = min(row0 + p * P + sub, a.H - 1);
+            raw[p] = F::load(m + (uint64_t)row * a.row_bytes, slot);
+        }
+        typename F::X X;
+        int gi[F::NG];
+        F::groups(slot, gi);
+        load_xslot(X, a.xq_act + (uint64_t)wv * a.xq_vstride, a.F, gi);
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            const float v = group_sum<G>(live * F::dot(raw[p], slot, X));
+            if ((lane % G) == 0) part[wv][p * P + sub] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < RB && row0 + tid < a.H) {
+        float acc = 0.f;
+        for (int e = 0; e < a.k; e++) acc = fmaf(a.weights[e], part[e][tid], acc);
+        if (a.shared) acc = fmaf(a.shared_w ? *a.shared_w : 1.0f, part[a.k][tid], acc);
+        a.out[row0 + tid] = (a.resid ? a.resid[row0 + tid] : 0.f) + acc;
+    }
+}
+
+hipError_t launch_reduce(int type, const ReduceArgs &a, hipStream_t s, int n_cu) {
+    (void)n_cu;
+    const int slot = type == GGML_TYPE_Q8_0 ? 32 : 64;
+    const int n_tot = a.k + (a.shared ? 1 : 0);
+    if (a.F % slot || a.F / slot > 64 || a.k <= 0 || n_tot > 16 || a.H <= 0) return hipErrorInvalidValue;
+    const int S = a.F / slot;
+    int G = 4;
+    while (G < S) G <<= 1;
+    constexpr int RP = 4;
+    const int RB = (64 / G) * RP;
+    const int grid = (a.H + RB - 1) / RB;
+    const int threads = 64 * n_tot;
+#define FO_K3(TT, GG) \
+    if (type == TT && G == GG) { k_reduce<TT, GG, RP><<<grid, threads, 0, s>>>(a); return hipGetLastError(); }
+#define FO_K3T(TT) FO_K3(TT, 64) FO_K3(TT, 32) FO_K3(TT, 16) FO_K3(TT, 8) FO_K3(TT, 4)
+    FO_K3T(GGML_TYPE_Q4_K) FO_K3T(GGML_TYPE_Q5_K) FO_K3T(GGML_TYPE_Q6_K) FO_K3T(GGML_TYPE_Q8_0)
+#undef FO_K3T
+#undef FO_K3
+    return hipErrorInvalidValue;
+}
+
+}  // namespace fo
