@@ -79,12 +79,25 @@ FO_DEV float ub2(uint32_t v) { return (float)((v >> 16) & 0xFFu); }
 FO_DEV float ub3(uint32_t v) { return (float)(v >> 24); }
 
 // ---------------------------------------------------------- reductions
+// DPP lane exchanges (gfx9 encodings): quad_perm [1,0,3,2] 0xB1 and
+// [2,3,0,1] 0x4E, row_half_mirror 0x141 (lane i <-> 7-i within 8), row_mirror
+// 0x140 (lane i <-> 15-i within 16).
+template <int CTRL>
+FO_DEV float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 // Sum over groups of G consecutive lanes (G a power of two <= 64); every lane
-// of the group receives the group sum.
+// of the group receives the group sum. Butterflies inside quads, then the
+// 8- and 16-lane mirrors (all DPP, no LDS round trip); 32/64 use permutes.
 template <int G>
 FO_DEV float group_sum(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    if (G >= 2) v += dpp<0xB1>(v);
+    if (G >= 4) v += dpp<0x4E>(v);
+    if (G >= 8) v += dpp<0x141>(v);
+    if (G >= 16) v += dpp<0x140>(v);
+    if (G >= 32) v += __shfl_xor(v, 16, kWave);
+    if (G >= 64) v += __shfl_xor(v, 32, kWave);
     return v;
 }
 

@@ -98,17 +98,17 @@ template <> struct Fmt<GGML_TYPE_Q4_K> {
     // 6-bit (scale, min) pairs of sub-blocks 2g, 2g+1 as two 16-bit byte
     // pairs (reference src/quant.c:72-80 unpacking, two at a time)
     static FO_DEV void scales(const uint4 &h, int g, uint32_t &scp, uint32_t &mp) {
+        // branch-free: both encodings are formed and selected, so the header
+        // stays in registers and no wait on later loads is forced here
         const int sh = 16 * (g & 1);
         const uint32_t A = (h.w >> sh) & 0xFFFFu;
         const uint32_t B = (h.y >> sh) & 0xFFFFu;
         const uint32_t C = (h.z >> sh) & 0xFFFFu;
-        if (g < 2) {
-            scp = B & 0x3F3Fu;
-            mp = C & 0x3F3Fu;
-        } else {
-            scp = (A & 0x0F0Fu) | ((B >> 2) & 0x3030u);
-            mp = ((A >> 4) & 0x0F0Fu) | ((C >> 2) & 0x3030u);
-        }
+        const uint32_t sc_lo = B & 0x3F3Fu, m_lo = C & 0x3F3Fu;
+        const uint32_t sc_hi = (A & 0x0F0Fu) | ((B >> 2) & 0x3030u);
+        const uint32_t m_hi = ((A >> 4) & 0x0F0Fu) | ((C >> 2) & 0x3030u);
+        scp = g < 2 ? sc_lo : sc_hi;
+        mp = g < 2 ? m_lo : m_hi;
     }
     static FO_DEV float finish(const uint4 &hdr, int g, float lo, float hi, const X &x) {
         uint32_t scp, mp;

@@ -31,94 +31,78 @@
 namespace fo {
 
 // ------------------------------------------------------------ wave primitives
-template <int CTRL>
-FO_DEV float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
-FO_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false); }
-
-// Maximum over the 64 lanes, returned in every lane: butterflies inside quads,
-// half-row and row mirrors (16-lane maxima), then the four row maxima.
-FO_DEV float wave_max_dpp(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));    // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
-    v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
-    v = fmaxf(v, dpp_f<0x140>(v));   // row_mirror
-    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
-FO_DEV int wave_min_dpp(int v) {
-    v = min(v, dpp_i<0xB1>(v));
-    v = min(v, dpp_i<0x4E>(v));
-    v = min(v, dpp_i<0x141>(v));
-    v = min(v, dpp_i<0x140>(v));
-    const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-    const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-    return min(min(a, b), min(c, d));
-}
-FO_DEV float wave_sum_dpp(float v) {
-    v += dpp_f<0xB1>(v);
-    v += dpp_f<0x4E>(v);
-    v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
-}
+FO_DEV float wave_sum_dpp(float v) { return group_sum<kWave>(v); }
 
 // Top-k of E logits (<= 1024) with ties to the lowest index — the order of
 // reference src/tensor.c:226-252 applied to softmax(logits), which is
 // monotone — and the renormalised weights exp(l_i - l_max) / sum over the
 // selection (= softmax then renormalise, reference src/inference.c:488-502).
-// Executed by one wave; results in ids[k], w[k].
+// One wave: k rounds of "largest (value, lowest index)" over its lanes; the
+// results go to LDS s_ids[k], s_w[k] (visible after the caller's barrier).
+// Each round costs ~500 cycles of dependent VALU/SGPR latency, so the whole
+// selection is ~2 us of single-wave latency; splitting it over four waves
+// measured slower (the merge round-trip through LDS costs more than it saves).
 constexpr int kMaxE = 1024, kMaxK = 16;
-FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *ids, float *w) {
-    constexpr int NV = kMaxE / 64;
+
+// One round of "take the largest (value, lowest index)" over the wave: lb/li
+// are this lane's best; returns the winner's value and index (uniform).
+FO_DEV void wave_argmax(float lb, int li, float &m, int &idx) {
+    float t = lb;
+    t = fmaxf(t, dpp<0xB1>(t));
+    t = fmaxf(t, dpp<0x4E>(t));
+    t = fmaxf(t, dpp<0x141>(t));
+    t = fmaxf(t, dpp<0x140>(t));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 48));
+    m = fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+    const uint64_t ball = __ballot(lb == m);
+    if (__popcll(ball) == 1) {
+        idx = __builtin_amdgcn_readlane(li, __ffsll((unsigned long long)ball) - 1);
+    } else {  // tie: lowest index among the lanes holding m
+        int c = lb == m ? li : 0x7FFFFFFF;
+        c = min(c, __builtin_amdgcn_update_dpp(c, c, 0xB1, 0xF, 0xF, false));
+        c = min(c, __builtin_amdgcn_update_dpp(c, c, 0x4E, 0xF, 0xF, false));
+        c = min(c, __builtin_amdgcn_update_dpp(c, c, 0x141, 0xF, 0xF, false));
+        c = min(c, __builtin_amdgcn_update_dpp(c, c, 0x140, 0xF, 0xF, false));
+        idx = min(min(__builtin_amdgcn_readlane(c, 0), __builtin_amdgcn_readlane(c, 16)),
+                  min(__builtin_amdgcn_readlane(c, 32), __builtin_amdgcn_readlane(c, 48)));
+    }
+}
+
+template <int NV>  // logits per lane: E <= 64*NV
+FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *s_ids, float *s_w) {
     const int lane = threadIdx.x & 63;
     float v[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
-        const int i = lane + 64 * j;
-        v[j] = (64 * j < E && i < E) ? logits[i] : -FLT_MAX;
+        const int i = 64 * j + lane;
+        v[j] = i < E ? logits[i] : -FLT_MAX;
     }
-    const int nv = (E + 63) / 64;
-    float sel_v[kMaxK];
-    int sel_i[kMaxK];
+    float my_v = -FLT_MAX;   // lane kk keeps selection kk (no indexed private arrays:
+    int my_i = 0;            // those would put the kernel on scratch, which throttles residency)
     for (int kk = 0; kk < k; kk++) {
-        float lb = -FLT_MAX;
+        float lb = v[0];
         int lj = 0;
 #pragma unroll
-        for (int j = 0; j < NV; j++)
-            if (j < nv && v[j] > lb) { lb = v[j]; lj = j; }
-        const float m = wave_max_dpp(lb);
-        const uint64_t ball = __ballot(lb == m);
+        for (int j = 1; j < NV; j++)
+            if (v[j] > lb) { lb = v[j]; lj = j; }
+        float m;
         int idx;
-        if (__popcll(ball) == 1) {
-            const int wl = __ffsll((unsigned long long)ball) - 1;
-            idx = 64 * __builtin_amdgcn_readlane(lj, wl) + wl;
-        } else {
-            idx = wave_min_dpp(lb == m ? 64 * lj + lane : 0x7FFFFFFF);
-        }
+        wave_argmax(lb, 64 * lj + lane, m, idx);
         if (idx < 0 || idx >= E) idx = 0;   // non-finite logits: never index outside the table
-        sel_v[kk] = m;
-        sel_i[kk] = idx;
+        if (lane == kk) { my_v = m; my_i = idx; }
         if (lane == (idx & 63)) {
 #pragma unroll
             for (int j = 0; j < NV; j++)
                 if (j == (idx >> 6)) v[j] = -FLT_MAX;
         }
     }
-    if (lane == 0) {
-        const float mx = sel_v[0];
-        float e[kMaxK], s = 0.f;
-        for (int kk = 0; kk < k; kk++) { e[kk] = expf(sel_v[kk] - mx); s += e[kk]; }
-        const float inv = 1.0f / s;
-        for (int kk = 0; kk < k; kk++) { ids[kk] = sel_i[kk]; w[kk] = e[kk] * inv; }
-    }
+    const float m0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(my_v)));
+    const float e = lane < k ? expf(my_v - m0) : 0.f;
+    const float inv = 1.0f / group_sum<kWave>(e);
+    if (lane < k) { s_ids[lane] = my_i; if (s_w) s_w[lane] = e * inv; }
 }
 
 // Prepare one group of G values held one per lane in lanes [0, G) of a wave
@@ -253,19 +237,29 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
 }
 
 // ============================================================ K2: expand
-// One work-group of 4 waves per task (expert slot e, block of TR rows, TR =
-// the activation-group size of the down projection); the grid is all tasks at
-// once (k=10 + shared, F=1024, TR=16: 704 WGs, all resident), and every wave
-// issues all its weight loads before any arithmetic, so the layer's whole
-// gate/up traffic is in flight together. Routed WGs first compute top-k (wave
+// One work-group of TR/RW waves per task (expert slot e, block of TR rows, TR
+// = the activation-group size of the down projection; RW rows per wave); the
+// grid is all tasks at once (k=10 + shared, F=1024, TR=16: 704 WGs of 4
+// waves, all resident), and every wave issues all its weight loads before any
+// arithmetic, so the layer's whole gate/up traffic is in flight together. Routed WGs first compute top-k (wave
 // 0) while the other waves stage the prepared h in LDS; the shared expert's
 // WGs skip the top-k. The TR results meet in LDS and wave 0 writes them in
 // prepared form for K3 (and as fp32 when a.act is set).
+// Rows per wave: 4 when a row's raw block is small (Q4_K, Q8_0), else 2, so
+// the weight registers of all rows stay resident without scratch.
+template <int T, int TR, int U>
+struct ExpandShape {
+    static constexpr int RW = (U == 1 && sizeof(typename Fmt<T>::Raw) <= 48) ? 4 : 2;
+    static constexpr int THREADS = TR / RW * 64;
+};
+
 template <int T, int TR, int G, int U>
-__global__ __launch_bounds__(256, 3) void k_expand(ExpandArgs a) {
+__global__ __launch_bounds__((ExpandShape<T, TR, U>::THREADS), 3) void k_expand(ExpandArgs a) {
     using F = Fmt<T>;
+    constexpr int RW = ExpandShape<T, TR, U>::RW;       // rows per wave
+    constexpr int NW = TR / RW;                         // waves
     constexpr int P = kWave / G;                        // rows side by side per pass
-    constexpr int PASS = (TR + 4 * P - 1) / (4 * P);    // passes per wave
+    constexpr int PASS = (RW + P - 1) / P;              // passes per wave
     extern __shared__ uint8_t lds[];                    // prepared h
     __shared__ int s_ids[kMaxK];
     __shared__ float s_w[kMaxK];
@@ -276,13 +270,17 @@ __global__ __launch_bounds__(256, 3) void k_expand(ExpandArgs a) {
     const int e = blockIdx.x / tpe, rb = blockIdx.x - e * tpe;
     const bool routed = e < a.k;
     const uint64_t xqb = xq_bytes(H, F::GSZ);
-    if (routed && wv == 0) {
-        wave_topk(a.logits, a.E, a.k, s_ids, s_w);
-        if (blockIdx.x == 0 && lane == 0)
-            for (int i = 0; i < a.k; i++) { a.ids[i] = s_ids[i]; a.weights[i] = s_w[i]; }
-    } else {
-        stage_lds(lds, a.xq_h, (uint32_t)xqb, routed ? wv - 1 : wv, routed ? 3 : 4);
+    // A routed WG of rank e needs only the first e+1 selections; the full
+    // top-k with weights (for K3) is computed once, by the first WG that has
+    // nothing else to wait for (the shared expert's first task, or WG 0).
+    const bool full = a.shared ? (e == a.k && rb == 0) : blockIdx.x == 0;
+    const int rounds = full ? a.k : (routed ? e + 1 : 0);
+    if (wv == 0 && rounds > 0) {
+        if (a.E <= 512) wave_topk<8>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
+        else wave_topk<16>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
+        if (full && lane < a.k) { a.ids[lane] = s_ids[lane]; a.weights[lane] = s_w[lane]; }
     }
+    stage_lds(lds, a.xq_h, (uint32_t)xqb, wv, NW);
     stage_lds_wait();
     const uint8_t *blob;
     uint64_t uo;
@@ -301,7 +299,7 @@ __global__ __launch_bounds__(256, 3) void k_expand(ExpandArgs a) {
     typename F::Raw rg[PASS][U], ru[PASS][U];
 #pragma unroll
     for (int p = 0; p < PASS; p++) {
-        const int rl = p * 4 * P + wv * P + sub;
+        const int rl = wv * RW + p * P + sub;
         const int row = rb * TR + min(rl, TR - 1);
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -326,8 +324,8 @@ __global__ __launch_bounds__(256, 3) void k_expand(ExpandArgs a) {
         }
         g = group_sum<G>(g);
         v = group_sum<G>(v);
-        const int rl = p * 4 * P + wv * P + sub;
-        if ((lane % G) == 0 && rl < TR) s_act[rl] = (g / (1.0f + expf(-g))) * v;
+        const int rl = wv * RW + p * P + sub;
+        if ((lane % G) == 0 && p * P + sub < RW) s_act[rl] = (g / (1.0f + expf(-g))) * v;
     }
     __syncthreads();
     if (wv == 0) {
@@ -354,7 +352,7 @@ hipError_t launch_expand(int type, const ExpandArgs &a, hipStream_t s, int n_cu)
     const size_t lds = lds_round(xq_bytes(a.H, type == GGML_TYPE_Q6_K ? 16 : 32));
     const int grid = a.F / TR * n_tot;
 #define FO_K2(TT, RR, GG, UU) \
-    if (type == TT && TR == RR && G == GG && U == UU) { k_expand<TT, RR, GG, UU><<<grid, 256, lds, s>>>(a); return hipGetLastError(); }
+    if (type == TT && TR == RR && G == GG && U == UU) { k_expand<TT, RR, GG, UU><<<grid, ExpandShape<TT, RR, UU>::THREADS, lds, s>>>(a); return hipGetLastError(); }
 #define FO_K2T(TT) \
     FO_K2(TT, 16, 64, 1) FO_K2(TT, 16, 64, 2) FO_K2(TT, 16, 32, 1) FO_K2(TT, 16, 16, 1) FO_K2(TT, 16, 8, 1) FO_K2(TT, 16, 4, 1) \
     FO_K2(TT, 32, 64, 1) FO_K2(TT, 32, 64, 2) FO_K2(TT, 32, 32, 1) FO_K2(TT, 32, 16, 1) FO_K2(TT, 32, 8, 1) FO_K2(TT, 32, 4, 1)
@@ -385,16 +383,17 @@ __global__ __launch_bounds__(1024) void k_reduce(ReduceArgs a) {
     if (wv < n_tot) {
         const uint8_t *m = (wv < a.k) ? a.base + (uint64_t)a.ids[wv] * a.stride + a.down_off
                                       : a.shared + a.sh_down_off;
+        // activation first: the first dot then waits only for it and row 0
+        typename F::X X;
+        int gi[F::NG];
+        F::groups(slot, gi);
+        load_xslot(X, a.xq_act + (uint64_t)wv * a.xq_vstride, a.F, gi);
         typename F::Raw raw[RP];
 #pragma unroll
         for (int p = 0; p < RP; p++) {
             const int row = min(row0 + p * P + sub, a.H - 1);
             raw[p] = F::load(m + (uint64_t)row * a.row_bytes, slot);
         }
-        typename F::X X;
-        int gi[F::NG];
-        F::groups(slot, gi);
-        load_xslot(X, a.xq_act + (uint64_t)wv * a.xq_vstride, a.F, gi);
 #pragma unroll
         for (int p = 0; p < RP; p++) {
             const float v = group_sum<G>(live * F::dot(raw[p], slot, X));
