@@ -58,7 +58,7 @@ def rotation(gpu, t, M, K, wseed, xseed, n_mats, steps, warmup):
     for _ in range(steps):
         gpu.matvec_batched(t, dW, stride, n_mats, dx, 0, dy, M, M, K)
     ms = gpu.timer_stop() / steps
-    bytes_per_mat = rb + 4 * K + 4 * M        # weights + x + y, each once
+    bytes_per_mat = rb + 4 * K + 4 * M        # weights + x + y, each counted once per launch
     total = bytes_per_mat * n_mats
     res = {"ms_per_step": ms, "bytes_per_step": total, "GB/s": total / ms / 1e6,
            "weight_bytes": rb * n_mats}

@@ -98,6 +98,10 @@ gpu_ctx_t *gpu_init(void) {
     c->n_cu = prop.multiProcessorCount;
     c->hbm = prop.totalGlobalMem;
     snprintf(c->arch, sizeof c->arch, "%s", prop.gcnArchName);
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {   // code objects are gfx950-only
+        delete c;
+        return nullptr;
+    }
     bool ok = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) == hipSuccess &&
               hipEventCreate(&c->ev0) == hipSuccess && hipEventCreate(&c->ev1) == hipSuccess &&
               hipMalloc((void **)&c->logits, 1024 * sizeof(float)) == hipSuccess &&

@@ -8,7 +8,7 @@
  *
  * Every function cites the reference file:line whose behaviour it restates.
  * The synthetic-data generator (fo_rng_*, fo_synth_*, fo_quantize_*) has no
- * reference counterpart: the reference ships no quantizer (SURVEY: its only
+ * reference counterpart: the reference ships no quantizer (its only
  * quantizer is quantize_row_q8_K). It is this build's own definition and the
  * GPU generator must reproduce it bit for bit.
  */
