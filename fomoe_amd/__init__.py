@@ -45,6 +45,9 @@ SIGNATURES = {
     "gpu_router_topk": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, C.c_int, C.c_int, C.c_int,
                                   _vp, _vp]),
     "gpu_moe_stack_decode": (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int]),
+    "gpu_moe_prefill": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, C.c_int]),
+    "gpu_moe_prefill_routing": (C.c_int, [_vp, _vp, _vp]),
+    "gpu_f32_to_bf16": (C.c_int, [_vp, _vp, _vp, C.c_int64]),
     "gpu_synth_f32": (C.c_int, [_vp, C.c_uint64, C.c_uint64, C.c_float, _vp, C.c_int64]),
     "gpu_synth_quant": (C.c_int, [_vp, C.c_int, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float,
                                   C.c_int64, C.c_int64, C.c_int, _vp, C.c_uint64]),
@@ -145,6 +148,12 @@ class Gpu:
         self.check(self.lib.gpu_upload(self.ctx, buf.ptr, arr.ctypes.data, arr.nbytes), "gpu_upload")
         return buf
 
+    def upload_to(self, dst, arr: np.ndarray):
+        """Copy a host array into an existing device buffer (sync)."""
+        arr = np.ascontiguousarray(arr)
+        p = dst.ptr if isinstance(dst, DeviceBuffer) else dst
+        self.check(self.lib.gpu_upload(self.ctx, p, arr.ctypes.data, arr.nbytes), "gpu_upload")
+
     def download(self, ptr, dtype, count: int) -> np.ndarray:
         out = np.empty(count, dtype)
         p = ptr.ptr if isinstance(ptr, DeviceBuffer) else ptr
@@ -189,6 +198,20 @@ class Gpu:
         arr = (MoeLayer * len(layers))(*layers)
         self.check(self.lib.gpu_moe_stack_decode(self.ctx, arr, len(layers), _p(x), n_steps),
                    "gpu_moe_stack_decode")
+
+    def moe_prefill(self, layer: MoeLayer, x_bf16, n_tokens: int, out, flags: int = 0):
+        self.check(self.lib.gpu_moe_prefill(self.ctx, C.byref(layer), _p(x_bf16), n_tokens, _p(out),
+                                            flags), "gpu_moe_prefill")
+
+    def prefill_routing(self, n_tokens: int, k: int):
+        ids = np.empty((n_tokens, k), np.int32)
+        w = np.empty((n_tokens, k + 1), np.float32)
+        self.check(self.lib.gpu_moe_prefill_routing(self.ctx, ids.ctypes.data, w.ctypes.data),
+                   "gpu_moe_prefill_routing")
+        return ids, w
+
+    def f32_to_bf16(self, src, dst, n: int):
+        self.check(self.lib.gpu_f32_to_bf16(self.ctx, _p(src), _p(dst), n), "gpu_f32_to_bf16")
 
     def expert_ffn(self, h: np.ndarray, blobs, scores: np.ndarray, H: int, F: int, gate_size: int,
                    up_size: int, stride: int, gt: int, ut: int, dt: int):

@@ -16,6 +16,7 @@
 #include "gpu.h"
 #include "kernels.h"
 #include "moe.h"
+#include "prefill.h"
 
 using namespace fo;
 
@@ -42,6 +43,18 @@ struct gpu_ctx {
     uint8_t *staging = nullptr;    size_t staging_cap = 0;
     int last_k = 0;
     bool last_fast = false;      // routing of the last layer came from the K1-K3 path
+
+    // prefill workspace (grown on demand)
+    float *pf_logits = nullptr;    size_t pf_logits_cap = 0;
+    int32_t *pf_ids = nullptr;     size_t pf_ids_cap = 0;
+    float *pf_w = nullptr;         size_t pf_w_cap = 0;
+    int32_t *pf_pairpos = nullptr; size_t pf_pairpos_cap = 0;
+    int32_t *pf_pairtok = nullptr; size_t pf_pairtok_cap = 0;
+    int32_t *pf_tiles = nullptr;   size_t pf_tiles_cap = 0;
+    int32_t *pf_ntiles = nullptr;  size_t pf_ntiles_cap = 0;
+    float *pf_act = nullptr;       size_t pf_act_cap = 0;
+    float *pf_outp = nullptr;      size_t pf_outp_cap = 0;
+    int pf_T = 0, pf_k = 0;
 
     // captured stack-decode graph
     hipGraphExec_t graph_exec = nullptr;
@@ -123,7 +136,9 @@ void gpu_free(gpu_ctx_t *c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
     void *bufs[] = {c->logits, c->counter, c->ids, c->weights, c->xq_h, c->xq_act, c->act,
-                    c->act2, c->vec_in, c->vec_out, c->staging};
+                    c->act2, c->vec_in, c->vec_out, c->staging, c->pf_logits, c->pf_ids,
+                    c->pf_w, c->pf_pairpos, c->pf_pairtok, c->pf_tiles, c->pf_ntiles,
+                    c->pf_act, c->pf_outp};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (c->ev0) (void)hipEventDestroy(c->ev0);
@@ -485,6 +500,66 @@ void gpu_synth_zipf_bias(uint64_t seed, uint64_t stream, int n, double s, float 
         std::swap(perm[(size_t)i], perm[(size_t)j]);
     }
     for (int r = 0; r < n; r++) bias[perm[(size_t)r]] = (float)(-s * log((double)(r + 1)));
+}
+
+
+// ------------------------------------------------------------------ prefill
+int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_x, int n_tokens,
+                    float *d_out, int flags) {
+    if (!ctx) return -1;
+    if (int rc = check_layer(ctx, L)) return rc;
+    if (!d_x || !d_out || n_tokens <= 0) return fail(ctx, -1, "moe prefill: null buffer or n_tokens %d", n_tokens);
+    if (flags & ~GPU_MOE_RESIDUAL) return fail(ctx, -1, "moe prefill: flags %d (only GPU_MOE_RESIDUAL)", flags);
+    const bool pt = (L->gate_type == GGML_TYPE_Q4_K || L->gate_type == GGML_TYPE_Q6_K) &&
+                    (L->down_type == GGML_TYPE_Q4_K || L->down_type == GGML_TYPE_Q6_K);
+    if (!pt) return fail(ctx, -1, "moe prefill: gate/up/down types must be Q4_K or Q6_K");
+    const int T = n_tokens, E = L->n_experts, k = L->k, H = L->n_embd, F = L->inter;
+    if (E > 1023 || E * ((T + 31) / 32) > 16384)
+        return fail(ctx, -1, "moe prefill: n_experts %d x n_tokens %d exceeds the grouping table", E, T);
+    const bool sh = L->shared != nullptr;
+    const size_t P = (size_t)fo::prefill_pairs(T, k, sh);
+    const int max_tiles = fo::prefill_max_tiles(T, k, E, sh);
+    HIPC(ensure(ctx->pf_logits, ctx->pf_logits_cap, sizeof(float) * (size_t)T * E));
+    HIPC(ensure(ctx->pf_ids, ctx->pf_ids_cap, sizeof(int32_t) * (size_t)T * k));
+    HIPC(ensure(ctx->pf_w, ctx->pf_w_cap, sizeof(float) * (size_t)T * (k + 1)));
+    HIPC(ensure(ctx->pf_pairpos, ctx->pf_pairpos_cap, sizeof(int32_t) * (size_t)T * (k + 1)));
+    HIPC(ensure(ctx->pf_pairtok, ctx->pf_pairtok_cap, sizeof(int32_t) * P));
+    HIPC(ensure(ctx->pf_tiles, ctx->pf_tiles_cap, sizeof(int32_t) * 4 * (size_t)max_tiles));
+    HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
+    HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, sizeof(float) * P * F));
+    HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
+    fo::PrefillArgs a{};
+    a.E = E; a.k = k; a.H = H; a.F = F;
+    a.gate_type = L->gate_type; a.up_type = L->up_type; a.down_type = L->down_type;
+    a.router = L->router; a.router_bias = L->router_bias;
+    a.experts = (const uint8_t *)L->experts; a.stride = L->expert_stride;
+    a.gate_size = L->gate_size; a.up_size = L->up_size;
+    a.shared = (const uint8_t *)L->shared; a.sh_gate_size = L->shared_gate_size; a.sh_up_size = L->shared_up_size;
+    a.shared_gate_vec = L->shared_gate_vec;
+    a.T = T; a.x = d_x; a.out = d_out; a.residual = (flags & GPU_MOE_RESIDUAL) ? 1 : 0;
+    a.logits = ctx->pf_logits; a.ids = ctx->pf_ids; a.w = ctx->pf_w; a.pairpos = ctx->pf_pairpos;
+    a.pair_tok = ctx->pf_pairtok; a.tiles = ctx->pf_tiles; a.n_tiles = ctx->pf_ntiles;
+    a.max_tiles = max_tiles; a.act = ctx->pf_act; a.outp = ctx->pf_outp;
+    HIPC(fo::launch_prefill(a, ctx->stream));
+    ctx->pf_T = T;
+    ctx->pf_k = k;
+    return 0;
+}
+
+int gpu_moe_prefill_routing(gpu_ctx_t *ctx, int32_t *ids, float *weights) {
+    if (!ctx) return -1;
+    if (ctx->pf_T <= 0) return fail(ctx, -1, "moe prefill routing: no prefill has run");
+    HIPC(hipStreamSynchronize(ctx->stream));
+    if (ids) HIPC(hipMemcpy(ids, ctx->pf_ids, sizeof(int32_t) * (size_t)ctx->pf_T * ctx->pf_k, hipMemcpyDeviceToHost));
+    if (weights)
+        HIPC(hipMemcpy(weights, ctx->pf_w, sizeof(float) * (size_t)ctx->pf_T * (ctx->pf_k + 1), hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int gpu_f32_to_bf16(gpu_ctx_t *ctx, const float *d_src, uint16_t *d_dst, int64_t n) {
+    if (!ctx || !d_src || !d_dst || n <= 0) return fail(ctx, -1, "f32_to_bf16: bad arguments");
+    HIPC(fo::launch_f32_to_bf16(d_src, d_dst, n, ctx->stream));
+    return 0;
 }
 
 }  // extern "C"

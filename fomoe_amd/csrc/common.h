@@ -56,7 +56,7 @@ FO_DEV void stage_lds(uint8_t *lds_dst, const uint8_t *g, uint32_t nbytes, int w
     const int lane = threadIdx.x & 63;
     for (uint32_t off = (uint32_t)wave * 1024u; off < nbytes; off += (uint32_t)nwaves * 1024u) {
         const uint32_t o = off + (uint32_t)lane * 16u;
-        const uint8_t *src = g + (o < nbytes ? o : nbytes - 16u);
+        const uint8_t *src = g + (o + 16u <= nbytes ? o : nbytes - 16u);
         __builtin_amdgcn_global_load_lds((const void *)src,
                                          (__attribute__((address_space(3))) void *)(lds_dst + off), 16, 0, 0);
     }

@@ -1,0 +1,52 @@
+// prefill.h — argument block and launchers of the multi-token (prefill) MoE
+// path: fp32 router GEMM, per-token top-k, deterministic grouping of
+// (token, expert) pairs by expert, grouped gate/up and down GEMMs on bf16
+// MFMA with the weights dequantized in registers, and the per-token combine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fo {
+
+constexpr int kPfMT = 64;        // tokens per GEMM tile (4 MFMA row blocks of 16)
+constexpr int kPfNT = 64;        // weight rows per GEMM tile (4 waves x 16)
+
+struct PrefillArgs {
+    // layer
+    int E, k, H, F;
+    int gate_type, up_type, down_type;
+    const float *router, *router_bias;
+    const uint8_t *experts;      // E blobs gate|up|down, stride apart
+    uint64_t stride, gate_size, up_size;
+    const uint8_t *shared;       // shared blob or NULL
+    uint64_t sh_gate_size, sh_up_size;
+    const float *shared_gate_vec;  // [H] or NULL
+    // tokens
+    int T;
+    const uint16_t *x;           // [T x H] bf16
+    float *out;                  // [T x H] fp32
+    int residual;                // out = x + ffn
+    // workspace (device)
+    float *logits;               // [T x E]
+    int32_t *ids;                // [T x k]
+    float *w;                    // [T x (k+1)]: renormalised weights, then the shared weight
+    int32_t *pairpos;            // [T x (k+1)]: pair slot of (token, rank); rank k = shared
+    int32_t *pair_tok;           // [P] token of each pair slot, grouped by expert
+    int32_t *tiles;              // [max_tiles x 4] {expert (E = shared), first pair, n, 0}
+    int32_t *n_tiles;            // [1]
+    int max_tiles;
+    float *act;                  // [P x F] fp32 SwiGLU activation
+    float *outp;                 // [P x H] fp32, per-pair down output
+};
+
+// Number of pair slots and an upper bound on the GEMM tiles for T tokens.
+inline int prefill_pairs(int T, int k, bool shared) { return T * (k + (shared ? 1 : 0)); }
+inline int prefill_max_tiles(int T, int k, int E, bool shared) {
+    return (prefill_pairs(T, k, shared) + kPfMT - 1) / kPfMT + E + (shared ? 1 : 0);
+}
+
+hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s);
+hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStream_t s);
+
+}  // namespace fo

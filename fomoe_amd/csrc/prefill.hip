@@ -1,0 +1,463 @@
+// prefill.hip — the multi-token MoE path (512 tokens,
+// top-10 of 512 experts, Q4_K gate/up and Q6_K down).
+//
+//   P1 k_pf_router   logits[T x E] = x . W_r^T (+ bias), fp32 (x is bf16,
+//                    converted exactly), LDS-tiled 32 x 32 outputs per WG.
+//   P2 k_pf_topk     one wave per token: top-k with lowest-index ties and the
+//                    renormalised weights (topk.h), the shared-expert weight
+//                    sigmoid(x . v) or 1.
+//   P3 k_pf_group    one work-group: (token, rank) pairs grouped by expert in
+//                    token order (a per-expert token bitmap in LDS and popcount
+//                    prefixes — deterministic, no global atomics), the shared
+//                    expert's T pairs after them, and the GEMM tile list
+//                    {expert, first pair, n <= 64}.
+//   P4 k_pf_gateup   per (tile, 64 rows of F): act = silu(X Wg^T) * (X Wu^T)
+//                    with X the tile's gathered bf16 token rows (staged in LDS
+//                    one 256-value super-block at a time) and the weights
+//                    dequantized in registers straight into the MFMA B operand
+//                    (bf16, round-to-nearest-even of the exact fp32 value);
+//                    v_mfma_f32_16x16x32_bf16, fp32 accumulate; act stored fp32.
+//   P5 k_pf_down     per (tile, 64 rows of H): outp = act Wd^T, same scheme,
+//                    with act fed as two bf16 terms hi = bf16(act), lo =
+//                    bf16(act - hi) (|act - hi - lo| <= 2^-18 |act|) and two
+//                    MFMAs per weight operand, so the intermediate keeps ~fp32
+//                    precision and no result hinges on which side of a bf16
+//                    rounding boundary an fp32 sum landed.
+//   P6 k_pf_combine  out[t] = (x[t]) + sum_r w[t,r] outp[pair(t,r)] in rank
+//                    order, then the shared expert's pair.
+//
+// Per-token semantics are those of the batch-1 layer (reference
+// src/inference.c:481-606); the reference has no prefill GEMM (its prompt
+// tokens go one by one through the decode path), so this path is pinned by
+// the oracle's per-token composition with bf16-rounded weights and activations
+// (oracle/oracle.c fo_moe_prefill: bf16 weights, fp32 activation).
+#include <float.h>
+
+#include "common.h"
+#include "prefill.h"
+#include "topk.h"
+
+namespace fo {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+FO_DEV float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
+FO_DEV uint32_t pack_bf16(float lo, float hi) {   // round to nearest even, lo in bits 0..15
+    const __bf16 a = (__bf16)lo, b = (__bf16)hi;
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// ============================================================ P1 router GEMM
+constexpr int kRT = 32, kRK = 64;   // 32 tokens x 32 experts per WG, K chunks of 64
+
+__global__ __launch_bounds__(256) void k_pf_router(PrefillArgs a) {
+    __shared__ float xs[kRK][kRT + 1];
+    __shared__ float rs[kRK][kRT + 1];
+    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+    const int t0 = blockIdx.y * kRT, e0 = blockIdx.x * kRT;
+    const int lt = tid >> 3, lk = (tid & 7) * 8;          // loader: row lt, 8 values at lk
+    const int tl = min(t0 + lt, a.T - 1), el = min(e0 + lt, a.E - 1);
+    const uint16_t *xp = a.x + (uint64_t)tl * a.H + lk;
+    const float *rp = a.router + (uint64_t)el * a.H + lk;
+    float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    for (int k0 = 0; k0 < a.H; k0 += kRK) {
+        const uint4 xv = *(const uint4 *)(xp + k0);
+        const float4 r0 = *(const float4 *)(rp + k0), r1 = *(const float4 *)(rp + k0 + 4);
+        __syncthreads();
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            xs[lk + 2 * i][lt] = bf2f(xw[i] & 0xFFFFu);
+            xs[lk + 2 * i + 1][lt] = bf2f(xw[i] >> 16);
+        }
+        rs[lk + 0][lt] = r0.x; rs[lk + 1][lt] = r0.y; rs[lk + 2][lt] = r0.z; rs[lk + 3][lt] = r0.w;
+        rs[lk + 4][lt] = r1.x; rs[lk + 5][lt] = r1.y; rs[lk + 6][lt] = r1.z; rs[lk + 7][lt] = r1.w;
+        __syncthreads();
+#pragma unroll 8
+        for (int k = 0; k < kRK; k++) {
+            const float x0 = xs[k][2 * ty], x1 = xs[k][2 * ty + 1];
+            const float w0 = rs[k][2 * tx], w1 = rs[k][2 * tx + 1];
+            acc[0][0] = fmaf(x0, w0, acc[0][0]); acc[0][1] = fmaf(x0, w1, acc[0][1]);
+            acc[1][0] = fmaf(x1, w0, acc[1][0]); acc[1][1] = fmaf(x1, w1, acc[1][1]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int t = t0 + 2 * ty + i, e = e0 + 2 * tx + j;
+            if (t < a.T && e < a.E) a.logits[(uint64_t)t * a.E + e] = acc[i][j] + (a.router_bias ? a.router_bias[e] : 0.f);
+        }
+}
+
+// ============================================================ P2 top-k
+__global__ __launch_bounds__(256) void k_pf_topk(PrefillArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= a.T) return;
+    const int K1 = a.k + 1;
+    if (a.E <= 512) wave_topk<8>(a.logits + (uint64_t)t * a.E, a.E, a.k, a.ids + (uint64_t)t * a.k, a.w + (uint64_t)t * K1);
+    else wave_topk<16>(a.logits + (uint64_t)t * a.E, a.E, a.k, a.ids + (uint64_t)t * a.k, a.w + (uint64_t)t * K1);
+    float sw = 1.f;
+    if (a.shared_gate_vec) {
+        float d = 0.f;
+        const uint16_t *xp = a.x + (uint64_t)t * a.H;
+        for (int i = lane; i < a.H; i += 64) d = fmaf(bf2f(xp[i]), a.shared_gate_vec[i], d);
+        d = wave_sum(d);
+        sw = 1.0f / (1.0f + expf(-d));
+    }
+    if (lane == 0) a.w[(uint64_t)t * K1 + a.k] = sw;
+}
+
+// ============================================================ P3 grouping
+// LDS: per-expert token bitmap bm[e][W] and popcount prefixes pre[e][W],
+// W = ceil(T/32) words; counts and offsets over E+1 entries (entry E is the
+// shared expert, all T tokens).
+constexpr int kPfGroupLds = 16384;     // E*W words of each table
+
+FO_DEV int block_exclusive_scan(int v, int *buf) {   // 1024 threads, returns exclusive prefix
+    const int tid = threadIdx.x;
+    buf[tid] = v;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+        const int add = tid >= o ? buf[tid - o] : 0;
+        __syncthreads();
+        buf[tid] += add;
+        __syncthreads();
+    }
+    const int incl = buf[tid];
+    __syncthreads();
+    return incl - v;
+}
+
+__global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
+    extern __shared__ uint32_t lds[];
+    __shared__ int scan_buf[1024];
+    const int tid = threadIdx.x;
+    const int W = (a.T + 31) / 32, E = a.E, k = a.k, K1 = k + 1;
+    uint32_t *bm = lds, *pre = lds + E * W;
+    for (int i = tid; i < E * W; i += 1024) bm[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < a.T * k; i += 1024) {
+        const int t = i / k, e = a.ids[i];
+        atomicOr(&bm[e * W + (t >> 5)], 1u << (t & 31));
+    }
+    __syncthreads();
+    const bool sh = a.shared != nullptr;
+    int cnt = 0;
+    if (tid < E) {
+        for (int w = 0; w < W; w++) { pre[tid * W + w] = cnt; cnt += __popc(bm[tid * W + w]); }
+    } else if (tid == E && sh) {
+        cnt = a.T;
+    }
+    const int off = block_exclusive_scan(cnt, scan_buf);   // pair offset of expert tid
+    const int nt = (cnt + kPfMT - 1) / kPfMT;
+    const int toff = block_exclusive_scan(nt, scan_buf);   // first tile of expert tid
+    if (tid <= E) {
+        for (int i = 0; i < nt; i++) {
+            int32_t *tp = a.tiles + 4 * (toff + i);
+            tp[0] = tid; tp[1] = off + kPfMT * i; tp[2] = min(kPfMT, cnt - kPfMT * i); tp[3] = 0;
+        }
+    }
+    if (tid == 1023) *a.n_tiles = toff + nt;
+    // pair offsets of each expert for the placement pass
+    __shared__ int s_off[1025];
+    if (tid <= E) s_off[tid] = off;
+    __syncthreads();
+    for (int i = tid; i < a.T * k; i += 1024) {
+        const int t = i / k, r = i - t * k, e = a.ids[i];
+        const uint32_t word = bm[e * W + (t >> 5)];
+        const int pos = s_off[e] + (int)pre[e * W + (t >> 5)] + __popc(word & ((1u << (t & 31)) - 1u));
+        a.pair_tok[pos] = t;
+        a.pairpos[t * K1 + r] = pos;
+    }
+    if (sh)
+        for (int t = tid; t < a.T; t += 1024) {
+            const int pos = s_off[E] + t;
+            a.pair_tok[pos] = t;
+            a.pairpos[t * K1 + k] = pos;
+        }
+}
+
+// ============================================================ weight decode
+// Eight consecutive values k = 32*ch + 8*kg .. +7 of one row's super-block,
+// dequantized exactly in fp32 (as reference src/quant.c:82-105, 147-175) and
+// rounded to bf16, packed for the MFMA B operand.
+template <int T> struct PfDec;
+
+template <> struct PfDec<GGML_TYPE_Q4_K> {
+    static constexpr int BLOCK = 144;
+    struct Sb { uint4 hdr; uint2 q[4]; };
+    static FO_DEV Sb load(const uint8_t *sb, int kg) {
+        Sb s;
+        s.hdr = ld16(sb);
+#pragma unroll
+        for (int c = 0; c < 4; c++) s.q[c] = ld8(sb + 16 + 32 * c + 8 * kg);
+        return s;
+    }
+    // group j (0..7) = 32-value chunk ch: scale/min per reference src/quant.c:72-80
+    static FO_DEV u32x4 decode(const Sb &s, int ch) {
+        const uint32_t sc4[3] = {s.hdr.y, s.hdr.z, s.hdr.w};
+        const int j = ch;
+        auto byte = [&](int i) -> uint32_t { return (sc4[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
+        uint32_t sc, mn;
+        if (j < 4) { sc = byte(j) & 63; mn = byte(j + 4) & 63; }
+        else {
+            sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
+            mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+        }
+        const float d1 = h2f(s.hdr.x) * (float)sc, m1 = h2f(s.hdr.x >> 16) * (float)mn;
+        const uint2 q = s.q[ch >> 1];
+        const int sh = 4 * (ch & 1);
+        const uint32_t w0 = (q.x >> sh) & 0x0F0F0F0Fu, w1 = (q.y >> sh) & 0x0F0F0F0Fu;
+        u32x4 r;
+        r[0] = pack_bf16(fmaf(d1, ub0(w0), -m1), fmaf(d1, ub1(w0), -m1));
+        r[1] = pack_bf16(fmaf(d1, ub2(w0), -m1), fmaf(d1, ub3(w0), -m1));
+        r[2] = pack_bf16(fmaf(d1, ub0(w1), -m1), fmaf(d1, ub1(w1), -m1));
+        r[3] = pack_bf16(fmaf(d1, ub2(w1), -m1), fmaf(d1, ub3(w1), -m1));
+        return r;
+    }
+};
+
+template <> struct PfDec<GGML_TYPE_Q6_K> {
+    static constexpr int BLOCK = 210;
+    struct Sb { uint2 ql[4], qh[2]; uint4 sc; uint32_t d; };
+    static FO_DEV Sb load(const uint8_t *sb, int kg) {
+        Sb s;
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            s.ql[2 * n] = ld8(sb + 64 * n + 8 * kg);
+            s.ql[2 * n + 1] = ld8(sb + 64 * n + 32 + 8 * kg);
+            s.qh[n] = ld8(sb + 128 + 32 * n + 8 * kg);
+        }
+        s.sc = ld16(sb + 192);
+        s.d = ld2(sb + 208);
+        return s;
+    }
+    // chunk ch = 4n + t: values 128n + 32t + l, l = 8kg..8kg+7; scale sc[8n + 2t + kg/2]
+    static FO_DEV u32x4 decode(const Sb &s, int ch, int kg) {
+        const int n = ch >> 2, t = ch & 3;
+        const uint2 l = s.ql[2 * n + (t & 1)];
+        const uint2 h = s.qh[n];
+        const int ls = 4 * (t >> 1), hs = 2 * t;
+        const uint32_t c0 = ((l.x >> ls) & 0x0F0F0F0Fu) | (((h.x >> hs) & 0x03030303u) << 4);
+        const uint32_t c1 = ((l.y >> ls) & 0x0F0F0F0Fu) | (((h.y >> hs) & 0x03030303u) << 4);
+        const int si = 8 * n + 2 * t + (kg >> 1);
+        const uint32_t scw = si < 4 ? s.sc.x : si < 8 ? s.sc.y : si < 12 ? s.sc.z : s.sc.w;
+        const int scv = (int)(int8_t)((scw >> (8 * (si & 3))) & 0xFFu);
+        const float d1 = h2f(s.d) * (float)scv;
+        u32x4 r;
+        r[0] = pack_bf16(d1 * (ub0(c0) - 32.f), d1 * (ub1(c0) - 32.f));
+        r[1] = pack_bf16(d1 * (ub2(c0) - 32.f), d1 * (ub3(c0) - 32.f));
+        r[2] = pack_bf16(d1 * (ub0(c1) - 32.f), d1 * (ub1(c1) - 32.f));
+        r[3] = pack_bf16(d1 * (ub2(c1) - 32.f), d1 * (ub3(c1) - 32.f));
+        return r;
+    }
+};
+
+template <int T>
+FO_DEV u32x4 pf_decode(const typename PfDec<T>::Sb &s, int ch, int kg) {
+    if constexpr (T == GGML_TYPE_Q4_K) return PfDec<T>::decode(s, ch);
+    else return PfDec<T>::decode(s, ch, kg);
+}
+
+FO_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// ============================================================ P4/P5 grouped GEMMs
+// Work-group: 4 waves, tile of <= 64 pairs (token rows) x 64 weight rows; wave
+// w owns weight rows 16w..16w+15 (MFMA columns: lane % 16) for every token
+// block. The tile's activations for one 256-value super-block sit in LDS
+// (row stride 264 bf16: 16-byte aligned, rows spread over banks).
+constexpr int kPfXS = 264;
+
+// Stage rows src_row(m), m < n (else zeros), values [k0, k0+256) into xs.
+template <typename RowPtr>
+FO_DEV void pf_stage(uint16_t *xs, int n, int k0, RowPtr src_row) {
+    for (int i = threadIdx.x; i < kPfMT * 32; i += 256) {
+        const int m = i >> 5, c = i & 31;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (m < n) v = *(const uint4 *)(src_row(m) + k0 + 8 * c);
+        *(uint4 *)(xs + m * kPfXS + 8 * c) = v;
+    }
+}
+
+#pragma clang fp contract(off)
+template <int GT, int UT>
+__global__ __launch_bounds__(256) void k_pf_gateup(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[kPfMT * kPfXS];
+    if ((int)blockIdx.y >= *a.n_tiles) return;
+    const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
+    const int e = tl.x, p0 = tl.y, n = tl.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
+    const bool shared = e == a.E;
+    const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
+    const uint64_t up_off = shared ? a.sh_gate_size : a.gate_size;
+    const int row = blockIdx.x * kPfNT + 16 * wave + col;
+    const uint64_t gb = (uint64_t)(a.H / 256) * PfDec<GT>::BLOCK, ub = (uint64_t)(a.H / 256) * PfDec<UT>::BLOCK;
+    const uint8_t *grow = blob + (uint64_t)row * gb, *urow = blob + up_off + (uint64_t)row * ub;
+    const int nb = (n + 15) >> 4;
+    f32x4 ag[4], au[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) { ag[b] = (f32x4){0, 0, 0, 0}; au[b] = (f32x4){0, 0, 0, 0}; }
+    const int32_t *toks = a.pair_tok + p0;
+    for (int kb = 0; kb < a.H / 256; kb++) {
+        const auto sg = PfDec<GT>::load(grow + (uint64_t)kb * PfDec<GT>::BLOCK, kg);
+        const auto su = PfDec<UT>::load(urow + (uint64_t)kb * PfDec<UT>::BLOCK, kg);
+        __syncthreads();
+        pf_stage(xs, n, kb * 256, [&](int m) { return a.x + (uint64_t)toks[m] * a.H; });
+        __syncthreads();
+#pragma unroll
+        for (int ch = 0; ch < 8; ch++) {
+            const bf16x8 bg = as_bf16x8(pf_decode<GT>(sg, ch, kg));
+            const bf16x8 bu = as_bf16x8(pf_decode<UT>(su, ch, kg));
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (b < nb) {
+                    const bf16x8 av = *(const bf16x8 *)(xs + (16 * b + col) * kPfXS + 32 * ch + 8 * kg);
+                    ag[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bg, ag[b], 0, 0, 0);
+                    au[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bu, au[b], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // D layout: lane holds rows 4*(lane/16)+i (tokens) of column lane%16 (weight row)
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (b >= nb) break;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * b + 4 * kg + i;
+            if (m < n) {
+                const float g = ag[b][i], u = au[b][i];
+                const float v = (g / (1.0f + expf(-g))) * u;
+                a.act[(uint64_t)(p0 + m) * a.F + row] = v;
+            }
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_pf_down(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xh[kPfMT * kPfXS];
+    __shared__ __attribute__((aligned(16))) uint16_t xl[kPfMT * kPfXS];
+    if ((int)blockIdx.y >= *a.n_tiles) return;
+    const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
+    const int e = tl.x, p0 = tl.y, n = tl.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
+    const bool shared = e == a.E;
+    const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
+    const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
+    const int row = blockIdx.x * kPfNT + 16 * wave + col;
+    const uint64_t db = (uint64_t)(a.F / 256) * PfDec<DT>::BLOCK;
+    const uint8_t *drow = blob + down_off + (uint64_t)row * db;
+    const int nb = (n + 15) >> 4;
+    f32x4 acc[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) acc[b] = (f32x4){0, 0, 0, 0};
+    for (int kb = 0; kb < a.F / 256; kb++) {
+        const auto sd = PfDec<DT>::load(drow + (uint64_t)kb * PfDec<DT>::BLOCK, kg);
+        __syncthreads();
+        // stage act rows (fp32) as hi/lo bf16 pairs
+        for (int i = threadIdx.x; i < kPfMT * 64; i += 256) {
+            const int m = i >> 6, c = i & 63;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m < n) v = *(const float4 *)(a.act + (uint64_t)(p0 + m) * a.F + kb * 256 + 4 * c);
+            const uint32_t h0 = pack_bf16(v.x, v.y), h1 = pack_bf16(v.z, v.w);
+            const uint32_t l0 = pack_bf16(v.x - bf2f(h0 & 0xFFFFu), v.y - bf2f(h0 >> 16));
+            const uint32_t l1 = pack_bf16(v.z - bf2f(h1 & 0xFFFFu), v.w - bf2f(h1 >> 16));
+            *(uint2 *)(xh + m * kPfXS + 4 * c) = make_uint2(h0, h1);
+            *(uint2 *)(xl + m * kPfXS + 4 * c) = make_uint2(l0, l1);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ch = 0; ch < 8; ch++) {
+            const bf16x8 bd = as_bf16x8(pf_decode<DT>(sd, ch, kg));
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (b < nb) {
+                    const int o = (16 * b + col) * kPfXS + 32 * ch + 8 * kg;
+                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(xh + o), bd, acc[b], 0, 0, 0);
+                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(xl + o), bd, acc[b], 0, 0, 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (b >= nb) break;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * b + 4 * kg + i;
+            if (m < n) a.outp[(uint64_t)(p0 + m) * a.H + row] = acc[b][i];
+        }
+    }
+}
+#pragma clang fp contract(on)
+
+// ============================================================ P6 combine
+__global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
+    const int t = blockIdx.x, K1 = a.k + 1;
+    const int32_t *pp = a.pairpos + (uint64_t)t * K1;
+    const float *w = a.w + (uint64_t)t * K1;
+    for (int i = threadIdx.x; i < a.H; i += 256) {
+        float acc = 0.f;
+        for (int r = 0; r < a.k; r++) acc = acc + w[r] * a.outp[(uint64_t)pp[r] * a.H + i];
+        if (a.shared) acc = acc + a.outp[(uint64_t)pp[a.k] * a.H + i] * w[a.k];
+        const float x = a.residual ? bf2f(a.x[(uint64_t)t * a.H + i]) : 0.f;
+        a.out[(uint64_t)t * a.H + i] = a.residual ? x + acc : acc;
+    }
+}
+
+__global__ void k_f32_to_bf16(const float *src, uint16_t *dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = __builtin_bit_cast(uint16_t, (__bf16)src[i]);
+}
+
+hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipErrorInvalidValue;
+    k_f32_to_bf16<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(src, dst, n);
+    return hipGetLastError();
+}
+
+// ============================================================ launcher
+template <int GT, int UT>
+static hipError_t launch_gateup_t(const PrefillArgs &a, hipStream_t s) {
+    k_pf_gateup<GT, UT><<<dim3(a.F / kPfNT, a.max_tiles), 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
+    const bool okt = (a.gate_type == GGML_TYPE_Q4_K || a.gate_type == GGML_TYPE_Q6_K) &&
+                     (a.up_type == GGML_TYPE_Q4_K || a.up_type == GGML_TYPE_Q6_K) &&
+                     (a.down_type == GGML_TYPE_Q4_K || a.down_type == GGML_TYPE_Q6_K);
+    const int W = (a.T + 31) / 32;
+    if (!okt || a.T <= 0 || a.E <= 0 || a.E > 1023 || a.k <= 0 || a.k > a.E || a.k > kMaxK ||
+        a.H <= 0 || a.H % 256 || a.F <= 0 || a.F % 256 || a.E * W > kPfGroupLds ||
+        a.max_tiles < prefill_max_tiles(a.T, a.k, a.E, a.shared != nullptr))
+        return hipErrorInvalidValue;
+    k_pf_router<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 256, 0, s>>>(a);
+    k_pf_topk<<<(a.T + 3) / 4, 256, 0, s>>>(a);
+    static bool lds_attr = false;   // the grouping tables may exceed the 64 KiB default
+    if (!lds_attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_pf_group, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           2 * kPfGroupLds * (int)sizeof(uint32_t));
+        if (e != hipSuccess) return e;
+        lds_attr = true;
+    }
+    k_pf_group<<<1, 1024, 2 * (size_t)a.E * W * sizeof(uint32_t), s>>>(a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+#define FO_GU(G, U) if (a.gate_type == G && a.up_type == U) err = launch_gateup_t<G, U>(a, s);
+    FO_GU(GGML_TYPE_Q4_K, GGML_TYPE_Q4_K) FO_GU(GGML_TYPE_Q4_K, GGML_TYPE_Q6_K)
+    FO_GU(GGML_TYPE_Q6_K, GGML_TYPE_Q4_K) FO_GU(GGML_TYPE_Q6_K, GGML_TYPE_Q6_K)
+#undef FO_GU
+    if (err != hipSuccess) return err;
+    if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<dim3(a.H / kPfNT, a.max_tiles), 256, 0, s>>>(a);
+    else k_pf_down<GGML_TYPE_Q6_K><<<dim3(a.H / kPfNT, a.max_tiles), 256, 0, s>>>(a);
+    k_pf_combine<<<a.T, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace fo

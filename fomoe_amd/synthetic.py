@@ -3,7 +3,8 @@
 Stream numbering (this build's own definition; the reference has no
 synthetic data): stream(layer, expert, kind) = ((layer + 1) << 24) |
 (expert << 4) | kind, with expert == n_experts naming the shared expert and
-kind GATE 0, UP 1, DOWN 2, ROUTER 3, HIDDEN 5. Weights are N(0, 0.02) fp32
+kind GATE 0, UP 1, DOWN 2, ROUTER 3, HIDDEN 5, ZIPF 6 (router bias), TOKENS 7
+(prefill activations). Weights are N(0, 0.02) fp32
 quantized by this build's quantizers; activations N(0, 1). Every byte is
 generated on the device by libfomoe_gfx950 (bit-identical to oracle/'s CPU
 generator, which the tests use to check samples).
@@ -16,7 +17,7 @@ import numpy as np
 
 from . import Q4_K, Q6_K, Gpu, MoeLayer, row_bytes
 
-GATE, UP, DOWN, ROUTER, HIDDEN = 0, 1, 2, 3, 5
+GATE, UP, DOWN, ROUTER, HIDDEN, ZIPF, TOKENS = 0, 1, 2, 3, 5, 6, 7
 W_STD = 0.02
 
 
@@ -74,7 +75,7 @@ def build_layer(gpu: Gpu, shape: LayerShape, layer: int, seed: int = 4,
     bufs = [experts, router]
     bias = None
     if zipf_s is not None:
-        bias = gpu.upload(gpu.zipf_bias(seed, stream(layer, 0, 6), E, zipf_s))
+        bias = gpu.upload(gpu.zipf_bias(seed, stream(layer, 0, ZIPF), E, zipf_s))
         bufs.append(bias)
     norm_w = None
     if norm:
@@ -99,3 +100,16 @@ def hidden(gpu: Gpu, n_embd: int, seed: int = 4):
     buf = gpu.alloc(4 * n_embd)
     gpu.synth_f32(seed, stream(0, 0, HIDDEN), 1.0, buf, n_embd)
     return buf
+
+
+def tokens_bf16(gpu: Gpu, n_tokens: int, n_embd: int, seed: int = 4):
+    """Prefill activations X [n_tokens x n_embd] ~ N(0, 1), rounded to bf16
+    (config 5); returns the bf16 device buffer."""
+    n = n_tokens * n_embd
+    tmp = gpu.alloc(4 * n)
+    gpu.synth_f32(seed, stream(0, 0, TOKENS), 1.0, tmp, n)
+    x = gpu.alloc(2 * n)
+    gpu.f32_to_bf16(tmp, x, n)
+    gpu.sync()
+    tmp.free()
+    return x

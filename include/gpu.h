@@ -128,6 +128,25 @@ int gpu_router_topk(gpu_ctx_t *ctx, const float *d_router, const float *d_bias,
 int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_layers,
                          float *d_x, int n_steps);
 
+/* ---------------------------------------------------------------- prefill
+ * n_tokens tokens through one MoE layer at once (async): d_x [n_tokens x
+ * n_embd] bf16, d_out [n_tokens x n_embd] fp32 (= x + ffn with
+ * GPU_MOE_RESIDUAL). Per token the semantics of gpu_moe_layer without the
+ * norm (fp32 router on the bf16 input, softmax, top-k, renormalise, shared
+ * expert); the expert GEMMs are grouped by expert and run on bf16 MFMA with
+ * the weights dequantized in registers (round to nearest even of the exact
+ * fp32 value) and fp32 accumulation; the SwiGLU activation enters the down
+ * projection as two bf16 terms (hi + lo, within 2^-18 of the fp32 value). gate/up/down types Q4_K or Q6_K; n_experts <=
+ * 1023 and n_experts * ceil(n_tokens/32) <= 16384. No counterpart in the
+ * reference, which decodes prompt tokens one at a time (gpu_forward). */
+int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *layer, const uint16_t *d_x, int n_tokens,
+                    float *d_out, int flags);
+/* Routing of the last gpu_moe_prefill (sync): ids [n_tokens x k], weights
+ * [n_tokens x (k+1)] (the last per token is the shared-expert weight). */
+int gpu_moe_prefill_routing(gpu_ctx_t *ctx, int32_t *ids, float *weights);
+/* d_dst[i] = bf16(d_src[i]), round to nearest even (async). */
+int gpu_f32_to_bf16(gpu_ctx_t *ctx, const float *d_src, uint16_t *d_dst, int64_t n);
+
 /* ---------------------------------------------------------------- synthetic data
  * This build's own generator (no reference counterpart): counter-based
  * SplitMix64 normals and this build's quantizers; bit-identical to the CPU

@@ -67,6 +67,8 @@ def _load_oracle():
         "fo_cpu_expert_ffn": (None, [_vp, _vp, C.c_float, C.c_int, C.c_int, C.c_int, C.c_uint64,
                                      C.c_uint64, C.c_int, C.c_int, _vp]),
         "fo_moe_layer": (None, [C.POINTER(MoeDesc), _vp, _vp, C.c_int, _vp, _vp]),
+        "fo_moe_prefill": (None, [C.POINTER(MoeDesc), _vp, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp]),
+        "fo_fp32_to_bf16_n": (None, [_vp, _vp, C.c_int64]),
         "fo_rng_key": (C.c_uint64, [C.c_uint64, C.c_uint64]),
         "fo_rng_u64": (C.c_uint64, [C.c_uint64, C.c_uint64]),
         "fo_normal": (C.c_float, [C.c_uint64, C.c_uint64]),
@@ -173,6 +175,29 @@ def moe_layer(desc: MoeDesc, x: np.ndarray, flags: int):
     w = np.empty(desc.k, np.float32)
     lib.fo_moe_layer(C.byref(desc), _ptr(np.ascontiguousarray(x, np.float32)), _ptr(out), flags,
                      _ptr(ids), _ptr(w))
+    return out, ids, w
+
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even (the oracle's rounding)."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib.fo_fp32_to_bf16_n(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def moe_prefill(desc: MoeDesc, x_bf16: np.ndarray, t0: int, nt: int, flags: int = 0):
+    """Oracle prefill for tokens t0..t0+nt-1 of x_bf16 [T x H] (uint16 bits)."""
+    x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
+    H, k = desc.n_embd, desc.k
+    out = np.empty((nt, H), np.float32)
+    ids = np.empty((nt, k), np.int32)
+    w = np.empty((nt, k + 1), np.float32)
+    lib.fo_moe_prefill(C.byref(desc), _ptr(x_bf16), t0, nt, _ptr(out), flags, _ptr(ids), _ptr(w))
     return out, ids, w
 
 

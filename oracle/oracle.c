@@ -522,6 +522,105 @@ void fo_moe_layer(const fo_moe_desc *L, const float *in, float *out, int flags,
 }
 
 /* ------------------------------------------------------------------------
+ * bf16 and the prefill composition.
+ * ------------------------------------------------------------------------ */
+uint16_t fo_fp32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+float fo_bf16_to_fp32(uint16_t b) { return u2f((uint32_t)b << 16); }
+void fo_fp32_to_bf16_n(const float *x, uint16_t *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = fo_fp32_to_bf16(x[i]);
+}
+
+/* rows x cols matrix of `type` dequantized exactly, then rounded to bf16 */
+static float *deq_bf16(const uint8_t *w, int type, int rows, int cols) {
+    float *m = (float *)malloc(sizeof(float) * (size_t)rows * cols);
+    const uint64_t rb = fomoe_row_bytes(type, cols);
+#pragma omp parallel for if (rows > 64)
+    for (int r = 0; r < rows; r++) {
+        float *y = m + (size_t)r * cols;
+        fo_dequantize_row(type, w + (uint64_t)r * rb, y, cols);
+        for (int c = 0; c < cols; c++) y[c] = fo_bf16_to_fp32(fo_fp32_to_bf16(y[c]));
+    }
+    return m;
+}
+
+static void matvec_f64(float *out, const float *m, const float *v, int rows, int cols) {
+#pragma omp parallel for if (rows > 64)
+    for (int r = 0; r < rows; r++) {
+        double s = 0.0;
+        const float *row = m + (size_t)r * cols;
+        for (int c = 0; c < cols; c++) s += (double)row[c] * (double)v[c];
+        out[r] = (float)s;
+    }
+}
+
+static void expert_ffn_bf16(const uint8_t *blob, const fo_moe_desc *L, uint64_t gs, uint64_t us,
+                            const float *x, float *out) {
+    const int H = L->n_embd, F = L->inter;
+    float *g = (float *)malloc(sizeof(float) * (size_t)F * 2), *u = g + F;
+    float *wg = deq_bf16(blob, L->gate_type, F, H);
+    matvec_f64(g, wg, x, F, H);
+    free(wg);
+    float *wu = deq_bf16(blob + gs, L->up_type, F, H);
+    matvec_f64(u, wu, x, F, H);
+    free(wu);
+    for (int i = 0; i < F; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+    float *wd = deq_bf16(blob + gs + us, L->down_type, H, F);
+    matvec_f64(out, wd, g, H, F);
+    free(wd);
+    free(g);
+}
+
+void fo_moe_prefill(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
+                    int *ids_out, float *w_out) {
+    const int H = L->n_embd, E = L->n_experts, k = L->k;
+    float *h = (float *)malloc(sizeof(float) * (size_t)H * 3);
+    float *ffn = h + H, *dn = ffn + H;
+    float *logits = (float *)malloc(sizeof(float) * (size_t)E);
+    int ids[64];
+    float sc[64];
+    for (int t = t0; t < t0 + nt; t++) {
+        for (int j = 0; j < H; j++) h[j] = fo_bf16_to_fp32(x[(size_t)t * H + j]);
+        fo_mat_vec_mul(logits, L->router, GGML_TYPE_F32, h, E, H);
+        if (L->router_bias) for (int e = 0; e < E; e++) logits[e] += L->router_bias[e];
+        fo_softmax(logits, E);
+        fo_top_k(logits, E, k, ids, sc);
+        float ssum = 0.0f;
+        for (int i = 0; i < k; i++) ssum += sc[i];
+        if (ssum > 0.0f) { const float inv = 1.0f / ssum; for (int i = 0; i < k; i++) sc[i] *= inv; }
+        memset(ffn, 0, sizeof(float) * (size_t)H);
+        for (int i = 0; i < k; i++) {
+            expert_ffn_bf16(L->experts + (uint64_t)ids[i] * L->expert_stride, L, L->gate_size, L->up_size, h, dn);
+            for (int j = 0; j < H; j++) ffn[j] += sc[i] * dn[j];
+        }
+        float gsc = 1.0f;
+        if (L->shared) {
+            expert_ffn_bf16(L->shared, L, L->shared_gate_size, L->shared_up_size, h, dn);
+            if (L->shared_gate_vec) {
+                float dot = 0.0f;
+                for (int j = 0; j < H; j++) dot += h[j] * L->shared_gate_vec[j];
+                gsc = 1.0f / (1.0f + expf(-dot));
+                for (int j = 0; j < H; j++) dn[j] *= gsc;
+            }
+            for (int j = 0; j < H; j++) ffn[j] = ffn[j] + dn[j];
+        }
+        float *o = out + (size_t)(t - t0) * H;
+        for (int j = 0; j < H; j++) o[j] = (flags & FO_MOE_RESIDUAL) ? h[j] + ffn[j] : ffn[j];
+        if (ids_out) memcpy(ids_out + (size_t)(t - t0) * k, ids, sizeof(int) * (size_t)k);
+        if (w_out) {
+            memcpy(w_out + (size_t)(t - t0) * (k + 1), sc, sizeof(float) * (size_t)k);
+            w_out[(size_t)(t - t0) * (k + 1) + k] = gsc;
+        }
+    }
+    free(h);
+    free(logits);
+}
+
+/* ------------------------------------------------------------------------
  * Synthetic data. Counter-based SplitMix64 (Steele, Lea & Flood 2014): the
  * i-th output for state `key` is mix(key + (i+1)*golden). Normals come from
  * Box-Muller evaluated in float64 with +,-,* only (log, sin/cos, 1/x and

@@ -92,6 +92,22 @@ typedef struct {
 void fo_moe_layer(const fo_moe_desc *L, const float *in, float *out, int flags,
                   int *ids, float *weights);
 
+/* ---- bf16 (round to nearest even; NaN kept quiet) ---- */
+uint16_t fo_fp32_to_bf16(float f);
+float    fo_bf16_to_fp32(uint16_t b);
+void     fo_fp32_to_bf16_n(const float *x, uint16_t *y, int64_t n);
+
+/* ---- multi-token MoE layer (prefill) for tokens t0 .. t0+nt-1 of x [T x H]
+ * bf16. Per token the semantics of fo_moe_layer (no norm), with the expert
+ * weights rounded to bf16 after exact dequantization, dot products
+ * accumulated in double, and the SwiGLU activation kept in fp32 — the
+ * arithmetic contract of the bf16 grouped-GEMM prefill.
+ * The reference has no prefill GEMM; this composes reference
+ * src/inference.c:481-606 per token. out [nt x H]; ids [nt x k];
+ * w [nt x (k+1)] (last = shared weight). Only FO_MOE_RESIDUAL is honoured. */
+void fo_moe_prefill(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
+                    int *ids_out, float *w_out);
+
 /* ---- synthetic data (this build's own definition; no reference) ---- */
 uint64_t fo_rng_key(uint64_t seed, uint64_t stream);
 uint64_t fo_rng_u64(uint64_t key, uint64_t i);

@@ -371,3 +371,114 @@ def test_stack_decode_small_vs_oracle(gpu):
     e = parity_err(got, x)
     say(f"  parity_err {e:.3e}")
     assert e <= TOL
+
+
+# ------------------------------------------------------------------ prefill (config 5)
+def _prefill_host_layer(shape, layer, seed, zipf, gvec=None, experts_needed=None):
+    """Host copy of a synthetic layer for the oracle; experts_needed limits
+    which expert blobs are filled (the rest stay zero pages)."""
+    from fomoe_amd import synthetic as S
+    from test_oracle import moe_desc
+    E, H, F, k = shape.n_experts, shape.n_embd, shape.inter, shape.k
+    router = O.synth_f32(seed, S.stream(layer, 0, S.ROUTER), 0.02, E * H)
+    experts = np.zeros((E + 1) * shape.stride, np.uint8)
+    need = range(E + 1) if experts_needed is None else experts_needed
+    for e in need:
+        blob = np.concatenate([O.synth_quant(O.Q4_K, seed, S.stream(layer, e, S.GATE), 0.02, F, H),
+                               O.synth_quant(O.Q4_K, seed, S.stream(layer, e, S.UP), 0.02, F, H),
+                               O.synth_quant(O.Q6_K, seed, S.stream(layer, e, S.DOWN), 0.02, H, F)])
+        experts[e * shape.stride:e * shape.stride + blob.size] = blob
+    bias = O.zipf_bias(seed, S.stream(layer, 0, S.ZIPF), E, 1.1) if zipf else None
+    d = moe_desc(E, k, H, F, router, experts, shape.gate_size, shape.down_size,
+                 shared_off=E * shape.stride if shape.shared else None, bias=bias, gvec=gvec)
+    d.expert_stride = shape.stride
+    return d, (router, experts, bias, gvec)
+
+
+# Prefill bar. Weights are bf16 on both sides (bit-identical); the GPU feeds
+# the fp32 SwiGLU activation to the bf16 MFMA as hi + lo bf16 terms, which
+# carry it to within 2^-18 relative, so outputs differ from the oracle's
+# (fp32 activation, fp64 sums) by ~2^-18 of sum |w*a| per output: inf_rel
+# ~1e-6, i.e. parity_err (1e-3*||ref|| floor) up to ~1e-3. Bar: parity_err
+# <= 1e-2 and inf_rel <= 1e-5 (the decode path keeps the 1e-3 parity bar).
+PF_PARITY, PF_INF = 1e-2, 1e-5
+
+
+@pytest.mark.parametrize("T,shared,gate_vec,resid", [(200, True, True, True), (1, True, False, False),
+                                                      (33, False, False, True)])
+def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid):
+    """Grouped bf16-MFMA prefill against the oracle's per-token composition
+    (bf16-rounded weights and activations): every token, every output; with
+    the residual flag the output is exactly x + ffn."""
+    from fomoe_amd import synthetic as S
+    say(f"prefill small T={T} shared={shared} gate_vec={gate_vec} resid={resid}")
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=16, k=4, shared=shared)
+    L = S.build_layer(gpu, shape, 0, seed=21, zipf_s=1.1, norm=False)
+    gv = O.synth_f32(22, 0, 0.05, shape.n_embd) if gate_vec else None
+    if gate_vec:
+        dgv = gpu.upload(gv)
+        L.desc.shared_gate_vec = dgv.ptr
+    dx = S.tokens_bf16(gpu, T, shape.n_embd, seed=23)
+    dout = gpu.alloc(4 * T * shape.n_embd)
+    gpu.moe_prefill(L.desc, dx, T, dout, 0)
+    got = gpu.download(dout, np.float32, T * shape.n_embd).reshape(T, shape.n_embd)
+    ids, w = gpu.prefill_routing(T, shape.k)
+    x = O.to_bf16(O.synth_f32(23, S.stream(0, 0, S.TOKENS), 1.0, T * shape.n_embd)).reshape(T, -1)
+    assert np.array_equal(gpu.download(dx, np.uint16, T * shape.n_embd).reshape(T, -1), x)
+    if resid:
+        gpu.moe_prefill(L.desc, dx, T, dout, 2)
+        got_r = gpu.download(dout, np.float32, T * shape.n_embd).reshape(T, shape.n_embd)
+        assert np.array_equal(got_r, O.bf16_to_f32(x).reshape(T, -1) + got)
+    d, keep = _prefill_host_layer(shape, 0, 21, True, gv)
+    want, oids, ow = O.moe_prefill(d, x, 0, T, 0)
+    assert np.array_equal(ids, oids)
+    assert inf_rel(w[:, :shape.k], ow[:, :shape.k]) < 1e-5
+    if shared:
+        assert inf_rel(w[:, shape.k], ow[:, shape.k]) < 1e-5
+    e = max(parity_err(got[t], want[t]) for t in range(T))
+    say(f"  parity_err {e:.3e} inf_rel {inf_rel(got, want):.3e}")
+    assert e < PF_PARITY and inf_rel(got, want) < PF_INF
+
+
+def test_prefill_config5_sampled(gpu):
+    """Config 5 at full size (512 tokens, 512 experts, top-10, H 4096, F 1024,
+    Zipf(1.1) router bias): routing of every token against the oracle's fp32
+    router, outputs of sampled tokens against the oracle, and every sampled
+    token against the batch-1 decode layer on the same input (independent
+    GPU path, fp32 weights: agreement to the bf16 rounding scale)."""
+    from fomoe_amd import synthetic as S
+    say("prefill config5")
+    shape = S.LayerShape()
+    T, E, H, F, k = 512, shape.n_experts, shape.n_embd, shape.inter, shape.k
+    L = S.build_layer(gpu, shape, 0, seed=4, zipf_s=1.1, norm=False)
+    dx = S.tokens_bf16(gpu, T, H, seed=4)
+    dout = gpu.alloc(4 * T * H)
+    gpu.moe_prefill(L.desc, dx, T, dout, 0)
+    got = gpu.download(dout, np.float32, T * H).reshape(T, H)
+    ids, w = gpu.prefill_routing(T, k)
+    x = gpu.download(dx, np.uint16, T * H).reshape(T, H)
+    assert np.array_equal(x[:4], O.to_bf16(O.synth_f32(4, S.stream(0, 0, S.TOKENS), 1.0, 4 * H)).reshape(4, H))
+    router = O.synth_f32(4, S.stream(0, 0, S.ROUTER), 0.02, E * H)
+    bias = O.zipf_bias(4, S.stream(0, 0, S.ZIPF), E, 1.1)
+    xf = O.bf16_to_f32(x).reshape(T, H)
+    for t in range(T):
+        p = O.softmax(O.mat_vec(O.F32, router, xf[t], E, H) + bias)
+        oi, ov = O.top_k(p, k)
+        assert np.array_equal(ids[t], oi), t
+        assert inf_rel(w[t, :k], ov / ov.sum()) < 1e-5
+    sample = [0, 257, 511]
+    need = sorted({int(v) for t in sample for v in ids[t]} | {E})
+    d, keep = _prefill_host_layer(shape, 0, 4, True, None, need)
+    dh = gpu.alloc(4 * H)
+    dl = gpu.alloc(4 * H)
+    for t in sample:
+        want, oids, _ = O.moe_prefill(d, x, t, 1, 0)
+        assert np.array_equal(oids[0], ids[t])
+        e = parity_err(got[t], want[0])
+        gpu.upload_to(dh, xf[t])
+        gpu.moe_layer(L.desc, dh, dl, 0)
+        dec = gpu.download(dl, np.float32, H)
+        say(f"  token {t}: parity_err {e:.3e} inf_rel {inf_rel(got[t], want[0]):.3e}  "
+            f"vs decode inf_rel {inf_rel(got[t], dec):.3e}")
+        assert e < PF_PARITY and inf_rel(got[t], want[0]) < PF_INF
+        assert inf_rel(got[t], dec) < 2e-2

@@ -349,3 +349,73 @@ def test_zipf_bias_is_a_permuted_log_rank():
     r = np.sort(-b / 1.1)
     assert np.allclose(np.exp(r), np.arange(1, 513), rtol=1e-5)
     assert not np.array_equal(np.argsort(-b)[:10], np.arange(10))
+
+
+# ------------------------------------------------------------------ bf16 / prefill
+def test_bf16_rounding_vs_torch():
+    """fp32 -> bf16 round-to-nearest-even equals torch's conversion, including
+    exact halfway cases, subnormals, infinities and the largest finite values."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    half = (rng.integers(0, 1 << 16, 4096, dtype=np.uint64).astype(np.uint32) << 16) | 0x8000
+    x = np.concatenate([bits, half, np.array([0x7F7FFFFF, 0xFF7FFFFF, 0x00008000, 0x00018000,
+                                              0x7F800000, 0xFF800000], np.uint32)]).view(np.float32)
+    x = x[np.isfinite(x) | np.isinf(x)]
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.to_bf16(x), ref)
+
+
+def _prefill_inputs(seed, E, H, F, T):
+    router, _, experts, gs, ds = _moe_inputs(seed, E, H, F)
+    x = O.to_bf16(O.synth_f32(seed, 9, 1.0, T * H)).reshape(T, H)
+    return router, x, experts, gs, ds
+
+
+def test_prefill_oracle_fp64_recomposition():
+    """Prefill oracle = numpy recomposition: bf16-rounded exact dequantized
+    weights, fp64 dots, fp32 SwiGLU activation, rank-order combine."""
+    E, k, H, F, T = 8, 3, 256, 256, 5
+    router, x, experts, gs, ds = _prefill_inputs(41, E, H, F, T)
+    stride = 2 * gs + ds
+    gvec = O.synth_f32(42, 0, 0.05, H)
+    d = moe_desc(E, k, H, F, router, experts, gs, ds, shared_off=E * stride, gvec=gvec)
+    out, ids, w = O.moe_prefill(d, x, 1, 3, O.MOE_RESIDUAL)
+    bf = lambda a: O.bf16_to_f32(O.to_bf16(a)).astype(np.float64)  # noqa: E731
+
+    def ffn(off, xt):
+        e = experts[off:off + stride]
+        G = bf(O.dequantize(O.Q4_K, e[:gs], F * H)).reshape(F, H)
+        U = bf(O.dequantize(O.Q4_K, e[gs:2 * gs], F * H)).reshape(F, H)
+        D = bf(O.dequantize(O.Q6_K, e[2 * gs:], H * F)).reshape(H, F)
+        g, u = (G @ xt).astype(np.float32), (U @ xt).astype(np.float32)
+        a = ((g / (1 + np.exp(-g))) * u).astype(np.float64)
+        return D @ a
+
+    for i, t in enumerate(range(1, 4)):
+        xt = O.bf16_to_f32(x[t]).astype(np.float64)
+        logits = router.reshape(E, H).astype(np.float64) @ xt
+        p = np.exp(logits - logits.max())
+        p /= p.sum()
+        sel = np.lexsort((np.arange(E), -p))[:k]
+        assert np.array_equal(ids[i], sel)
+        wt = p[sel] / p[sel].sum()
+        assert inf_rel(w[i, :k], wt) < 1e-5
+        sg = 1 / (1 + np.exp(-(xt @ gvec.astype(np.float64))))
+        assert abs(w[i, k] - sg) < 1e-6
+        ref = sum(wt[j] * ffn(int(sel[j]) * stride, xt) for j in range(k)) + sg * ffn(E * stride, xt)
+        assert parity_err(out[i], xt + ref) < 1e-5
+
+
+def test_prefill_oracle_close_to_fp32_layer():
+    """bf16 weights/activations move the prefill output by ~1e-3 of its scale
+    from the fp32 decode oracle on the same (bf16) input; routing identical."""
+    E, k, H, F, T = 8, 3, 512, 256, 4
+    router, x, experts, gs, ds = _prefill_inputs(43, E, H, F, T)
+    d = moe_desc(E, k, H, F, router, experts, gs, ds, shared_off=E * (2 * gs + ds))
+    out, ids, w = O.moe_prefill(d, x, 0, T, 0)
+    for t in range(T):
+        ref, rids, rw = O.moe_layer(d, O.bf16_to_f32(x[t]), 0)
+        assert np.array_equal(ids[t], rids)
+        assert inf_rel(w[t, :k], rw) < 1e-6
+        assert inf_rel(out[t], ref) < 2e-2
