@@ -11,7 +11,9 @@ weights already resident in HBM.
 Also measured in the same run (reported under "extra"): the config-1 Q4_K
 rotation, the Q8_0 variant of config 2, one MoE layer (config 3) per call,
 and the 60-layer HBM-resident decode stack (config 4) replayed from a HIP
-graph, which gives the us-per-MoE-layer figure; plus the reference CPU path
+graph, which gives the us-per-MoE-layer figure; the config-5 prefill (512
+bf16 tokens through one Zipf-routed layer on grouped bf16-MFMA GEMMs); plus
+the reference CPU path
 (oracle/_ref, compiled from the reference's quant.c/cpu_expert.c) timed on
 this host on a bounded sample.
 
@@ -109,7 +111,7 @@ def cpu_baseline(gpu, dW, stride, M, K, t, seconds):
                       f"{n_s} of the rotation's matrices, {dt:.1f} s; CPU {cpu}"}
 
 
-def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls):
+def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0):
     shape = S.LayerShape()
     t0 = time.perf_counter()
     layers = []
@@ -144,7 +146,8 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls):
     layer_bytes = 4 * shape.n_experts * shape.n_embd + (shape.k + 1) * shape.expert_bytes()
     tok_s = stack_steps / (ms / 1e3)
     us_layer = ms * 1e3 / (stack_steps * n_layers)
-    return {
+    res = prefill_config5(gpu, layers[0], shape, prefill_reps) if prefill_reps > 0 else {}
+    return {**res,
         "config3_us_per_layer_call": round(us_layer_call, 2),
         "config4_layers": n_layers, "config4_steps": stack_steps,
         "config4_tok_per_s": round(tok_s, 2),
@@ -159,6 +162,31 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls):
     }
 
 
+def prefill_config5(gpu, layer, shape, reps):
+    """Config 5: 512 bf16 tokens through one Zipf-routed layer (grouped GEMMs)."""
+    T, H, F, E, k = 512, shape.n_embd, shape.inter, shape.n_experts, shape.k
+    x = S.tokens_bf16(gpu, T, H, seed=4)
+    out = gpu.alloc(4 * T * H)
+    for _ in range(2):
+        gpu.moe_prefill(layer.desc, x, T, out, 0)
+    gpu.sync()
+    gpu.timer_start()
+    for _ in range(reps):
+        gpu.moe_prefill(layer.desc, x, T, out, 0)
+    ms = gpu.timer_stop() / reps
+    ids, _ = gpu.prefill_routing(T, k)
+    n_unique = len(np.unique(ids)) + 1                      # + the shared expert
+    pairs = T * (k + 1)
+    flops = pairs * 6.0 * H * F + 2.0 * T * E * H
+    wbytes = n_unique * shape.expert_bytes() + 4 * E * H   # each touched weight byte once
+    return {"config5_ms": round(ms, 4), "config5_tok_per_s": round(T / (ms / 1e3), 1),
+            "config5_experts_touched": n_unique, "config5_weight_bytes": wbytes,
+            "config5_GB/s": round(wbytes / (ms * 1e6), 1),
+            "config5_frac_hbm": round(wbytes / (ms * 1e6) / HBM_PEAK_GBS, 4),
+            "config5_TFLOP/s": round(flops / (ms * 1e9), 2),
+            "config5_frac_mfma_bf16": round(flops / (ms * 1e9) / 2500.0, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,7 +196,8 @@ def main():
     ap.add_argument("--stack-steps", type=int, default=256)
     ap.add_argument("--layer-calls", type=int, default=600)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--skip", default="", help="comma list: q4k,q8_0,stack,cpu")
+    ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--skip", default="", help="comma list: q4k,q8_0,stack,cpu,prefill")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -200,8 +229,12 @@ def main():
         log(f"CPU baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['kind']})")
     if "stack" not in skip and args.stack_layers > 0:
         del keep6
-        extra.update(moe_layer_and_stack(gpu, args.stack_layers, args.stack_steps, args.layer_calls))
+        extra.update(moe_layer_and_stack(gpu, args.stack_layers, args.stack_steps, args.layer_calls,
+                                         0 if "prefill" in skip else args.prefill_reps))
         log(f"stack: {extra['config4_tok_per_s']} tok/s, {extra['config4_us_per_layer']} us/layer")
+        if "config5_ms" in extra:
+            log(f"prefill: {extra['config5_ms']} ms per 512 tokens, {extra['config5_TFLOP/s']} TFLOP/s, "
+                f"{extra['config5_GB/s']} GB/s")
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic_q6k_rotation.json")
     if os.path.exists(tf):
