@@ -52,7 +52,7 @@ struct gpu_ctx {
     int32_t *pf_pairtok = nullptr; size_t pf_pairtok_cap = 0;
     int32_t *pf_tiles = nullptr;   size_t pf_tiles_cap = 0;
     int32_t *pf_ntiles = nullptr;  size_t pf_ntiles_cap = 0;
-    float *pf_act = nullptr;       size_t pf_act_cap = 0;
+    uint16_t *pf_act = nullptr;    size_t pf_act_cap = 0;   // hi plane then lo plane
     float *pf_outp = nullptr;      size_t pf_outp_cap = 0;
     int pf_T = 0, pf_k = 0;
 
@@ -526,7 +526,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     HIPC(ensure(ctx->pf_pairtok, ctx->pf_pairtok_cap, sizeof(int32_t) * P));
     HIPC(ensure(ctx->pf_tiles, ctx->pf_tiles_cap, sizeof(int32_t) * 4 * (size_t)max_tiles));
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
-    HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, sizeof(float) * P * F));
+    HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * P * F));
     HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
     fo::PrefillArgs a{};
     a.E = E; a.k = k; a.H = H; a.F = F;
@@ -539,7 +539,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.T = T; a.x = d_x; a.out = d_out; a.residual = (flags & GPU_MOE_RESIDUAL) ? 1 : 0;
     a.logits = ctx->pf_logits; a.ids = ctx->pf_ids; a.w = ctx->pf_w; a.pairpos = ctx->pf_pairpos;
     a.pair_tok = ctx->pf_pairtok; a.tiles = ctx->pf_tiles; a.n_tiles = ctx->pf_ntiles;
-    a.max_tiles = max_tiles; a.act = ctx->pf_act; a.outp = ctx->pf_outp;
+    a.max_tiles = max_tiles; a.act_hi = ctx->pf_act; a.act_lo = ctx->pf_act + P * F; a.outp = ctx->pf_outp;
     HIPC(fo::launch_prefill(a, ctx->stream));
     ctx->pf_T = T;
     ctx->pf_k = k;

@@ -208,12 +208,146 @@ static hipError_t matvec_t(const MatvecArgs &a, hipStream_t s, int n_cu) {
     return hipErrorInvalidValue;
 }
 
+
+// ============================================================ Q6_K matvec, tile-staged MFMA
+// For Q6_K rows of K <= 1024 (the expert down-projection shape). One wave
+// per work-group streams a tile of 16 consecutive rows (16 * row_bytes
+// contiguous bytes) with 1 KiB coalesced loads, the next tile's loads in
+// flight while the current one is computed, writes it to its LDS area and
+// reads every lane's pieces back from there. The integer dots run on
+// v_mfma_i32_16x16x64_i8: B (weights) = lane (row = lane%16, lane group g)
+// with the 64 codes of slot (n = g>>1, j = g&1) for one t; A = the activation
+// limbs routed so that D lane (row, g) receives the three limb sums of its own
+// 16-value scale group, rows 4g..4g+2 of A being nonzero only over lane group
+// g's k-range (other lanes read a zeroed LDS region). D layout: lane holds
+// rows 4*(lane/16)+i of column lane%16. Group scales / offsets / sub-block
+// scales are then applied per lane as in Fmt<Q6_K>.
+typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr int kT6Rows = 16, kT6MaxNV = 14;   // 16 rows x 840 B <= 14 KiB
+
+template <int NSB, int TPW>
+__global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
+    constexpr int NV = (kT6Rows * NSB * 210 + 1023) / 1024;
+    constexpr int K = NSB * 256;
+    const int lane = threadIdx.x;
+    const int mat = blockIdx.y;
+    constexpr uint32_t limb_bytes = 3u * K, xbytes = limb_bytes + (K / 16) * 8;
+    constexpr uint32_t zoff = lds_round(xbytes);
+    uint8_t *tb = sx + zoff + lds_round(limb_bytes);
+    const uint8_t *Wm = a.W + mat * a.mat_stride;
+    const uint64_t rb = a.row_bytes;
+    const int tile0 = blockIdx.x * TPW;
+    const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
+    // A piece that straddles the end of a partial tile (16*rows*rb need not be a
+    // multiple of 16) is read from the last 16 valid bytes and written to that
+    // same LDS position (overlapping its neighbour with identical bytes).
+    auto tile_bytes = [&](int tile) { return (uint32_t)(min(kT6Rows, a.M - tile * kT6Rows) * rb); };
+    auto pos = [&](uint32_t o, uint32_t nb) { return o + 16 <= nb ? o : nb - 16; };
+    auto issue = [&](uint4 (&v)[NV], int tile) {
+        const uint32_t nb = tile_bytes(tile);
+        const uint8_t *tp = Wm + (uint64_t)tile * kT6Rows * rb;
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = ld16(tp + pos(i * 1024 + lane * 16, nb));
+    };
+    uint4 va[NV], vb[NV];
+    if (tile0 < ntiles) issue(va, tile0);
+    stage_lds(sx, a.xq + mat * a.x_stride, (xbytes + 15) & ~15u, 0, 1);
+    for (uint32_t o = lane * 16; o < limb_bytes; o += 64 * 16) *(uint4 *)(sx + zoff + o) = make_uint4(0, 0, 0, 0);
+    stage_lds_wait();
+    const int r = lane & 15, g = lane >> 4, n = g >> 1, j = g & 1, L = r & 3;
+    const bool valid = (r >> 2) == g && L < 3;
+    const uint8_t *abase = sx + (valid ? 0u : zoff) + (8 * n + j) * 48 + 16 * L;
+    const uint8_t *ssb = sx + limb_bytes + (8 * n + j) * 8;
+    auto step = [&](uint4 (&v)[NV], int tt) {
+        const int tile = tile0 + tt;
+        {
+            const uint32_t nb = tile_bytes(tile);
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const uint32_t o = i * 1024 + lane * 16;
+                *(uint4 *)(tb + (o < nb ? pos(o, nb) : o)) = v[i];
+            }
+        }
+        if (tt + 2 < TPW && tile + 2 < ntiles) issue(v, tile + 2);
+        const uint8_t *rp = tb + r * rb;
+        float acc = 0.f;
+#pragma unroll
+        for (int b = 0; b < NSB; b++) {
+            const uint8_t *bp = rp + b * 210;
+            uint4 l0, l1, hh;
+            uint2 scb;
+            __builtin_memcpy(&l0, bp + 64 * n + 16 * j, 16);
+            __builtin_memcpy(&l1, bp + 64 * n + 32 + 16 * j, 16);
+            __builtin_memcpy(&hh, bp + 128 + 32 * n + 16 * j, 16);
+            __builtin_memcpy(&scb, bp + 192 + 8 * n, 8);
+            uint16_t d16;
+            __builtin_memcpy(&d16, bp + 208, 2);
+            const uint32_t Lo[4] = {l0.x, l0.y, l0.z, l0.w};
+            const uint32_t Hi[4] = {l1.x, l1.y, l1.z, l1.w};
+            const uint32_t H[4] = {hh.x, hh.y, hh.z, hh.w};
+            float accb = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                v4i B;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    uint32_t q;
+                    if (t == 0) q = (Lo[k] & 0x0F0F0F0Fu) | ((H[k] << 4) & 0x30303030u);
+                    else if (t == 1) q = (Hi[k] & 0x0F0F0F0Fu) | ((H[k] << 2) & 0x30303030u);
+                    else if (t == 2) q = ((Lo[k] >> 4) & 0x0F0F0F0Fu) | (H[k] & 0x30303030u);
+                    else q = ((Hi[k] >> 4) & 0x0F0F0F0Fu) | ((H[k] >> 2) & 0x30303030u);
+                    B[k] = (int)q;
+                }
+                const int go = 16 * b + 2 * t;                   // group 16b + 8n + 2t + j
+                const v4i A = *(const v4i *)(abase + go * 48);
+                const v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                const float f = fmaf(fmaf((float)D[2], 256.f, (float)D[1]), 256.f, (float)D[0]);
+                const float2 ss = *(const float2 *)(ssb + go * 8);
+                const float vv = fmaf(f, ss.x, -32.f * ss.y);
+                const uint32_t sw = (t < 2) ? scb.x : scb.y;       // sc[8n + 2t + j]
+                const int scv = (int)(sw << (24 - 8 * (2 * (t & 1) + j))) >> 24;
+                accb = fmaf((float)scv, vv, accb);
+            }
+            acc = fmaf(h2f(d16), accb, acc);
+        }
+        acc += __shfl_xor(acc, 16);
+        acc += __shfl_xor(acc, 32);
+        const int row = tile * kT6Rows + r;
+        if (g == 0 && row < a.M) a.y[mat * a.y_stride + row] = acc;
+    };
+    for (int tt = 0; tt < TPW; tt += 2) {
+        if (tile0 + tt >= ntiles) break;
+        if (tt + 1 < TPW && tile0 + tt + 1 < ntiles) issue(vb, tile0 + tt + 1);
+        step(va, tt);
+        if (tt + 1 >= TPW || tile0 + tt + 1 >= ntiles) break;
+        step(vb, tt + 1);
+    }
+}
+
+template <int NSB>
+static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
+    constexpr int TPW = 8, K = NSB * 256;
+    const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
+    const uint32_t lds = lds_round(xq_bytes(K, 16)) + lds_round(3u * K) +
+                         (uint32_t)((kT6Rows * NSB * 210 + 1023) / 1024) * 1024;
+    k_matvec_q6k_tile<NSB, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
+    return hipGetLastError();
+}
+
 hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu) {
     if (a.M <= 0 || a.n_mats <= 0) return hipErrorInvalidValue;
     switch (type) {
         case GGML_TYPE_Q4_K: return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q5_K: return matvec_t<GGML_TYPE_Q5_K, 2>(a, s, n_cu);
-        case GGML_TYPE_Q6_K: return matvec_t<GGML_TYPE_Q6_K, 2>(a, s, n_cu);
+        case GGML_TYPE_Q6_K:
+            if (a.row_bytes == (uint64_t)a.K / 256 * 210) {   // contiguous rows: tile-staged path
+                if (a.K == 1024) return matvec_q6k_tile<4>(a, s);
+                if (a.K == 768) return matvec_q6k_tile<3>(a, s);
+                if (a.K == 512) return matvec_q6k_tile<2>(a, s);
+                if (a.K == 256) return matvec_q6k_tile<1>(a, s);
+            }
+            return matvec_t<GGML_TYPE_Q6_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q8_0: return matvec_t<GGML_TYPE_Q8_0, 2>(a, s, n_cu);
         default: return hipErrorInvalidValue;
     }

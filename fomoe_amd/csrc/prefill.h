@@ -10,7 +10,8 @@
 namespace fo {
 
 constexpr int kPfMT = 64;        // tokens per GEMM tile (4 MFMA row blocks of 16)
-constexpr int kPfNT = 64;        // weight rows per GEMM tile (4 waves x 16)
+constexpr int kPfGateWaves = 16;                  // gate/up work-group: 8 gate + 8 up waves
+constexpr int kPfGateRows = 16 * kPfGateWaves / 2; // F rows per gate/up work-group
 
 struct PrefillArgs {
     // layer
@@ -36,7 +37,7 @@ struct PrefillArgs {
     int32_t *tiles;              // [max_tiles x 4] {expert (E = shared), first pair, n, 0}
     int32_t *n_tiles;            // [1]
     int max_tiles;
-    float *act;                  // [P x F] fp32 SwiGLU activation
+    uint16_t *act_hi, *act_lo;   // [P x F] SwiGLU activation as bf16 hi + lo terms
     float *outp;                 // [P x H] fp32, per-pair down output
 };
 

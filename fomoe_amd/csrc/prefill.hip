@@ -12,17 +12,19 @@
 //                    expert's T pairs after them, and the GEMM tile list
 //                    {expert, first pair, n <= 64}.
 //   P4 k_pf_gateup   per (tile, 64 rows of F): act = silu(X Wg^T) * (X Wu^T)
-//                    with X the tile's gathered bf16 token rows (staged in LDS
-//                    one 256-value super-block at a time) and the weights
+//                    with X the tile's gathered bf16 token rows and the weights
 //                    dequantized in registers straight into the MFMA B operand
 //                    (bf16, round-to-nearest-even of the exact fp32 value);
-//                    v_mfma_f32_16x16x32_bf16, fp32 accumulate; act stored fp32.
-//   P5 k_pf_down     per (tile, 64 rows of H): outp = act Wd^T, same scheme,
-//                    with act fed as two bf16 terms hi = bf16(act), lo =
-//                    bf16(act - hi) (|act - hi - lo| <= 2^-18 |act|) and two
-//                    MFMAs per weight operand, so the intermediate keeps ~fp32
-//                    precision and no result hinges on which side of a bf16
-//                    rounding boundary an fp32 sum landed.
+//                    v_mfma_f32_16x16x32_bf16, fp32 accumulate. The token rows
+//                    of super-block kb+1 stream into a second LDS buffer
+//                    (direct global->LDS loads) and its weights into registers
+//                    while super-block kb is multiplied. act is stored as two
+//                    bf16 planes hi = bf16(act), lo = bf16(act - hi)
+//                    (|act - hi - lo| <= 2^-18 |act|).
+//   P5 k_pf_down     per (tile, 128 rows of H): outp = act Wd^T, same scheme,
+//                    two MFMAs (hi, lo) per weight operand, so the intermediate
+//                    keeps ~fp32 precision and no result hinges on which side of
+//                    a bf16 rounding boundary an fp32 sum landed.
 //   P6 k_pf_combine  out[t] = (x[t]) + sum_r w[t,r] outp[pair(t,r)] in rank
 //                    order, then the shared expert's pair.
 //
@@ -188,7 +190,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
 template <int T> struct PfDec;
 
 template <> struct PfDec<GGML_TYPE_Q4_K> {
-    static constexpr int BLOCK = 144;
+    static constexpr int TYPE = GGML_TYPE_Q4_K, BLOCK = 144;
     struct Sb { uint4 hdr; uint2 q[4]; };
     static FO_DEV Sb load(const uint8_t *sb, int kg) {
         Sb s;
@@ -222,7 +224,7 @@ template <> struct PfDec<GGML_TYPE_Q4_K> {
 };
 
 template <> struct PfDec<GGML_TYPE_Q6_K> {
-    static constexpr int BLOCK = 210;
+    static constexpr int TYPE = GGML_TYPE_Q6_K, BLOCK = 210;
     struct Sb { uint2 ql[4], qh[2]; uint4 sc; uint32_t d; };
     static FO_DEV Sb load(const uint8_t *sb, int kg) {
         Sb s;
@@ -270,78 +272,119 @@ FO_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 // w owns weight rows 16w..16w+15 (MFMA columns: lane % 16) for every token
 // block. The tile's activations for one 256-value super-block sit in LDS
 // (row stride 264 bf16: 16-byte aligned, rows spread over banks).
-constexpr int kPfXS = 264;
 
-// Stage rows src_row(m), m < n (else zeros), values [k0, k0+256) into xs.
+// Activation tile in LDS: 64 token rows x 256 bf16 (32 chunks of 16 B), no
+// padding; chunk c of row m sits at slot c ^ (m & 15) so that the 16 rows an
+// MFMA A-operand read touches fall on 16 different 16-byte bank groups.
+// Filled with gfx950's direct global->LDS loads (one wave instruction = two
+// rows), so the next super-block's tile streams in while the current one is
+// multiplied, without holding it in registers.
+constexpr int kPfTile = kPfMT * 256;              // bf16 elements per tile buffer
+FO_DEV int pf_swz(int m, int c) { return m * 256 + 8 * (c ^ (m & 15)); }
+
 template <typename RowPtr>
-FO_DEV void pf_stage(uint16_t *xs, int n, int k0, RowPtr src_row) {
-    for (int i = threadIdx.x; i < kPfMT * 32; i += 256) {
-        const int m = i >> 5, c = i & 31;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (m < n) v = *(const uint4 *)(src_row(m) + k0 + 8 * c);
-        *(uint4 *)(xs + m * kPfXS + 8 * c) = v;
+FO_DEV void pf_stage_async(uint16_t *buf, int n, int k0, RowPtr src_row) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int q = wave; q < kPfMT / 2; q += nw) {
+        const int m = 2 * q + (lane >> 5), cs = lane & 31;      // LDS slot (m, cs)
+        const int c = cs ^ (m & 15);                            // global chunk stored there
+        const uint16_t *src = src_row(m < n ? m : 0) + k0 + 8 * c;
+        __builtin_amdgcn_global_load_lds((const void *)src,
+                                         (__attribute__((address_space(3))) void *)(buf + q * 512), 16, 0, 0);
     }
 }
 
 #pragma clang fp contract(off)
+// Work-group: kPfGateWaves waves over kPfGateRows rows of F: the first half
+// computes the gate rows, the second half the same up rows, for every token
+// block of the tile; the up sums meet the gate sums in LDS for the SwiGLU
+// epilogue. Wide work-groups share one staged token tile among many rows.
 template <int GT, int UT>
-__global__ __launch_bounds__(256) void k_pf_gateup(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[kPfMT * kPfXS];
+__global__ __launch_bounds__(kPfGateWaves * 64) void k_pf_gateup(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2 * kPfTile];
     if ((int)blockIdx.y >= *a.n_tiles) return;
     const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
     const int e = tl.x, p0 = tl.y, n = tl.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
     const bool shared = e == a.E;
     const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
-    const uint64_t up_off = shared ? a.sh_gate_size : a.gate_size;
-    const int row = blockIdx.x * kPfNT + 16 * wave + col;
-    const uint64_t gb = (uint64_t)(a.H / 256) * PfDec<GT>::BLOCK, ub = (uint64_t)(a.H / 256) * PfDec<UT>::BLOCK;
-    const uint8_t *grow = blob + (uint64_t)row * gb, *urow = blob + up_off + (uint64_t)row * ub;
-    const int nb = (n + 15) >> 4;
-    f32x4 ag[4], au[4];
-#pragma unroll
-    for (int b = 0; b < 4; b++) { ag[b] = (f32x4){0, 0, 0, 0}; au[b] = (f32x4){0, 0, 0, 0}; }
+    constexpr int HW = kPfGateWaves / 2;
+    const bool is_up = wave >= HW;
+    const int rl = 16 * (wave % HW) + col;                // row within the WG's kPfGateRows
+    const int row = blockIdx.x * kPfGateRows + rl;
+    const int nb = (n + 15) >> 4, NK = a.H / 256;
     const int32_t *toks = a.pair_tok + p0;
-    for (int kb = 0; kb < a.H / 256; kb++) {
-        const auto sg = PfDec<GT>::load(grow + (uint64_t)kb * PfDec<GT>::BLOCK, kg);
-        const auto su = PfDec<UT>::load(urow + (uint64_t)kb * PfDec<UT>::BLOCK, kg);
-        __syncthreads();
-        pf_stage(xs, n, kb * 256, [&](int m) { return a.x + (uint64_t)toks[m] * a.H; });
-        __syncthreads();
+    auto xrow = [&](int m) { return a.x + (uint64_t)toks[m] * a.H; };
+    f32x4 acc[4];
 #pragma unroll
-        for (int ch = 0; ch < 8; ch++) {
-            const bf16x8 bg = as_bf16x8(pf_decode<GT>(sg, ch, kg));
-            const bf16x8 bu = as_bf16x8(pf_decode<UT>(su, ch, kg));
+    for (int b = 0; b < 4; b++) acc[b] = (f32x4){0, 0, 0, 0};
+    auto run = [&](auto dec, const uint8_t *wrow) {
+        using D = decltype(dec);
+        pf_stage_async(xs, n, 0, xrow);
+        auto s_next = D::load(wrow, kg);
+        for (int kb = 0; kb < NK; kb++) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();                              // tile kb in LDS; buffer kb-1 free
+            const auto sw = s_next;
+            if (kb + 1 < NK) {
+                pf_stage_async(xs + ((kb + 1) & 1) * kPfTile, n, (kb + 1) * 256, xrow);
+                s_next = D::load(wrow + (uint64_t)(kb + 1) * D::BLOCK, kg);
+            }
+            const uint16_t *xb = xs + (kb & 1) * kPfTile;
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                if (b < nb) {
-                    const bf16x8 av = *(const bf16x8 *)(xs + (16 * b + col) * kPfXS + 32 * ch + 8 * kg);
-                    ag[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bg, ag[b], 0, 0, 0);
-                    au[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bu, au[b], 0, 0, 0);
-                }
+            for (int ch = 0; ch < 8; ch++) {
+                const bf16x8 bw = as_bf16x8(pf_decode<D::TYPE>(sw, ch, kg));
+#pragma unroll
+                for (int b = 0; b < 4; b++)
+                    if (b < nb)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            *(const bf16x8 *)(xb + pf_swz(16 * b + col, 4 * ch + kg)), bw, acc[b], 0, 0, 0);
             }
         }
+    };
+    if (!is_up) {
+        run(PfDec<GT>{}, blob + (uint64_t)row * ((uint64_t)NK * PfDec<GT>::BLOCK));
+    } else {
+        const uint64_t up_off = shared ? a.sh_gate_size : a.gate_size;
+        run(PfDec<UT>{}, blob + up_off + (uint64_t)row * ((uint64_t)NK * PfDec<UT>::BLOCK));
     }
-    // D layout: lane holds rows 4*(lane/16)+i (tokens) of column lane%16 (weight row)
+    __syncthreads();                                      // all reads of xs done: reuse it
+    float *ub = (float *)xs;                              // [64 tokens][kPfGateRows] up sums
+    if (is_up) {
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        if (b >= nb) break;
+        for (int b = 0; b < 4; b++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 16 * b + 4 * kg + i;
-            if (m < n) {
-                const float g = ag[b][i], u = au[b][i];
-                const float v = (g / (1.0f + expf(-g))) * u;
-                a.act[(uint64_t)(p0 + m) * a.F + row] = v;
+            for (int i = 0; i < 4; i++) ub[(16 * b + 4 * kg + i) * kPfGateRows + rl] = acc[b][i];
+    }
+    __syncthreads();
+    if (!is_up) {
+        // D layout: lane holds rows 4*(lane/16)+i (tokens) of column lane%16 (weight row);
+        // the activation is stored as hi/lo bf16 planes for the down projection
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            if (b >= nb) break;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * b + 4 * kg + i;
+                if (m < n) {
+                    const float g = acc[b][i], u = ub[m * kPfGateRows + rl];
+                    const float v = (g / (1.0f + expf(-g))) * u;
+                    const __bf16 hi = (__bf16)v;
+                    const __bf16 lo = (__bf16)(v - (float)hi);
+                    const uint64_t o = (uint64_t)(p0 + m) * a.F + row;
+                    a.act_hi[o] = __builtin_bit_cast(uint16_t, hi);
+                    a.act_lo[o] = __builtin_bit_cast(uint16_t, lo);
+                }
             }
         }
     }
 }
 
+constexpr int kPfDownWaves = 8;                   // 128 weight rows per work-group
+
 template <int DT>
-__global__ __launch_bounds__(256) void k_pf_down(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t xh[kPfMT * kPfXS];
-    __shared__ __attribute__((aligned(16))) uint16_t xl[kPfMT * kPfXS];
+__global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t dxs[];   // 2 buffers x {hi, lo} tiles
     if ((int)blockIdx.y >= *a.n_tiles) return;
     const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
     const int e = tl.x, p0 = tl.y, n = tl.z;
@@ -349,35 +392,44 @@ __global__ __launch_bounds__(256) void k_pf_down(PrefillArgs a) {
     const bool shared = e == a.E;
     const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
     const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
-    const int row = blockIdx.x * kPfNT + 16 * wave + col;
+    const int row = blockIdx.x * (16 * kPfDownWaves) + 16 * wave + col;
     const uint64_t db = (uint64_t)(a.F / 256) * PfDec<DT>::BLOCK;
     const uint8_t *drow = blob + down_off + (uint64_t)row * db;
-    const int nb = (n + 15) >> 4;
+    const int nb = (n + 15) >> 4, NK = a.F / 256;
     f32x4 acc[4];
 #pragma unroll
     for (int b = 0; b < 4; b++) acc[b] = (f32x4){0, 0, 0, 0};
-    for (int kb = 0; kb < a.F / 256; kb++) {
-        const auto sd = PfDec<DT>::load(drow + (uint64_t)kb * PfDec<DT>::BLOCK, kg);
-        __syncthreads();
-        // stage act rows (fp32) as hi/lo bf16 pairs
-        for (int i = threadIdx.x; i < kPfMT * 64; i += 256) {
-            const int m = i >> 6, c = i & 63;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m < n) v = *(const float4 *)(a.act + (uint64_t)(p0 + m) * a.F + kb * 256 + 4 * c);
-            const uint32_t h0 = pack_bf16(v.x, v.y), h1 = pack_bf16(v.z, v.w);
-            const uint32_t l0 = pack_bf16(v.x - bf2f(h0 & 0xFFFFu), v.y - bf2f(h0 >> 16));
-            const uint32_t l1 = pack_bf16(v.z - bf2f(h1 & 0xFFFFu), v.w - bf2f(h1 >> 16));
-            *(uint2 *)(xh + m * kPfXS + 4 * c) = make_uint2(h0, h1);
-            *(uint2 *)(xl + m * kPfXS + 4 * c) = make_uint2(l0, l1);
+    auto stage = [&](int kb) {   // first half of the waves stages hi, second half lo
+        constexpr int HW = kPfDownWaves / 2;
+        uint16_t *buf = dxs + (kb & 1) * 2 * kPfTile + (wave / HW) * kPfTile;
+        const uint16_t *plane = (wave / HW) ? a.act_lo : a.act_hi;
+        const int lane_ = threadIdx.x & 63, w4 = wave % HW;
+        for (int q = w4; q < kPfMT / 2; q += HW) {
+            const int m = 2 * q + (lane_ >> 5), cs = lane_ & 31;
+            const int c = cs ^ (m & 15);
+            const uint16_t *src = plane + (uint64_t)(p0 + (m < n ? m : 0)) * a.F + kb * 256 + 8 * c;
+            __builtin_amdgcn_global_load_lds((const void *)src,
+                                             (__attribute__((address_space(3))) void *)(buf + q * 512), 16, 0, 0);
         }
+    };
+    stage(0);
+    auto sd_next = PfDec<DT>::load(drow, kg);
+    for (int kb = 0; kb < NK; kb++) {
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        const auto sd = sd_next;
+        if (kb + 1 < NK) {
+            stage(kb + 1);
+            sd_next = PfDec<DT>::load(drow + (uint64_t)(kb + 1) * PfDec<DT>::BLOCK, kg);
+        }
+        const uint16_t *xh = dxs + (kb & 1) * 2 * kPfTile, *xl = xh + kPfTile;
 #pragma unroll
         for (int ch = 0; ch < 8; ch++) {
             const bf16x8 bd = as_bf16x8(pf_decode<DT>(sd, ch, kg));
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 if (b < nb) {
-                    const int o = (16 * b + col) * kPfXS + 32 * ch + 8 * kg;
+                    const int o = pf_swz(16 * b + col, 4 * ch + kg);
                     acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(xh + o), bd, acc[b], 0, 0, 0);
                     acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(xl + o), bd, acc[b], 0, 0, 0);
                 }
@@ -424,7 +476,7 @@ hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStr
 // ============================================================ launcher
 template <int GT, int UT>
 static hipError_t launch_gateup_t(const PrefillArgs &a, hipStream_t s) {
-    k_pf_gateup<GT, UT><<<dim3(a.F / kPfNT, a.max_tiles), 256, 0, s>>>(a);
+    k_pf_gateup<GT, UT><<<dim3(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -434,7 +486,7 @@ hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
                      (a.down_type == GGML_TYPE_Q4_K || a.down_type == GGML_TYPE_Q6_K);
     const int W = (a.T + 31) / 32;
     if (!okt || a.T <= 0 || a.E <= 0 || a.E > 1023 || a.k <= 0 || a.k > a.E || a.k > kMaxK ||
-        a.H <= 0 || a.H % 256 || a.F <= 0 || a.F % 256 || a.E * W > kPfGroupLds ||
+        a.H <= 0 || a.H % 256 || a.H % (16 * kPfDownWaves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
         a.max_tiles < prefill_max_tiles(a.T, a.k, a.E, a.shared != nullptr))
         return hipErrorInvalidValue;
     k_pf_router<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 256, 0, s>>>(a);
@@ -454,8 +506,22 @@ hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
     FO_GU(GGML_TYPE_Q6_K, GGML_TYPE_Q4_K) FO_GU(GGML_TYPE_Q6_K, GGML_TYPE_Q6_K)
 #undef FO_GU
     if (err != hipSuccess) return err;
-    if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<dim3(a.H / kPfNT, a.max_tiles), 256, 0, s>>>(a);
-    else k_pf_down<GGML_TYPE_Q6_K><<<dim3(a.H / kPfNT, a.max_tiles), 256, 0, s>>>(a);
+    {
+        const size_t lds = 4 * (size_t)kPfTile * sizeof(uint16_t);       // 128 KiB
+        const dim3 grid(a.H / (16 * kPfDownWaves), a.max_tiles);
+        static bool down_attr = false;
+        if (!down_attr) {
+            hipError_t e1 = hipFuncSetAttribute((const void *)k_pf_down<GGML_TYPE_Q4_K>,
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            hipError_t e2 = hipFuncSetAttribute((const void *)k_pf_down<GGML_TYPE_Q6_K>,
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e1 != hipSuccess) return e1;
+            if (e2 != hipSuccess) return e2;
+            down_attr = true;
+        }
+        if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
+        else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
+    }
     k_pf_combine<<<a.T, 256, 0, s>>>(a);
     return hipGetLastError();
 }

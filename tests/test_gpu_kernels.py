@@ -105,7 +105,8 @@ def test_matvec_baseline_configs(gpu, name, t, M, K, ws, xs):
 @pytest.mark.parametrize("t,M,K", [
     (O.Q4_K, 1, 256), (O.Q4_K, 3, 512), (O.Q4_K, 7, 1024), (O.Q4_K, 33, 2048), (O.Q4_K, 5, 3072),
     (O.Q4_K, 9, 8192), (O.Q4_K, 2, 16384), (O.Q5_K, 17, 1024), (O.Q5_K, 8, 4096),
-    (O.Q6_K, 1, 256), (O.Q6_K, 11, 768), (O.Q6_K, 64, 3072), (O.Q6_K, 3, 16384),
+    (O.Q6_K, 1, 256), (O.Q6_K, 11, 768), (O.Q6_K, 17, 1024), (O.Q6_K, 40, 512), (O.Q6_K, 64, 3072),
+    (O.Q6_K, 3, 16384),
     (O.Q8_0, 1, 32), (O.Q8_0, 5, 96), (O.Q8_0, 19, 4096), (O.Q8_0, 2, 8192),
 ])
 def test_matvec_shapes(gpu, t, M, K):
