@@ -21,10 +21,11 @@ struct RouteArgs {
 };
 
 // K2: top-k of logits, then act_e = silu(gate_e . h) * (up_e . h) for the k
-// routed experts (blob = base + id*stride: gate at 0, up at gate_size) and the
-// shared expert (gate at 0, up at sh_gate_size), written in prepared form
-// (groups of down_gsz) at xq_act + e*xq_vstride, and as fp32 to act if set.
-// Work-group 0 writes ids[k] / weights[k].
+// routed experts (blob = base + id*stride: gate at 0, up at gate_size) and,
+// when shared is set, the shared expert (gate at 0, up at sh_gate_size),
+// written in prepared form (groups of down_gsz) at xq_act + e*xq_vstride
+// (shared: e = k), and as fp32 to act if set. The first work-group with
+// nothing else to wait for writes ids[k] / weights[k].
 struct ExpandArgs {
     const float *logits;
     int E, k;

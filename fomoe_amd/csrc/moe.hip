@@ -194,6 +194,8 @@ __global__ __launch_bounds__((ExpandShape<T, TR, U>::THREADS), 3) void k_expand(
     const int e = blockIdx.x / tpe, rb = blockIdx.x - e * tpe;
     const bool routed = e < a.k;
     const uint64_t xqb = xq_bytes(H, F::GSZ);
+    // the prepared h streams into LDS while wave 0 selects experts
+    stage_lds(lds, a.xq_h, (uint32_t)xqb, wv, NW);
     // A routed WG of rank e needs only the first e+1 selections; the full
     // top-k with weights (for K3) is computed once, by the first WG that has
     // nothing else to wait for (the shared expert's first task, or WG 0).
@@ -204,7 +206,6 @@ __global__ __launch_bounds__((ExpandShape<T, TR, U>::THREADS), 3) void k_expand(
         else wave_topk<16>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
         if (full && lane < a.k) { a.ids[lane] = s_ids[lane]; a.weights[lane] = s_w[lane]; }
     }
-    stage_lds(lds, a.xq_h, (uint32_t)xqb, wv, NW);
     stage_lds_wait();
     const uint8_t *blob;
     uint64_t uo;
