@@ -45,6 +45,9 @@ SIGNATURES = {
     "gpu_router_topk": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, C.c_int, C.c_int, C.c_int,
                                   _vp, _vp]),
     "gpu_moe_stack_decode": (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int]),
+    "gpu_qmoe_read_index": (C.c_int, [C.c_char_p, _vp, _vp, C.c_int, C.POINTER(C.c_char_p)]),
+    "gpu_qmoe_upload_layer": (C.c_int, [_vp, C.c_char_p, C.c_int, _vp, C.c_uint64]),
+    "gpu_qmoe_layer_desc": (C.c_int, [_vp, _vp, _vp]),
     "gpu_moe_prefill": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, C.c_int]),
     "gpu_moe_prefill_routing": (C.c_int, [_vp, _vp, _vp]),
     "gpu_f32_to_bf16": (C.c_int, [_vp, _vp, _vp, C.c_int64]),
@@ -84,6 +87,34 @@ class MoeLayer(C.Structure):
                 ("shared_inter", C.c_int), ("shared_gate_size", C.c_uint64),
                 ("shared_up_size", C.c_uint64), ("shared_gate_vec", _vp), ("norm_w", _vp),
                 ("eps", C.c_float)]
+
+
+class QmoeHeader(C.Structure):
+    """Expert-store file header (64 bytes; reference include/expert_store.h:17-29)."""
+    _fields_ = [("magic", C.c_uint32), ("version", C.c_uint32), ("n_moe_layers", C.c_uint32),
+                ("n_experts", C.c_uint32), ("quant_type", C.c_uint32), ("alignment", C.c_uint32),
+                ("expert_gate_size", C.c_uint64), ("expert_up_size", C.c_uint64),
+                ("expert_down_size", C.c_uint64), ("expert_stride", C.c_uint64),
+                ("reserved", C.c_uint8 * 8)]
+
+
+class QmoeLayerEntry(C.Structure):
+    """Per-layer index entry (32 bytes; reference include/expert_store.h:33-39)."""
+    _fields_ = [("data_offset", C.c_uint64), ("expert_stride", C.c_uint64), ("down_size", C.c_uint64),
+                ("down_type", C.c_uint32), ("pad", C.c_uint32)]
+
+
+def qmoe_read_index(path: str, lib=None):
+    """Header and layer entries of a .qmoe file (host only); raises on a bad file."""
+    lib = lib or load_library()
+    h = QmoeHeader()
+    err = C.c_char_p()
+    n = lib.gpu_qmoe_read_index(path.encode(), C.byref(h), None, 0, C.byref(err))
+    if n < 0:
+        raise RuntimeError(err.value.decode())
+    layers = (QmoeLayerEntry * n)()
+    lib.gpu_qmoe_read_index(path.encode(), C.byref(h), layers, n, C.byref(err))
+    return h, list(layers)
 
 
 class GpuError(RuntimeError):
@@ -198,6 +229,14 @@ class Gpu:
         arr = (MoeLayer * len(layers))(*layers)
         self.check(self.lib.gpu_moe_stack_decode(self.ctx, arr, len(layers), _p(x), n_steps),
                    "gpu_moe_stack_decode")
+
+    def qmoe_upload_layer(self, path: str, layer: int, dst, nbytes: int):
+        self.check(self.lib.gpu_qmoe_upload_layer(self.ctx, path.encode(), layer, _p(dst), nbytes),
+                   "gpu_qmoe_upload_layer")
+
+    def qmoe_layer_desc(self, hdr: "QmoeHeader", entry: "QmoeLayerEntry", layer: MoeLayer):
+        self.check(self.lib.gpu_qmoe_layer_desc(C.byref(hdr), C.byref(entry), C.byref(layer)),
+                   "gpu_qmoe_layer_desc")
 
     def moe_prefill(self, layer: MoeLayer, x_bf16, n_tokens: int, out, flags: int = 0):
         self.check(self.lib.gpu_moe_prefill(self.ctx, C.byref(layer), _p(x_bf16), n_tokens, _p(out),

@@ -3,12 +3,16 @@
 // One context = one device, one stream, lazily grown scratch. Every launch is
 // argument-checked on the host against the shapes the kernels cover before
 // anything reaches the device.
+#include <fcntl.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -56,6 +60,10 @@ struct gpu_ctx {
     float *pf_outp = nullptr;      size_t pf_outp_cap = 0;
     int pf_T = 0, pf_k = 0;
 
+    // pinned staging for host->device uploads of expert stores
+    uint8_t *pin[2] = {nullptr, nullptr};
+    hipEvent_t pin_ev[2] = {nullptr, nullptr};
+
     // captured stack-decode graph
     hipGraphExec_t graph_exec = nullptr;
 };
@@ -94,7 +102,8 @@ static hipError_t ensure(Tp *&p, size_t &cap, size_t need) {
 }
 
 static bool kquant(int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K; }
-static bool matvec_type(int t) { return kquant(t) || t == GGML_TYPE_Q8_0; }
+static bool layer_type(int t) { return kquant(t) || t == GGML_TYPE_Q8_0; }
+static bool matvec_type(int t) { return layer_type(t) || t == GGML_TYPE_MXFP4; }
 
 extern "C" {
 
@@ -141,6 +150,10 @@ void gpu_free(gpu_ctx_t *c) {
                     c->pf_act, c->pf_outp};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
+    for (int b = 0; b < 2; b++) {
+        if (c->pin[b]) (void)hipHostFree(c->pin[b]);
+        if (c->pin_ev[b]) (void)hipEventDestroy(c->pin_ev[b]);
+    }
     if (c->ev0) (void)hipEventDestroy(c->ev0);
     if (c->ev1) (void)hipEventDestroy(c->ev1);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -261,7 +274,7 @@ static int check_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L) {
         return fail(ctx, -1, "moe layer: inter %d (multiple of 256, <= 8192)", L->inter);
     if (L->n_experts <= 0 || L->n_experts > 1024 || L->k <= 0 || L->k > 16 || L->k > L->n_experts)
         return fail(ctx, -1, "moe layer: n_experts %d / k %d", L->n_experts, L->k);
-    if (!matvec_type(L->gate_type) || L->up_type != L->gate_type || !matvec_type(L->down_type))
+    if (!layer_type(L->gate_type) || L->up_type != L->gate_type || !layer_type(L->down_type))
         return fail(ctx, -1, "moe layer: types gate %d up %d down %d", L->gate_type, L->up_type,
                     L->down_type);
     const uint64_t gs = fomoe_row_bytes(L->gate_type, L->n_embd) * (uint64_t)L->inter;
@@ -478,7 +491,7 @@ int gpu_synth_quant(gpu_ctx_t *ctx, int type, uint64_t seed, uint64_t stream0, u
                     int64_t M, int64_t K, int n_mats, void *dst, uint64_t dst_stride) {
     if (!ctx || !dst || M <= 0 || K <= 0 || K % 256 || n_mats <= 0)
         return fail(ctx, -1, "gpu_synth_quant: bad argument");
-    if (!matvec_type(type)) return fail(ctx, -1, "gpu_synth_quant: type %d", type);
+    if (!layer_type(type)) return fail(ctx, -1, "gpu_synth_quant: type %d", type);
     HIPC(launch_synth_quant(type, seed, stream0, step, std, M, K, n_mats, (uint8_t *)dst, dst_stride,
                             ctx->stream));
     return 0;
@@ -559,6 +572,117 @@ int gpu_moe_prefill_routing(gpu_ctx_t *ctx, int32_t *ids, float *weights) {
 int gpu_f32_to_bf16(gpu_ctx_t *ctx, const float *d_src, uint16_t *d_dst, int64_t n) {
     if (!ctx || !d_src || !d_dst || n <= 0) return fail(ctx, -1, "f32_to_bf16: bad arguments");
     HIPC(fo::launch_f32_to_bf16(d_src, d_dst, n, ctx->stream));
+    return 0;
+}
+
+
+// ------------------------------------------------------------------ expert store
+static_assert(sizeof(gpu_qmoe_header_t) == 64, "qmoe header is 64 bytes on disk");
+static_assert(sizeof(gpu_qmoe_layer_entry_t) == 32, "qmoe layer entry is 32 bytes on disk");
+constexpr size_t kPinChunk = 32u << 20;
+
+// Header and index of a .qmoe file (reference src/expert_store.c:11-100),
+// validated against the file size so that later reads stay inside it.
+static bool qmoe_index(const char *path, gpu_qmoe_header_t &h, std::vector<gpu_qmoe_layer_entry_t> &idx,
+                       std::string &err) {
+    const int fd = path ? open(path, O_RDONLY) : -1;
+    if (fd < 0) { err = std::string("qmoe: cannot open ") + (path ? path : "(null)"); return false; }
+    struct stat st;
+    bool ok = fstat(fd, &st) == 0 && pread(fd, &h, sizeof h, 0) == (ssize_t)sizeof h;
+    if (!ok) err = "qmoe: cannot read the header";
+    else if (h.magic != GPU_QMOE_MAGIC) { ok = false; err = "qmoe: bad magic"; }
+    else if (h.version < GPU_QMOE_VERSION) { ok = false; err = "qmoe: format version < 2"; }
+    else if (h.n_moe_layers == 0 || h.n_moe_layers > 65536 || h.n_experts == 0 || h.n_experts > 65536) {
+        ok = false; err = "qmoe: bad layer / expert counts";
+    }
+    if (ok) {
+        idx.resize(h.n_moe_layers);
+        const size_t bytes = idx.size() * sizeof(gpu_qmoe_layer_entry_t);
+        ok = pread(fd, idx.data(), bytes, 64) == (ssize_t)bytes;
+        if (!ok) err = "qmoe: truncated layer index";
+    }
+    const uint64_t index_end = 64 + (uint64_t)h.n_moe_layers * sizeof(gpu_qmoe_layer_entry_t);
+    for (size_t l = 0; ok && l < idx.size(); l++) {
+        const uint64_t stride = idx[l].expert_stride ? idx[l].expert_stride : h.expert_stride;
+        const uint64_t down = idx[l].down_size ? idx[l].down_size : h.expert_down_size;
+        if (stride == 0 || stride < h.expert_gate_size + h.expert_up_size + down ||
+            idx[l].data_offset < index_end ||
+            idx[l].data_offset + (uint64_t)h.n_experts * stride > (uint64_t)st.st_size) {
+            ok = false;
+            err = "qmoe: layer " + std::to_string(l) + " does not fit the file";
+        }
+    }
+    close(fd);
+    return ok;
+}
+
+int gpu_qmoe_read_index(const char *path, gpu_qmoe_header_t *hdr, gpu_qmoe_layer_entry_t *layers,
+                        int max_layers, const char **err) {
+    static thread_local std::string msg;
+    gpu_qmoe_header_t h;
+    std::vector<gpu_qmoe_layer_entry_t> idx;
+    if (!qmoe_index(path, h, idx, msg)) {
+        if (err) *err = msg.c_str();
+        return -1;
+    }
+    msg.clear();
+    if (err) *err = msg.c_str();
+    if (hdr) *hdr = h;
+    if (layers)
+        for (int l = 0; l < max_layers && l < (int)idx.size(); l++) layers[l] = idx[l];
+    return (int)h.n_moe_layers;
+}
+
+int gpu_qmoe_upload_layer(gpu_ctx_t *ctx, const char *path, int layer, void *d_dst, uint64_t dst_bytes) {
+    if (!ctx || !d_dst) return fail(ctx, -1, "qmoe upload: null context or destination");
+    gpu_qmoe_header_t h;
+    std::vector<gpu_qmoe_layer_entry_t> idx;
+    std::string msg;
+    if (!qmoe_index(path, h, idx, msg)) return fail(ctx, -1, "%s", msg.c_str());
+    if (layer < 0 || layer >= (int)idx.size()) return fail(ctx, -1, "qmoe upload: layer %d of %zu", layer, idx.size());
+    const uint64_t stride = idx[layer].expert_stride ? idx[layer].expert_stride : h.expert_stride;
+    const uint64_t total = (uint64_t)h.n_experts * stride;
+    if (dst_bytes < total) return fail(ctx, -1, "qmoe upload: destination %llu < %llu bytes",
+                                       (unsigned long long)dst_bytes, (unsigned long long)total);
+    for (int b = 0; b < 2; b++) {
+        if (!ctx->pin[b]) HIPC(hipHostMalloc((void **)&ctx->pin[b], kPinChunk, hipHostMallocDefault));
+        if (!ctx->pin_ev[b]) HIPC(hipEventCreateWithFlags(&ctx->pin_ev[b], hipEventDisableTiming));
+    }
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return fail(ctx, -1, "qmoe upload: cannot open %s", path);
+    // two pinned chunks alternate: the read of one overlaps the copy of the other
+    int rc = 0;
+    bool used[2] = {false, false};
+    uint64_t off = 0;
+    for (int b = 0; off < total && rc == 0; b ^= 1) {
+        const size_t n = (size_t)std::min<uint64_t>(kPinChunk, total - off);
+        if (used[b] && hipEventSynchronize(ctx->pin_ev[b]) != hipSuccess) { rc = -2; break; }
+        size_t got = 0;
+        while (got < n) {
+            const ssize_t r = pread(fd, ctx->pin[b] + got, n - got, (off_t)(idx[layer].data_offset + off + got));
+            if (r <= 0) break;
+            got += (size_t)r;
+        }
+        if (got != n) { rc = fail(ctx, -1, "qmoe upload: short read at offset %llu", (unsigned long long)off); break; }
+        if (hipMemcpyAsync((uint8_t *)d_dst + off, ctx->pin[b], n, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+            hipEventRecord(ctx->pin_ev[b], ctx->stream) != hipSuccess) { rc = -2; break; }
+        used[b] = true;
+        off += n;
+    }
+    close(fd);
+    // copies still in flight read the pinned chunks: drain them on every path
+    const hipError_t se = hipStreamSynchronize(ctx->stream);
+    if (rc == -2 || se != hipSuccess) return fail(ctx, -2, "qmoe upload: device copy failed");
+    return rc;
+}
+
+int gpu_qmoe_layer_desc(const gpu_qmoe_header_t *h, const gpu_qmoe_layer_entry_t *e, gpu_moe_layer_t *L) {
+    if (!h || !e || !L) return -1;
+    L->gate_type = L->up_type = (int)h->quant_type;
+    L->down_type = e->down_size ? (int)e->down_type : (int)h->quant_type;
+    L->gate_size = h->expert_gate_size;
+    L->up_size = h->expert_up_size;
+    L->expert_stride = e->expert_stride ? e->expert_stride : h->expert_stride;
     return 0;
 }
 

@@ -242,5 +242,46 @@ template <> struct Fmt<GGML_TYPE_Q8_0> {
     }
 };
 
+// ---------------------------------------------------------------- MXFP4
+// Slot = one 17-byte block: E8M0 exponent s + 32 E2M1 codes (low nibble of
+// qs[j] is value j, high nibble value 16+j; reference src/quant.c:290-337).
+// Codes are mapped to twice their value as int8 ({0,1,2,3,4,6,8,12} and
+// negatives) through v_perm byte tables, so the block scale is 2^(s-128)
+// (0 for s = 0xFF, as the reference).
+template <> struct Fmt<GGML_TYPE_MXFP4> {
+    static constexpr int SLOT = 32, BLOCK = 17, NG = 1, GSZ = 32;
+    using X = XSlot<NG, GSZ>;
+    struct Raw { uint4 q; uint32_t s; };
+
+    static FO_DEV Raw load(const uint8_t *row, int s) {
+        const uint8_t *b = row + s * BLOCK;
+        return Raw{ld16(b + 1), ld2(b) & 0xFFu};
+    }
+    static FO_DEV void groups(int s, int gi[NG]) { gi[0] = s; }
+    // four 4-bit codes (one per byte, 0..15) -> 2 * E2M1 value as int8
+    static FO_DEV uint32_t e2m1x2(uint32_t c) {
+        const uint32_t m = c & 0x07070707u;
+        const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, m);
+        const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, m);
+        const uint32_t sgn = ((c >> 3) & 0x01010101u) * 0xFFu;
+        return (neg & sgn) | (pos & ~sgn);
+    }
+    static FO_DEV float dot(const Raw &r, int, const X &x) {
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        int a[kLimbs] = {};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t lo = e2m1x2(q[k] & 0x0F0F0F0Fu), hi = e2m1x2((q[k] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int L = 0; L < kLimbs; L++) {
+                a[L] = dot4(lo, x.l[0][L][k], a[L]);
+                a[L] = dot4(hi, x.l[0][L][k + 4], a[L]);
+            }
+        }
+        const float scale = r.s == 0xFFu ? 0.f : ldexpf(1.0f, (int)r.s - 128);
+        return scale * (combine(a) * x.sc[0]);
+    }
+};
+
 
 }  // namespace fo

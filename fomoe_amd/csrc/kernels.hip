@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
 
 // Slot geometry of a K-wide row: lanes per row G and slots per lane U.
 static bool geometry(int type, int K, int &G, int &U) {
-    const int slot = (type == GGML_TYPE_Q8_0) ? 32 : 64;
+    const int slot = (type == GGML_TYPE_Q8_0 || type == GGML_TYPE_MXFP4) ? 32 : 64;
     if (K <= 0 || K % slot) return false;
     if ((type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K || type == GGML_TYPE_Q6_K) && K % 256)
         return false;
@@ -349,6 +349,7 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
             }
             return matvec_t<GGML_TYPE_Q6_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q8_0: return matvec_t<GGML_TYPE_Q8_0, 2>(a, s, n_cu);
+        case GGML_TYPE_MXFP4: return matvec_t<GGML_TYPE_MXFP4, 2>(a, s, n_cu);
         default: return hipErrorInvalidValue;
     }
 }

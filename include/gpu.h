@@ -128,6 +128,37 @@ int gpu_router_topk(gpu_ctx_t *ctx, const float *d_router, const float *d_bias,
 int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_layers,
                          float *d_x, int n_steps);
 
+/* ---------------------------------------------------------------- expert store (.qmoe)
+ * The reference's expert-store file (reference include/expert_store.h:8-40,
+ * src/expert_store.c, tools/prepare_experts.c:116-170): a 64-byte header and
+ * one 32-byte entry per MoE layer, then per layer n_experts blobs gate|up|down
+ * at expert_stride (4096-aligned) from data_offset; down_type may differ per
+ * layer. The layouts below are that file format, byte for byte. */
+#define GPU_QMOE_MAGIC   0x454F4D51u   /* "QMOE" */
+#define GPU_QMOE_VERSION 2
+typedef struct {
+    uint32_t magic, version, n_moe_layers, n_experts, quant_type, alignment;
+    uint64_t expert_gate_size, expert_up_size, expert_down_size, expert_stride;
+    uint8_t reserved[8];
+} gpu_qmoe_header_t;                  /* 64 bytes */
+typedef struct {
+    uint64_t data_offset, expert_stride, down_size;
+    uint32_t down_type, pad;
+} gpu_qmoe_layer_entry_t;             /* 32 bytes */
+
+/* Host only (no device needed): read and validate the header and up to
+ * max_layers index entries. Returns n_moe_layers, or -1 (unreadable file, bad
+ * magic, version < 2, inconsistent sizes); *err (may be NULL) gets a message. */
+int gpu_qmoe_read_index(const char *path, gpu_qmoe_header_t *hdr, gpu_qmoe_layer_entry_t *layers,
+                        int max_layers, const char **err);
+/* Copy layer `layer` (n_experts * expert_stride bytes) from the file into
+ * device memory d_dst (sync; pinned double-buffered staging). 0 / -1 / -2. */
+int gpu_qmoe_upload_layer(gpu_ctx_t *ctx, const char *path, int layer, void *d_dst, uint64_t dst_bytes);
+/* Fill the type / size / stride fields of *L for one layer of the store
+ * (experts, router and the other pointers are left to the caller). */
+int gpu_qmoe_layer_desc(const gpu_qmoe_header_t *hdr, const gpu_qmoe_layer_entry_t *entry,
+                        gpu_moe_layer_t *L);
+
 /* ---------------------------------------------------------------- prefill
  * n_tokens tokens through one MoE layer at once (async): d_x [n_tokens x
  * n_embd] bf16, d_out [n_tokens x n_embd] fp32 (= x + ffn with

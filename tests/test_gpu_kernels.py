@@ -131,6 +131,29 @@ def test_matvec_activation_extremes(gpu):
     assert parity_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("M,K", [(1, 32), (5, 96), (64, 4096), (33, 2880), (7, 8192)])
+def test_matvec_mxfp4(gpu, M, K):
+    """MXFP4 (E8M0 + E2M1, reference src/quant.c:290-337) matvec on random
+    blocks, including NaN-exponent (0xFF) blocks that the reference zeroes."""
+    say("matvec mxfp4", M, K)
+    rng = np.random.default_rng(M * 7 + K)
+    nb = M * K // 32
+    blk = np.zeros((nb, 17), np.uint8)
+    blk[:, 0] = rng.integers(118, 136, nb)
+    blk[rng.random(nb) < 0.01, 0] = 0xFF
+    blk[:, 1:] = rng.integers(0, 256, (nb, 16))
+    W = blk.reshape(-1)
+    x = O.synth_f32(77, K, 1.0, K)
+    dW, dx, dy = gpu.upload(W), gpu.upload(x), gpu.alloc(4 * M)
+    gpu.matvec(O.MXFP4, dW, dx, dy, M, K)
+    got = gpu.download(dy, np.float32, M)
+    want = O.mat_vec(O.MXFP4, W, x, M, K)
+    ref = O.dequantize(O.MXFP4, W, M * K).reshape(M, K).astype(np.float64) @ x.astype(np.float64)
+    say(f"  parity_err {parity_err(got, ref):.3e} inf_rel(oracle) {inf_rel(got, want):.3e}")
+    assert parity_err(got, ref) <= TOL
+    assert inf_rel(got, want) < 1e-5
+
+
 @pytest.mark.parametrize("t,M,K,per_x", [(O.Q4_K, 1024, 4096, False), (O.Q6_K, 4096, 1024, True),
                                          (O.Q8_0, 256, 1024, True)])
 def test_matvec_batched(gpu, t, M, K, per_x):
