@@ -236,13 +236,13 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
     constexpr uint32_t zoff = lds_round(xbytes);
     uint8_t *tb = sx + zoff + lds_round(limb_bytes);
     const uint8_t *Wm = a.W + mat * a.mat_stride;
-    const uint64_t rb = a.row_bytes;
+    constexpr uint32_t rb = NSB * 210;                 // launched only for contiguous rows
     const int tile0 = blockIdx.x * TPW;
     const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
     // A piece that straddles the end of a partial tile (16*rows*rb need not be a
     // multiple of 16) is read from the last 16 valid bytes and written to that
     // same LDS position (overlapping its neighbour with identical bytes).
-    auto tile_bytes = [&](int tile) { return (uint32_t)(min(kT6Rows, a.M - tile * kT6Rows) * rb); };
+    auto tile_bytes = [&](int tile) { return (uint32_t)min(kT6Rows, a.M - tile * kT6Rows) * rb; };
     auto pos = [&](uint32_t o, uint32_t nb) { return o + 16 <= nb ? o : nb - 16; };
     auto issue = [&](uint4 (&v)[NV], int tile) {
         const uint32_t nb = tile_bytes(tile);
