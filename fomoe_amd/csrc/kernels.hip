@@ -12,6 +12,7 @@
 
 #include "formats.h"
 #include "kernels.h"
+#include "q6k_mfma.h"
 
 namespace fo {
 
@@ -222,7 +223,6 @@ static hipError_t matvec_t(const MatvecArgs &a, hipStream_t s, int n_cu) {
 // g's k-range (other lanes read a zeroed LDS region). D layout: lane holds
 // rows 4*(lane/16)+i of column lane%16. Group scales / offsets / sub-block
 // scales are then applied per lane as in Fmt<Q6_K>.
-typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kT6Rows = 16, kT6MaxNV = 14;   // 16 rows x 840 B <= 14 KiB
 
 template <int NSB, int TPW>
@@ -273,44 +273,7 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
         const uint8_t *rp = tb + r * rb;
         float acc = 0.f;
 #pragma unroll
-        for (int b = 0; b < NSB; b++) {
-            const uint8_t *bp = rp + b * 210;
-            uint4 l0, l1, hh;
-            uint2 scb;
-            __builtin_memcpy(&l0, bp + 64 * n + 16 * j, 16);
-            __builtin_memcpy(&l1, bp + 64 * n + 32 + 16 * j, 16);
-            __builtin_memcpy(&hh, bp + 128 + 32 * n + 16 * j, 16);
-            __builtin_memcpy(&scb, bp + 192 + 8 * n, 8);
-            uint16_t d16;
-            __builtin_memcpy(&d16, bp + 208, 2);
-            const uint32_t Lo[4] = {l0.x, l0.y, l0.z, l0.w};
-            const uint32_t Hi[4] = {l1.x, l1.y, l1.z, l1.w};
-            const uint32_t H[4] = {hh.x, hh.y, hh.z, hh.w};
-            float accb = 0.f;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                v4i B;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    uint32_t q;
-                    if (t == 0) q = (Lo[k] & 0x0F0F0F0Fu) | ((H[k] << 4) & 0x30303030u);
-                    else if (t == 1) q = (Hi[k] & 0x0F0F0F0Fu) | ((H[k] << 2) & 0x30303030u);
-                    else if (t == 2) q = ((Lo[k] >> 4) & 0x0F0F0F0Fu) | (H[k] & 0x30303030u);
-                    else q = ((Hi[k] >> 4) & 0x0F0F0F0Fu) | ((H[k] >> 2) & 0x30303030u);
-                    B[k] = (int)q;
-                }
-                const int go = 16 * b + 2 * t;                   // group 16b + 8n + 2t + j
-                const v4i A = *(const v4i *)(abase + go * 48);
-                const v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
-                const float f = fmaf(fmaf((float)D[2], 256.f, (float)D[1]), 256.f, (float)D[0]);
-                const float2 ss = *(const float2 *)(ssb + go * 8);
-                const float vv = fmaf(f, ss.x, -32.f * ss.y);
-                const uint32_t sw = (t < 2) ? scb.x : scb.y;       // sc[8n + 2t + j]
-                const int scv = (int)(sw << (24 - 8 * (2 * (t & 1) + j))) >> 24;
-                accb = fmaf((float)scv, vv, accb);
-            }
-            acc = fmaf(h2f(d16), accb, acc);
-        }
+        for (int b = 0; b < NSB; b++) acc += q6k_sb_dot_mfma(rp + b * 210, abase, ssb, 16 * b, n, j);
         acc += __shfl_xor(acc, 16);
         acc += __shfl_xor(acc, 32);
         const int row = tile * kT6Rows + r;

@@ -264,6 +264,52 @@ def test_moe_layer_norm_residual_gate(gpu):
     assert np.array_equal(got, (x + ffn).astype(np.float32))
 
 
+@pytest.mark.parametrize("H,F,E,k,shared", [(512, 512, 16, 4, True), (1024, 1024, 24, 12, True),
+                                             (512, 1024, 8, 3, False), (2048, 512, 16, 13, False)])
+def test_moe_layer_shapes_vs_fp64(gpu, H, F, E, k, shared):
+    """Layer shapes on both down-projection kernels (the tile-staged Q6_K one
+    for F = 512 / 1024 up to 13 experts per work-group), with RMSNorm and a
+    shared expert, against an fp64 recomposition and the fp32 oracle."""
+    from fomoe_amd import synthetic as S
+    from test_oracle import moe_desc
+    say(f"layer H={H} F={F} E={E} k={k} shared={shared}")
+    shape = S.LayerShape(n_embd=H, inter=F, n_experts=E, k=k, shared=shared)
+    L = S.build_layer(gpu, shape, 0, seed=31, zipf_s=1.1, norm=True)
+    x = O.synth_f32(32, 0, 1.5, H)
+    dx, dout = gpu.upload(x), gpu.alloc(4 * H)
+    gpu.moe_layer(L.desc, dx, dout, FA.MOE_NORM)
+    got = gpu.download(dout, np.float32, H)
+    ids, w, _ = gpu.last_routing(k)
+    router = O.synth_f32(31, S.stream(0, 0, S.ROUTER), 0.02, E * H)
+    experts = np.zeros((E + 1) * shape.stride, np.uint8)
+    blobs = {}
+    for e in range(E + 1):
+        blobs[e] = (O.synth_quant(O.Q4_K, 31, S.stream(0, e, S.GATE), 0.02, F, H),
+                    O.synth_quant(O.Q4_K, 31, S.stream(0, e, S.UP), 0.02, F, H),
+                    O.synth_quant(O.Q6_K, 31, S.stream(0, e, S.DOWN), 0.02, H, F))
+        b = np.concatenate(blobs[e])
+        experts[e * shape.stride:e * shape.stride + b.size] = b
+    bias = O.zipf_bias(31, S.stream(0, 0, S.ZIPF), E, 1.1)
+    norm_w = np.ones(H, np.float32)    # the descriptor keeps raw pointers: hold the arrays
+    d = moe_desc(E, k, H, F, router, experts, shape.gate_size, shape.down_size,
+                 shared_off=E * shape.stride if shared else None, bias=bias, norm_w=norm_w)
+    d.expert_stride = shape.stride
+    want, oid, ow = O.moe_layer(d, x, O.MOE_NORM)
+    hn = O.rms_norm(x, norm_w, 1e-6).astype(np.float64)
+    assert np.array_equal(ids, oid)
+    ref = np.zeros(H)
+    for r, e in enumerate(list(oid) + ([E] if shared else [])):
+        G, U, D = (O.dequantize(t, m, n).reshape(rr, cc).astype(np.float64) for t, m, n, rr, cc in
+                   ((O.Q4_K, blobs[e][0], F * H, F, H), (O.Q4_K, blobs[e][1], F * H, F, H),
+                    (O.Q6_K, blobs[e][2], H * F, H, F)))
+        g = G @ hn
+        ref += (float(ow[r]) if r < k else 1.0) * (D @ (g / (1 + np.exp(-g)) * (U @ hn)))
+    e = parity_err(got, ref)
+    say(f"  parity_err(fp64) {e:.3e} inf_rel(fp32 oracle) {inf_rel(got, want):.3e}")
+    assert e <= TOL
+    assert inf_rel(got, want) < 1e-5
+
+
 def test_moe_layer_config3_full(gpu):
     """BASELINE config 3 at full size: 512 experts (Q4_K gate/up 1024x4096, Q6_K
     down 4096x1024) + shared, top-10, generated in HBM; the oracle rebuilds the
