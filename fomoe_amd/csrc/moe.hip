@@ -34,6 +34,11 @@ namespace fo {
 // ------------------------------------------------------------ wave primitives
 FO_DEV float wave_sum_dpp(float v) { return group_sum<kWave>(v); }
 
+// Prepare one group of G values held one per lane in lanes [0, G) of a wave
+// (G = 16 or 32): exponent from the group maximum, three balanced int8 limbs
+// per value packed four values per dword, {2^-e, fp32 sum}. Layout as in
+// formats.h. `dst` points at the vector's limb area, `ss` at its {scale,sum}
+// area, g is the group index.
 template <int G>
 FO_DEV void prep_group_lanes(float val, int g, uint8_t *__restrict__ dst, uint8_t *__restrict__ ss) {
     const int lane = threadIdx.x & 63;

@@ -80,10 +80,4 @@ FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *s_ids
     if (lane < k) { s_ids[lane] = my_i; if (s_w) s_w[lane] = e * inv; }
 }
 
-// Prepare one group of G values held one per lane in lanes [0, G) of a wave
-// (G = 16 or 32): exponent from the group maximum, four balanced int8 limbs
-// per value packed four values per dword, {2^-e, fp32 sum}. Layout as in
-// formats.h. `dst` points at the vector's limb area, `ss` at its {scale,sum}
-// area, g is the group index.
-
 }  // namespace fo
