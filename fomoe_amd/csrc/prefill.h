@@ -11,7 +11,7 @@ namespace fo {
 
 constexpr int kPfMT = 64;        // tokens per GEMM tile (4 MFMA row blocks of 16)
 constexpr int kPfGateWaves = 16;                  // gate/up work-group: 8 gate + 8 up waves
-constexpr int kPfGateRows = 16 * kPfGateWaves / 2; // F rows per gate/up work-group
+constexpr int kPfGateRows = 32 * kPfGateWaves / 2; // F rows per gate/up work-group (32 per wave)
 
 struct PrefillArgs {
     // layer

@@ -11,7 +11,7 @@
 //                    prefixes — deterministic, no global atomics), the shared
 //                    expert's T pairs after them, and the GEMM tile list
 //                    {expert, first pair, n <= 64}.
-//   P4 k_pf_gateup   per (tile, 64 rows of F): act = silu(X Wg^T) * (X Wu^T)
+//   P4 k_pf_gateup   per (tile, 256 rows of F): act = silu(X Wg^T) * (X Wu^T)
 //                    with X the tile's gathered bf16 token rows and the weights
 //                    dequantized in registers straight into the MFMA B operand
 //                    (bf16, round-to-nearest-even of the exact fp32 value);
@@ -21,7 +21,7 @@
 //                    while super-block kb is multiplied. act is stored as two
 //                    bf16 planes hi = bf16(act), lo = bf16(act - hi)
 //                    (|act - hi - lo| <= 2^-18 |act|).
-//   P5 k_pf_down     per (tile, 128 rows of H): outp = act Wd^T, same scheme,
+//   P5 k_pf_down     per (tile, 256 rows of H): outp = act Wd^T, same scheme,
 //                    two MFMAs (hi, lo) per weight operand, so the intermediate
 //                    keeps ~fp32 precision and no result hinges on which side of
 //                    a bf16 rounding boundary an fp32 sum landed.
@@ -310,77 +310,92 @@ __global__ __launch_bounds__(kPfGateWaves * 64) void k_pf_gateup(PrefillArgs a) 
     const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
     constexpr int HW = kPfGateWaves / 2;
     const bool is_up = wave >= HW;
-    const int rl = 16 * (wave % HW) + col;                // row within the WG's kPfGateRows
+    const int rl = 32 * (wave % HW) + col;                // rows rl, rl + 16 within the WG's kPfGateRows
     const int row = blockIdx.x * kPfGateRows + rl;
     const int nb = (n + 15) >> 4, NK = a.H / 256;
     const int32_t *toks = a.pair_tok + p0;
     auto xrow = [&](int m) { return a.x + (uint64_t)toks[m] * a.H; };
-    f32x4 acc[4];
+    f32x4 acc[2][4];
 #pragma unroll
-    for (int b = 0; b < 4; b++) acc[b] = (f32x4){0, 0, 0, 0};
-    auto run = [&](auto dec, const uint8_t *wrow) {
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
+    auto run = [&](auto dec, const uint8_t *w0, uint64_t rowb) {
         using D = decltype(dec);
+        const uint8_t *w1 = w0 + 16 * rowb;
         pf_stage_async(xs, n, 0, xrow);
-        auto s_next = D::load(wrow, kg);
+        auto s0_next = D::load(w0, kg);
+        auto s1_next = D::load(w1, kg);
         for (int kb = 0; kb < NK; kb++) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();                              // tile kb in LDS; buffer kb-1 free
-            const auto sw = s_next;
+            const auto s0 = s0_next;
+            const auto s1 = s1_next;
             if (kb + 1 < NK) {
                 pf_stage_async(xs + ((kb + 1) & 1) * kPfTile, n, (kb + 1) * 256, xrow);
-                s_next = D::load(wrow + (uint64_t)(kb + 1) * D::BLOCK, kg);
+                s0_next = D::load(w0 + (uint64_t)(kb + 1) * D::BLOCK, kg);
+                s1_next = D::load(w1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
             }
             const uint16_t *xb = xs + (kb & 1) * kPfTile;
 #pragma unroll
             for (int ch = 0; ch < 8; ch++) {
-                const bf16x8 bw = as_bf16x8(pf_decode<D::TYPE>(sw, ch, kg));
+                const bf16x8 b0 = as_bf16x8(pf_decode<D::TYPE>(s0, ch, kg));
+                const bf16x8 b1 = as_bf16x8(pf_decode<D::TYPE>(s1, ch, kg));
 #pragma unroll
                 for (int b = 0; b < 4; b++)
-                    if (b < nb)
-                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            *(const bf16x8 *)(xb + pf_swz(16 * b + col, 4 * ch + kg)), bw, acc[b], 0, 0, 0);
+                    if (b < nb) {
+                        const bf16x8 av = *(const bf16x8 *)(xb + pf_swz(16 * b + col, 4 * ch + kg));
+                        acc[0][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b0, acc[0][b], 0, 0, 0);
+                        acc[1][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, acc[1][b], 0, 0, 0);
+                    }
             }
         }
     };
     if (!is_up) {
-        run(PfDec<GT>{}, blob + (uint64_t)row * ((uint64_t)NK * PfDec<GT>::BLOCK));
+        const uint64_t rb = (uint64_t)NK * PfDec<GT>::BLOCK;
+        run(PfDec<GT>{}, blob + (uint64_t)row * rb, rb);
     } else {
         const uint64_t up_off = shared ? a.sh_gate_size : a.gate_size;
-        run(PfDec<UT>{}, blob + up_off + (uint64_t)row * ((uint64_t)NK * PfDec<UT>::BLOCK));
+        const uint64_t rb = (uint64_t)NK * PfDec<UT>::BLOCK;
+        run(PfDec<UT>{}, blob + up_off + (uint64_t)row * rb, rb);
     }
     __syncthreads();                                      // all reads of xs done: reuse it
     float *ub = (float *)xs;                              // [64 tokens][kPfGateRows] up sums
     if (is_up) {
 #pragma unroll
-        for (int b = 0; b < 4; b++)
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) ub[(16 * b + 4 * kg + i) * kPfGateRows + rl] = acc[b][i];
+            for (int b = 0; b < 4; b++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) ub[(16 * b + 4 * kg + i) * kPfGateRows + rl + 16 * h] = acc[h][b][i];
     }
     __syncthreads();
     if (!is_up) {
         // D layout: lane holds rows 4*(lane/16)+i (tokens) of column lane%16 (weight row);
         // the activation is stored as hi/lo bf16 planes for the down projection
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            if (b >= nb) break;
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 16 * b + 4 * kg + i;
-                if (m < n) {
-                    const float g = acc[b][i], u = ub[m * kPfGateRows + rl];
-                    const float v = (g / (1.0f + expf(-g))) * u;
-                    const __bf16 hi = (__bf16)v;
-                    const __bf16 lo = (__bf16)(v - (float)hi);
-                    const uint64_t o = (uint64_t)(p0 + m) * a.F + row;
-                    a.act_hi[o] = __builtin_bit_cast(uint16_t, hi);
-                    a.act_lo[o] = __builtin_bit_cast(uint16_t, lo);
+            for (int b = 0; b < 4; b++) {
+                if (b >= nb) break;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = 16 * b + 4 * kg + i;
+                    if (m < n) {
+                        const float g = acc[h][b][i], u = ub[m * kPfGateRows + rl + 16 * h];
+                        const float v = (g / (1.0f + expf(-g))) * u;
+                        const __bf16 hi = (__bf16)v;
+                        const __bf16 lo = (__bf16)(v - (float)hi);
+                        const uint64_t o = (uint64_t)(p0 + m) * a.F + row + 16 * h;
+                        a.act_hi[o] = __builtin_bit_cast(uint16_t, hi);
+                        a.act_lo[o] = __builtin_bit_cast(uint16_t, lo);
+                    }
                 }
             }
-        }
     }
 }
 
-constexpr int kPfDownWaves = 8;                   // 128 weight rows per work-group
+constexpr int kPfDownWaves = 8;                   // 8 waves x 32 rows = 256 weight rows per work-group
 
 template <int DT>
 __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
@@ -392,13 +407,15 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
     const bool shared = e == a.E;
     const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
     const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
-    const int row = blockIdx.x * (16 * kPfDownWaves) + 16 * wave + col;
+    const int row = blockIdx.x * (32 * kPfDownWaves) + 32 * wave + col;   // rows row, row + 16
     const uint64_t db = (uint64_t)(a.F / 256) * PfDec<DT>::BLOCK;
-    const uint8_t *drow = blob + down_off + (uint64_t)row * db;
+    const uint8_t *drow = blob + down_off + (uint64_t)row * db, *drow1 = drow + 16 * db;
     const int nb = (n + 15) >> 4, NK = a.F / 256;
-    f32x4 acc[4];
+    f32x4 acc[2][4];
 #pragma unroll
-    for (int b = 0; b < 4; b++) acc[b] = (f32x4){0, 0, 0, 0};
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
     auto stage = [&](int kb) {   // first half of the waves stages hi, second half lo
         constexpr int HW = kPfDownWaves / 2;
         uint16_t *buf = dxs + (kb & 1) * 2 * kPfTile + (wave / HW) * kPfTile;
@@ -413,38 +430,47 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
         }
     };
     stage(0);
-    auto sd_next = PfDec<DT>::load(drow, kg);
+    auto s0_next = PfDec<DT>::load(drow, kg);
+    auto s1_next = PfDec<DT>::load(drow1, kg);
     for (int kb = 0; kb < NK; kb++) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        const auto sd = sd_next;
+        const auto s0 = s0_next;
+        const auto s1 = s1_next;
         if (kb + 1 < NK) {
             stage(kb + 1);
-            sd_next = PfDec<DT>::load(drow + (uint64_t)(kb + 1) * PfDec<DT>::BLOCK, kg);
+            s0_next = PfDec<DT>::load(drow + (uint64_t)(kb + 1) * PfDec<DT>::BLOCK, kg);
+            s1_next = PfDec<DT>::load(drow1 + (uint64_t)(kb + 1) * PfDec<DT>::BLOCK, kg);
         }
         const uint16_t *xh = dxs + (kb & 1) * 2 * kPfTile, *xl = xh + kPfTile;
 #pragma unroll
         for (int ch = 0; ch < 8; ch++) {
-            const bf16x8 bd = as_bf16x8(pf_decode<DT>(sd, ch, kg));
+            const bf16x8 b0 = as_bf16x8(pf_decode<DT>(s0, ch, kg));
+            const bf16x8 b1 = as_bf16x8(pf_decode<DT>(s1, ch, kg));
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 if (b < nb) {
                     const int o = pf_swz(16 * b + col, 4 * ch + kg);
-                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(xh + o), bd, acc[b], 0, 0, 0);
-                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(xl + o), bd, acc[b], 0, 0, 0);
+                    const bf16x8 ah = *(const bf16x8 *)(xh + o), al = *(const bf16x8 *)(xl + o);
+                    acc[0][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b0, acc[0][b], 0, 0, 0);
+                    acc[0][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b0, acc[0][b], 0, 0, 0);
+                    acc[1][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b1, acc[1][b], 0, 0, 0);
+                    acc[1][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b1, acc[1][b], 0, 0, 0);
                 }
             }
         }
     }
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        if (b >= nb) break;
+    for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 16 * b + 4 * kg + i;
-            if (m < n) a.outp[(uint64_t)(p0 + m) * a.H + row] = acc[b][i];
+        for (int b = 0; b < 4; b++) {
+            if (b >= nb) break;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * b + 4 * kg + i;
+                if (m < n) a.outp[(uint64_t)(p0 + m) * a.H + row + 16 * h] = acc[h][b][i];
+            }
         }
-    }
 }
 #pragma clang fp contract(on)
 
@@ -486,7 +512,7 @@ hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
                      (a.down_type == GGML_TYPE_Q4_K || a.down_type == GGML_TYPE_Q6_K);
     const int W = (a.T + 31) / 32;
     if (!okt || a.T <= 0 || a.E <= 0 || a.E > 1023 || a.k <= 0 || a.k > a.E || a.k > kMaxK ||
-        a.H <= 0 || a.H % 256 || a.H % (16 * kPfDownWaves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
+        a.H <= 0 || a.H % 256 || a.H % (32 * kPfDownWaves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
         a.max_tiles < prefill_max_tiles(a.T, a.k, a.E, a.shared != nullptr))
         return hipErrorInvalidValue;
     k_pf_router<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 256, 0, s>>>(a);
@@ -508,7 +534,7 @@ hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
     if (err != hipSuccess) return err;
     {
         const size_t lds = 4 * (size_t)kPfTile * sizeof(uint16_t);       // 128 KiB
-        const dim3 grid(a.H / (16 * kPfDownWaves), a.max_tiles);
+        const dim3 grid(a.H / (32 * kPfDownWaves), a.max_tiles);
         static bool down_attr = false;
         if (!down_attr) {
             hipError_t e1 = hipFuncSetAttribute((const void *)k_pf_down<GGML_TYPE_Q4_K>,
