@@ -60,10 +60,17 @@ def rotation(gpu, t, M, K, wseed, xseed, n_mats, steps, warmup):
     for _ in range(steps):
         gpu.matvec_batched(t, dW, stride, n_mats, dx, 0, dy, M, M, K)
     ms = gpu.timer_stop() / steps
+    # per-launch spread, from separately timed launches after the timed region
+    each = []
+    for _ in range(max(steps, 10)):
+        gpu.timer_start()
+        gpu.matvec_batched(t, dW, stride, n_mats, dx, 0, dy, M, M, K)
+        each.append(gpu.timer_stop())
+    p10, p50, p90 = np.percentile(each, [10, 50, 90])
     bytes_per_mat = rb + 4 * K + 4 * M        # weights + x + y, each counted once per launch
     total = bytes_per_mat * n_mats
     res = {"ms_per_step": ms, "bytes_per_step": total, "GB/s": total / ms / 1e6,
-           "weight_bytes": rb * n_mats}
+           "weight_bytes": rb * n_mats, "launch_ms_p10": p10, "launch_ms_p50": p50, "launch_ms_p90": p90}
     res["frac_hbm"] = res["GB/s"] / HBM_PEAK_GBS
     keep = (dW, dx, dy, stride)
     return res, keep
@@ -111,7 +118,64 @@ def cpu_baseline(gpu, dW, stride, M, K, t, seconds):
                       f"{n_s} of the rotation's matrices, {dt:.1f} s; CPU {cpu}"}
 
 
-def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0):
+def cpu_layer_baseline(gpu, layers, shape, seconds, n_sample=4):
+    """The reference CPU MoE layer (inference.c:484-596 with the cpu_expert.c
+    engine: fp32 router mat_vec_mul, softmax, top_k, renormalise, then
+    cpu_expert_ffn per routed expert and for the shared expert) timed on a
+    sample of the stack's layers. Only the experts each layer selects for the
+    config-3 input are copied to the host (the GPU's routing is the same); the
+    CPU still computes its own router every call and looks its experts up."""
+    import ctypes as C
+    import oracle as O
+    R = O.load_ref()
+    if R is None:
+        return None
+    E, H, F, k = shape.n_experts, shape.n_embd, shape.inter, shape.k
+    h = S.hidden(gpu, H)
+    out = gpu.alloc(4 * H)
+    x = gpu.download(h, np.float32, H)
+    sample = []
+    for L in layers[:n_sample]:
+        gpu.moe_layer(L.desc, h, out, 0)
+        ids, _, _ = gpu.last_routing(k)
+        router = gpu.download(L.desc.router, np.float32, E * H)
+        bias = gpu.download(L.desc.router_bias, np.float32, E) if L.desc.router_bias else np.zeros(E, np.float32)
+        blobs = {int(e): gpu.download(L.desc.experts + int(e) * shape.stride, np.uint8, shape.expert_bytes())
+                 for e in ids}
+        shared = gpu.download(L.desc.shared, np.uint8, shape.expert_bytes())
+        sample.append((router, bias, blobs, shared))
+    ctx = R.cpu_expert_create(H, F)
+    logits = np.empty(E, np.float32)
+    cids = np.empty(16, np.int32)
+    csc = np.empty(16, np.float32)
+    gs = shape.gate_size
+
+    def layer(router, bias, blobs, shared):
+        R.mat_vec_mul(logits.ctypes.data, router.ctypes.data, FA.F32, x.ctypes.data, E, H)
+        logits[:] += bias
+        R.softmax(logits.ctypes.data, E)
+        R.top_k(logits.ctypes.data, E, k, cids.ctypes.data, csc.ctypes.data)
+        sc = csc[:k] / csc[:k].sum()
+        R.cpu_expert_reset(ctx)
+        for i in range(k):
+            R.cpu_expert_ffn(ctx, blobs[int(cids[i])].ctypes.data, x.ctypes.data, float(sc[i]),
+                             shape.gate_type, shape.gate_type, shape.down_type, gs, gs)
+        R.cpu_expert_ffn(ctx, shared.ctypes.data, x.ctypes.data, 1.0,
+                         shape.gate_type, shape.gate_type, shape.down_type, gs, gs)
+
+    layer(*sample[0])
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        layer(*sample[n % len(sample)])
+        n += 1
+    dt = time.perf_counter() - t0
+    R.cpu_expert_free(ctx)
+    return {"cpu_layer_us": round(dt / n * 1e6, 1), "cpu_layer_calls": n, "cpu_layer_sample_layers": len(sample),
+            "cpu_layer_threads": int(os.environ.get("OMP_NUM_THREADS", "16"))}
+
+
+def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0, cpu_seconds=0.0):
     shape = S.LayerShape()
     t0 = time.perf_counter()
     layers = []
@@ -147,6 +211,11 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0)
     tok_s = stack_steps / (ms / 1e3)
     us_layer = ms * 1e3 / (stack_steps * n_layers)
     res = prefill_config5(gpu, layers[0], shape, prefill_reps) if prefill_reps > 0 else {}
+    if cpu_seconds > 0:
+        cl = cpu_layer_baseline(gpu, layers, shape, cpu_seconds)
+        if cl:
+            res.update(cl)
+            res["config3_speedup_vs_cpu_layer"] = round(cl["cpu_layer_us"] / us_layer_call, 1)
     return {**res,
         "config3_us_per_layer_call": round(us_layer_call, 2),
         "config4_layers": n_layers, "config4_steps": stack_steps,
@@ -230,7 +299,8 @@ def main():
     if "stack" not in skip and args.stack_layers > 0:
         del keep6
         extra.update(moe_layer_and_stack(gpu, args.stack_layers, args.stack_steps, args.layer_calls,
-                                         0 if "prefill" in skip else args.prefill_reps))
+                                         0 if "prefill" in skip else args.prefill_reps,
+                                         0.0 if "cpu" in skip else args.cpu_seconds / 2))
         log(f"stack: {extra['config4_tok_per_s']} tok/s, {extra['config4_us_per_layer']} us/layer")
         if "config5_ms" in extra:
             log(f"prefill: {extra['config5_ms']} ms per 512 tokens, {extra['config5_TFLOP/s']} TFLOP/s, "

@@ -48,6 +48,26 @@ SIGNATURES = {
     "gpu_qmoe_read_index": (C.c_int, [C.c_char_p, _vp, _vp, C.c_int, C.POINTER(C.c_char_p)]),
     "gpu_qmoe_upload_layer": (C.c_int, [_vp, C.c_char_p, C.c_int, _vp, C.c_uint64]),
     "gpu_qmoe_layer_desc": (C.c_int, [_vp, _vp, _vp]),
+    "gpu_gguf_open": (_vp, [C.c_char_p, C.POINTER(C.c_char_p)]),
+    "gpu_gguf_close": (None, [_vp]),
+    "gpu_gguf_n_tensors": (C.c_int64, [_vp]),
+    "gpu_gguf_n_keys": (C.c_int64, [_vp]),
+    "gpu_gguf_find_tensor": (C.c_int64, [_vp, C.c_char_p]),
+    "gpu_gguf_tensor_info": (C.c_int, [_vp, C.c_int64, _vp]),
+    "gpu_gguf_find_key": (C.c_int64, [_vp, C.c_char_p]),
+    "gpu_gguf_key": (C.c_char_p, [_vp, C.c_int64, C.POINTER(C.c_int)]),
+    "gpu_gguf_get_int": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int64)]),
+    "gpu_gguf_get_float": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double)]),
+    "gpu_gguf_get_str": (C.c_char_p, [_vp, C.c_char_p]),
+    "gpu_gguf_get_arr": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_uint64),
+                                   C.POINTER(_vp)]),
+    "gpu_gguf_get_arr_str": (C.c_char_p, [_vp, C.c_char_p, C.c_uint64]),
+    "gpu_gguf_type_bytes": (C.c_uint64, [C.c_int, C.c_uint64]),
+    "gpu_gguf_read_tensor": (C.c_int64, [_vp, C.c_int64, _vp, C.c_uint64]),
+    "gpu_gguf_upload_tensor": (C.c_int, [_vp, _vp, C.c_int64, _vp, C.c_uint64]),
+    "gpu_gguf_upload_f32": (C.c_int, [_vp, _vp, C.c_int64, _vp, C.c_int64]),
+    "gpu_gguf_load_moe_layer": (C.c_int, [_vp, _vp, C.c_int, _vp]),
+    "gpu_gguf_free_moe_layer": (None, [_vp, _vp]),
     "gpu_moe_prefill": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp, C.c_int]),
     "gpu_moe_prefill_routing": (C.c_int, [_vp, _vp, _vp]),
     "gpu_f32_to_bf16": (C.c_int, [_vp, _vp, _vp, C.c_int64]),
@@ -115,6 +135,91 @@ def qmoe_read_index(path: str, lib=None):
     layers = (QmoeLayerEntry * n)()
     lib.gpu_qmoe_read_index(path.encode(), C.byref(h), layers, n, C.byref(err))
     return h, list(layers)
+
+
+class GgufTensorInfo(C.Structure):
+    """gpu_gguf_tensor_t (include/gpu.h)."""
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_uint32), ("type", C.c_int32),
+                ("dims", C.c_int64 * 4), ("offset", C.c_uint64), ("size", C.c_uint64),
+                ("split", C.c_int32), ("pad", C.c_int32)]
+
+
+class Gguf:
+    """A GGUF model file opened through the library's reader (host only)."""
+
+    def __init__(self, path: str, lib=None):
+        self.lib = lib or load_library()
+        err = C.c_char_p()
+        self.h = self.lib.gpu_gguf_open(path.encode(), C.byref(err))
+        if not self.h:
+            raise RuntimeError(err.value.decode())
+
+    def close(self):
+        if self.h:
+            self.lib.gpu_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def tensors(self):
+        out = []
+        for i in range(self.lib.gpu_gguf_n_tensors(self.h)):
+            t = GgufTensorInfo()
+            assert self.lib.gpu_gguf_tensor_info(self.h, i, C.byref(t)) == 0
+            out.append({"name": t.name.decode(), "type": t.type, "dims": list(t.dims[:t.n_dims]),
+                        "offset": t.offset, "size": t.size, "split": t.split})
+        return out
+
+    def find_tensor(self, name: str) -> int:
+        return self.lib.gpu_gguf_find_tensor(self.h, name.encode())
+
+    def keys(self):
+        out = []
+        for i in range(self.lib.gpu_gguf_n_keys(self.h)):
+            ty = C.c_int()
+            out.append((self.lib.gpu_gguf_key(self.h, i, C.byref(ty)).decode(), ty.value))
+        return out
+
+    def get_int(self, key: str):
+        v = C.c_int64()
+        return v.value if self.lib.gpu_gguf_get_int(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def get_float(self, key: str):
+        v = C.c_double()
+        return v.value if self.lib.gpu_gguf_get_float(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def get_str(self, key: str):
+        v = self.lib.gpu_gguf_get_str(self.h, key.encode())
+        return None if v is None else v.decode()
+
+    def get_arr(self, key: str):
+        ty, n, data = C.c_int(), C.c_uint64(), _vp()
+        if self.lib.gpu_gguf_get_arr(self.h, key.encode(), C.byref(ty), C.byref(n), C.byref(data)) != 0:
+            return None
+        if ty.value == 8:
+            return [self.lib.gpu_gguf_get_arr_str(self.h, key.encode(), i).decode() for i in range(n.value)]
+        dt = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32,
+              6: np.float32, 7: np.int8, 10: np.uint64, 11: np.int64, 12: np.float64}[ty.value]
+        if n.value == 0:
+            return np.zeros(0, dt)
+        buf = (C.c_uint8 * (n.value * np.dtype(dt).itemsize)).from_address(data.value)
+        return np.frombuffer(bytes(buf), dt)
+
+    def read_tensor(self, i: int) -> np.ndarray:
+        t = GgufTensorInfo()
+        if self.lib.gpu_gguf_tensor_info(self.h, i, C.byref(t)) != 0:
+            raise IndexError(i)
+        out = np.empty(t.size, np.uint8)
+        if self.lib.gpu_gguf_read_tensor(self.h, i, out.ctypes.data, out.size) != t.size:
+            raise RuntimeError(f"gguf: reading tensor {i} failed")
+        return out
 
 
 class GpuError(RuntimeError):
@@ -237,6 +342,20 @@ class Gpu:
     def qmoe_layer_desc(self, hdr: "QmoeHeader", entry: "QmoeLayerEntry", layer: MoeLayer):
         self.check(self.lib.gpu_qmoe_layer_desc(C.byref(hdr), C.byref(entry), C.byref(layer)),
                    "gpu_qmoe_layer_desc")
+
+    def gguf_upload_tensor(self, g: Gguf, i: int, dst, nbytes: int):
+        self.check(self.lib.gpu_gguf_upload_tensor(self.ctx, g.h, i, _p(dst), nbytes), "gpu_gguf_upload_tensor")
+
+    def gguf_upload_f32(self, g: Gguf, i: int, dst, n: int):
+        self.check(self.lib.gpu_gguf_upload_f32(self.ctx, g.h, i, _p(dst), n), "gpu_gguf_upload_f32")
+
+    def gguf_load_moe_layer(self, g: Gguf, blk: int) -> MoeLayer:
+        L = MoeLayer()
+        self.check(self.lib.gpu_gguf_load_moe_layer(self.ctx, g.h, blk, C.byref(L)), "gpu_gguf_load_moe_layer")
+        return L
+
+    def gguf_free_moe_layer(self, L: MoeLayer):
+        self.lib.gpu_gguf_free_moe_layer(self.ctx, C.byref(L))
 
     def moe_prefill(self, layer: MoeLayer, x_bf16, n_tokens: int, out, flags: int = 0):
         self.check(self.lib.gpu_moe_prefill(self.ctx, C.byref(layer), _p(x_bf16), n_tokens, _p(out),

@@ -21,89 +21,9 @@
 #include "kernels.h"
 #include "moe.h"
 #include "prefill.h"
+#include "context.h"
 
 using namespace fo;
-
-struct gpu_ctx {
-    int device = 0;
-    int n_cu = 0;
-    uint64_t hbm = 0;
-    char arch[64] = {0};
-    hipStream_t stream = nullptr;
-    hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    std::string err;
-
-    // scratch (device)
-    float *logits = nullptr;       // [1024]
-    unsigned *counter = nullptr;   // router completion counter
-    int32_t *ids = nullptr;        // [16]
-    float *weights = nullptr;      // [17]
-    uint8_t *xq_h = nullptr;       size_t xq_h_cap = 0;
-    uint8_t *xq_act = nullptr;     size_t xq_act_cap = 0;
-    float *act = nullptr;          size_t act_cap = 0;
-    float *act2 = nullptr;         size_t act2_cap = 0;
-    float *vec_in = nullptr;       size_t vec_in_cap = 0;
-    float *vec_out = nullptr;      size_t vec_out_cap = 0;
-    uint8_t *staging = nullptr;    size_t staging_cap = 0;
-    int last_k = 0;
-    bool last_fast = false;      // routing of the last layer came from the K1-K3 path
-
-    // prefill workspace (grown on demand)
-    float *pf_logits = nullptr;    size_t pf_logits_cap = 0;
-    int32_t *pf_ids = nullptr;     size_t pf_ids_cap = 0;
-    float *pf_w = nullptr;         size_t pf_w_cap = 0;
-    int32_t *pf_pairpos = nullptr; size_t pf_pairpos_cap = 0;
-    int32_t *pf_pairtok = nullptr; size_t pf_pairtok_cap = 0;
-    int32_t *pf_tiles = nullptr;   size_t pf_tiles_cap = 0;
-    int32_t *pf_ntiles = nullptr;  size_t pf_ntiles_cap = 0;
-    uint16_t *pf_act = nullptr;    size_t pf_act_cap = 0;   // hi plane then lo plane
-    float *pf_outp = nullptr;      size_t pf_outp_cap = 0;
-    int pf_T = 0, pf_k = 0;
-
-    // pinned staging for host->device uploads of expert stores
-    uint8_t *pin[2] = {nullptr, nullptr};
-    hipEvent_t pin_ev[2] = {nullptr, nullptr};
-
-    // captured stack-decode graph
-    hipGraphExec_t graph_exec = nullptr;
-};
-
-static int fail(gpu_ctx *c, int code, const char *fmt, ...) {
-    if (c) {
-        char buf[512];
-        va_list ap;
-        va_start(ap, fmt);
-        vsnprintf(buf, sizeof buf, fmt, ap);
-        va_end(ap);
-        c->err = buf;
-    }
-    return code;
-}
-
-#define HIPC(call)                                                                         \
-    do {                                                                                   \
-        hipError_t e_ = (call);                                                            \
-        if (e_ != hipSuccess)                                                              \
-            return fail(ctx, e_ == hipErrorInvalidValue ? -1 : -2, "%s: %s (%s:%d)", #call, \
-                        hipGetErrorString(e_), __FILE__, __LINE__);                        \
-    } while (0)
-
-// Grow a device scratch buffer to at least `need` bytes (never inside a
-// captured region: callers size everything first).
-template <typename Tp>
-static hipError_t ensure(Tp *&p, size_t &cap, size_t need) {
-    if (cap >= need) return hipSuccess;
-    if (p) (void)hipFree(p);
-    p = nullptr;
-    cap = 0;
-    hipError_t e = hipMalloc((void **)&p, need);
-    if (e == hipSuccess) cap = need;
-    return e;
-}
-
-static bool kquant(int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K; }
-static bool layer_type(int t) { return kquant(t) || t == GGML_TYPE_Q8_0; }
-static bool matvec_type(int t) { return layer_type(t) || t == GGML_TYPE_MXFP4; }
 
 extern "C" {
 
@@ -575,11 +495,54 @@ int gpu_f32_to_bf16(gpu_ctx_t *ctx, const float *d_src, uint16_t *d_dst, int64_t
     return 0;
 }
 
+}  // extern "C"
+
+// ------------------------------------------------------------------ file staging
+constexpr size_t kPinChunk = 32u << 20;
+
+int file_to_device(gpu_ctx *ctx, int fd, uint64_t file_off, uint64_t bytes, uint8_t *dst, uint64_t seg,
+                   uint64_t dst_pitch, const char *what) {
+    if (seg == 0) return fail(ctx, -1, "%s: empty segment", what);
+    for (int b = 0; b < 2; b++) {
+        if (!ctx->pin[b]) HIPC(hipHostMalloc((void **)&ctx->pin[b], kPinChunk, hipHostMallocDefault));
+        if (!ctx->pin_ev[b]) HIPC(hipEventCreateWithFlags(&ctx->pin_ev[b], hipEventDisableTiming));
+    }
+    int rc = 0;
+    bool used[2] = {false, false};
+    uint64_t off = 0;
+    for (int b = 0; off < bytes && rc == 0; b ^= 1) {
+        const size_t n = (size_t)std::min<uint64_t>(kPinChunk, bytes - off);
+        if (used[b] && hipEventSynchronize(ctx->pin_ev[b]) != hipSuccess) { rc = -2; break; }
+        size_t got = 0;
+        while (got < n) {
+            const ssize_t r = pread(fd, ctx->pin[b] + got, n - got, (off_t)(file_off + off + got));
+            if (r <= 0) break;
+            got += (size_t)r;
+        }
+        if (got != n) { rc = fail(ctx, -1, "%s: short read at offset %llu", what, (unsigned long long)(file_off + off)); break; }
+        // the chunk's pieces, each inside one segment
+        for (uint64_t p = 0; p < n && rc == 0;) {
+            const uint64_t lb = off + p, s = lb / seg, w = lb % seg;
+            const uint64_t len = std::min<uint64_t>(n - p, seg - w);
+            if (hipMemcpyAsync(dst + s * dst_pitch + w, ctx->pin[b] + p, len, hipMemcpyHostToDevice, ctx->stream) != hipSuccess)
+                rc = -2;
+            p += len;
+        }
+        if (rc == 0 && hipEventRecord(ctx->pin_ev[b], ctx->stream) != hipSuccess) rc = -2;
+        used[b] = true;
+        off += n;
+    }
+    // copies still in flight read the pinned chunks: drain them on every path
+    const hipError_t se = hipStreamSynchronize(ctx->stream);
+    if (rc == -2 || se != hipSuccess) return fail(ctx, -2, "%s: device copy failed", what);
+    return rc;
+}
 
 // ------------------------------------------------------------------ expert store
 static_assert(sizeof(gpu_qmoe_header_t) == 64, "qmoe header is 64 bytes on disk");
 static_assert(sizeof(gpu_qmoe_layer_entry_t) == 32, "qmoe layer entry is 32 bytes on disk");
-constexpr size_t kPinChunk = 32u << 20;
+
+extern "C" {
 
 // Header and index of a .qmoe file (reference src/expert_store.c:11-100),
 // validated against the file size so that later reads stay inside it.
@@ -644,35 +607,10 @@ int gpu_qmoe_upload_layer(gpu_ctx_t *ctx, const char *path, int layer, void *d_d
     const uint64_t total = (uint64_t)h.n_experts * stride;
     if (dst_bytes < total) return fail(ctx, -1, "qmoe upload: destination %llu < %llu bytes",
                                        (unsigned long long)dst_bytes, (unsigned long long)total);
-    for (int b = 0; b < 2; b++) {
-        if (!ctx->pin[b]) HIPC(hipHostMalloc((void **)&ctx->pin[b], kPinChunk, hipHostMallocDefault));
-        if (!ctx->pin_ev[b]) HIPC(hipEventCreateWithFlags(&ctx->pin_ev[b], hipEventDisableTiming));
-    }
     const int fd = open(path, O_RDONLY);
     if (fd < 0) return fail(ctx, -1, "qmoe upload: cannot open %s", path);
-    // two pinned chunks alternate: the read of one overlaps the copy of the other
-    int rc = 0;
-    bool used[2] = {false, false};
-    uint64_t off = 0;
-    for (int b = 0; off < total && rc == 0; b ^= 1) {
-        const size_t n = (size_t)std::min<uint64_t>(kPinChunk, total - off);
-        if (used[b] && hipEventSynchronize(ctx->pin_ev[b]) != hipSuccess) { rc = -2; break; }
-        size_t got = 0;
-        while (got < n) {
-            const ssize_t r = pread(fd, ctx->pin[b] + got, n - got, (off_t)(idx[layer].data_offset + off + got));
-            if (r <= 0) break;
-            got += (size_t)r;
-        }
-        if (got != n) { rc = fail(ctx, -1, "qmoe upload: short read at offset %llu", (unsigned long long)off); break; }
-        if (hipMemcpyAsync((uint8_t *)d_dst + off, ctx->pin[b], n, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
-            hipEventRecord(ctx->pin_ev[b], ctx->stream) != hipSuccess) { rc = -2; break; }
-        used[b] = true;
-        off += n;
-    }
+    const int rc = file_to_device(ctx, fd, idx[layer].data_offset, total, (uint8_t *)d_dst, total, 0, "qmoe upload");
     close(fd);
-    // copies still in flight read the pinned chunks: drain them on every path
-    const hipError_t se = hipStreamSynchronize(ctx->stream);
-    if (rc == -2 || se != hipSuccess) return fail(ctx, -2, "qmoe upload: device copy failed");
     return rc;
 }
 

@@ -159,6 +159,73 @@ int gpu_qmoe_upload_layer(gpu_ctx_t *ctx, const char *path, int layer, void *d_d
 int gpu_qmoe_layer_desc(const gpu_qmoe_header_t *hdr, const gpu_qmoe_layer_entry_t *entry,
                         gpu_moe_layer_t *L);
 
+/* ---------------------------------------------------------------- GGUF model files
+ * Direct tensor loads from a GGUF model (replaces reference include/gguf.h:
+ * gguf_open 121, gguf_close 124, gguf_find_key 127, gguf_get_* 130-140,
+ * gguf_find_tensor 143, gguf_read_tensor 147, gguf_tensor_nbytes 150; format
+ * and split-file rules of src/gguf.c:10-449). The handle is host-only and
+ * read-only after open, so one handle may serve several contexts. */
+typedef struct gpu_gguf gpu_gguf_t;
+typedef struct {
+    const char *name;          /* owned by the handle */
+    uint32_t n_dims;
+    int32_t type;              /* enum ggml_dtype id */
+    int64_t dims[4];           /* ggml order: dims[0] is the contiguous one; unused = 1 */
+    uint64_t offset;           /* within its split's data section */
+    uint64_t size;             /* bytes, whole blocks (0: type of unknown size) */
+    int32_t split;             /* index of the split file holding the data */
+    int32_t pad;
+} gpu_gguf_tensor_t;
+/* Host only. Open and parse a GGUF file; a name with "-00001-of-0000N" also
+ * reads the other splits (missing ones are skipped, as the reference does).
+ * NULL on an unreadable or malformed file, *err (may be NULL) says why; the
+ * message stays valid until the next failing call on this thread. */
+gpu_gguf_t *gpu_gguf_open(const char *path, const char **err);
+void gpu_gguf_close(gpu_gguf_t *g);
+int64_t gpu_gguf_n_tensors(const gpu_gguf_t *g);
+int64_t gpu_gguf_n_keys(const gpu_gguf_t *g);
+int64_t gpu_gguf_find_tensor(const gpu_gguf_t *g, const char *name);   /* -1: absent */
+int gpu_gguf_tensor_info(const gpu_gguf_t *g, int64_t id, gpu_gguf_tensor_t *out);  /* 0 / -1 */
+int64_t gpu_gguf_find_key(const gpu_gguf_t *g, const char *key);       /* -1: absent */
+/* Key i: name and gguf value type (8 string, 9 array, ...); NULL if out of range. */
+const char *gpu_gguf_key(const gpu_gguf_t *g, int64_t i, int *type);
+/* Typed getters: 0, or -1 when the key is absent or of another kind (any
+ * integer or bool type reads as int, f32/f64 and integers as double). */
+int gpu_gguf_get_int(const gpu_gguf_t *g, const char *key, int64_t *v);
+int gpu_gguf_get_float(const gpu_gguf_t *g, const char *key, double *v);
+const char *gpu_gguf_get_str(const gpu_gguf_t *g, const char *key);      /* NULL: absent */
+/* Array key: element type and count, and the raw elements (NULL for a string
+ * array; use gpu_gguf_get_arr_str). -1: absent or not an array. */
+int gpu_gguf_get_arr(const gpu_gguf_t *g, const char *key, int *elem_type, uint64_t *n,
+                     const void **data);
+const char *gpu_gguf_get_arr_str(const gpu_gguf_t *g, const char *key, uint64_t i);
+/* Bytes of n elements of a ggml type (whole blocks), 0 for an unknown type. */
+uint64_t gpu_gguf_type_bytes(int type, uint64_t n);
+/* Host only: copy tensor id into h_dst (bytes >= its size). Returns the size
+ * read, or -1 (bad id, small buffer, data past the end of its file). */
+int64_t gpu_gguf_read_tensor(const gpu_gguf_t *g, int64_t id, void *h_dst, uint64_t bytes);
+/* Copy tensor id into device memory d_dst (sync, pinned staging). 0 / -1 / -2. */
+int gpu_gguf_upload_tensor(gpu_ctx_t *ctx, const gpu_gguf_t *g, int64_t id, void *d_dst,
+                           uint64_t dst_bytes);
+/* Upload tensor id as fp32 into d_dst [n elements] (sync): F32 as is, F16 /
+ * BF16 widened, Q4_K/Q5_K/Q6_K/Q8_0/MXFP4 dequantized bit-exactly (the
+ * conversions of reference src/model.c:42-87). 0 / -1 / -2. */
+int gpu_gguf_upload_f32(gpu_ctx_t *ctx, const gpu_gguf_t *g, int64_t id, float *d_dst, int64_t n);
+/* Make MoE block `blk` resident (sync): allocates and fills the experts
+ * ([E x stride] gate|up|down, stride = gate+up+down rounded up to 4096, the
+ * .qmoe layout built by reference tools/prepare_experts.c:107-133, 261-279)
+ * from blk.N.ffn_{gate,up,down}_exps.weight, the fp32 router
+ * (ffn_gate_inp), the shared expert (ffn_{gate,up,down}_shexp, optional) and
+ * its sigmoid gate vector (ffn_gate_inp_shexp, optional), and the RMSNorm
+ * weight (post_attention_norm, else ffn_norm; optional), and sets every field
+ * of *L: n_embd / inter / n_experts from the tensor shapes, k from
+ * {arch}.expert_used_count, eps from {arch}.attention.layer_norm_rms_epsilon
+ * (1e-6 if absent) (reference src/model.c:141-162, 349-371). Free with
+ * gpu_gguf_free_moe_layer. 0 / -1 (missing tensor, unsupported type or shape)
+ * / -2. */
+int gpu_gguf_load_moe_layer(gpu_ctx_t *ctx, const gpu_gguf_t *g, int blk, gpu_moe_layer_t *L);
+void gpu_gguf_free_moe_layer(gpu_ctx_t *ctx, gpu_moe_layer_t *L);
+
 /* ---------------------------------------------------------------- prefill
  * n_tokens tokens through one MoE layer at once (async): d_x [n_tokens x
  * n_embd] bf16, d_out [n_tokens x n_embd] fp32 (= x + ffn with
