@@ -61,6 +61,11 @@ FO_DEV void stage_lds(uint8_t *lds_dst, const uint8_t *g, uint32_t nbytes, int w
                                          (__attribute__((address_space(3))) void *)(lds_dst + off), 16, 0, 0);
     }
 }
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory
+// operations of this wave are outstanding and ignores the other counters.
+__host__ __device__ constexpr int vmcnt_le(int n) {
+    return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
 FO_DEV void stage_lds_wait() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();

@@ -79,8 +79,11 @@ FO_DEV void prep_group_lanes(float val, int g, uint8_t *__restrict__ dst, uint8_
 
 // ============================================================ K1: route
 // WG of 256 threads = 4 waves; WG b handles router rows 2b, 2b+1, each split
-// over two waves (half of H each). The weight loads are issued before the
-// norm so their latency overlaps it.
+// over two waves (half of H each). Every thread first requests its 2*UH
+// values of x and norm_w, then its UH float4 of router weights; the norm
+// waits only for the first requests (loads retire in issue order), so the
+// norm, the activation prep and the shared gate run while the weights are
+// in flight.
 template <int UH>  // H = 512*UH; a lane holds UH float4 of one half-row
 __global__ __launch_bounds__(256) void k_route(RouteArgs a) {
     extern __shared__ float sh[];             // h [H]
@@ -88,29 +91,35 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a) {
     __shared__ float red[4];
     const int H = a.H, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int row = 2 * blockIdx.x + (wv >> 1), half = wv & 1;
+    float2 xv[UH], nv[UH];
+#pragma unroll
+    for (int u = 0; u < UH; u++) xv[u] = ((const float2 *)a.x)[tid + 256 * u];
+    if (a.norm_w) {
+#pragma unroll
+        for (int u = 0; u < UH; u++) nv[u] = ((const float2 *)a.norm_w)[tid + 256 * u];
+    }
     float4 wr[UH];
     const bool has_row = row < a.E;
-    if (has_row) {
-        const float4 *rp = (const float4 *)(a.router + (uint64_t)row * H) + half * (H / 8);
+    const float4 *rp = (const float4 *)(a.router + (uint64_t)min(row, a.E - 1) * H) + half * (H / 8);
 #pragma unroll
-        for (int u = 0; u < UH; u++) wr[u] = rp[lane + 64 * u];
-    }
-    float *shw = sh + lds_round((uint64_t)H * 4) / 4;   // norm weight
-    stage_lds((uint8_t *)sh, (const uint8_t *)a.x, (uint32_t)H * 4, wv, 4);
-    if (a.norm_w) stage_lds((uint8_t *)shw, (const uint8_t *)a.norm_w, (uint32_t)H * 4, wv, 4);
-    stage_lds_wait();
+    for (int u = 0; u < UH; u++) wr[u] = rp[lane + 64 * u];
     if (a.norm_w) {
         float ss = 0.f;
-        for (int i = tid; i < H; i += 256) ss += sh[i] * sh[i];
+#pragma unroll
+        for (int u = 0; u < UH; u++) ss += xv[u].x * xv[u].x + xv[u].y * xv[u].y;
         ss = wave_sum_dpp(ss);
         if (lane == 0) red[wv] = ss;
         __syncthreads();
         const float tot = (red[0] + red[1]) + (red[2] + red[3]);
         const float scale = 1.0f / sqrtf(tot / (float)H + a.eps);
-        __syncthreads();
-        for (int i = tid; i < H; i += 256) sh[i] = sh[i] * scale * shw[i];
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < UH; u++)
+            *(float2 *)(sh + 2 * tid + 512 * u) = make_float2(xv[u].x * scale * nv[u].x, xv[u].y * scale * nv[u].y);
+    } else {
+#pragma unroll
+        for (int u = 0; u < UH; u++) *(float2 *)(sh + 2 * tid + 512 * u) = xv[u];
     }
+    __syncthreads();
     // this WG's share of the prepared h (groups of a.gsz values, one wave each)
     if (a.xq_h) {
         const int ng = H / a.gsz;
@@ -158,7 +167,7 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a) {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
     if (a.E <= 0 || a.E > kMaxE || a.H % 512 || a.H > 8192) return hipErrorInvalidValue;
     const int blocks = (a.E + 1) / 2;
-    const size_t lds = 2 * (size_t)lds_round((uint64_t)a.H * 4);
+    const size_t lds = (size_t)a.H * 4;
 #define FO_K1(U) if (a.H == 512 * U) { k_route<U><<<blocks, 256, lds, s>>>(a); return hipGetLastError(); }
     FO_K1(1) FO_K1(2) FO_K1(3) FO_K1(4) FO_K1(6) FO_K1(8) FO_K1(12) FO_K1(16)
 #undef FO_K1
@@ -191,7 +200,8 @@ __global__ __launch_bounds__((ExpandShape<T, TR, U>::THREADS), 3) void k_expand(
     constexpr int PASS = (RW + P - 1) / P;              // passes per wave
     extern __shared__ uint8_t lds[];                    // prepared h
     __shared__ int s_ids[kMaxK];
-    __shared__ float s_w[kMaxK];
+    __shared__ float s_w[kMaxK], s_val[kMaxK];
+    __shared__ float2 s_cand[64];
     __shared__ float s_act[TR];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, sub = lane / G;
     const int H = a.H, F_ = a.F;
@@ -207,8 +217,14 @@ __global__ __launch_bounds__((ExpandShape<T, TR, U>::THREADS), 3) void k_expand(
     const bool full = a.shared ? (e == a.k && rb == 0) : blockIdx.x == 0;
     const int rounds = full ? a.k : (routed ? e + 1 : 0);
     if (wv == 0 && rounds > 0) {
-        if (a.E <= 512) wave_topk<8>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
-        else wave_topk<16>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
+        // one or two selections: arg-max rounds; more: the threshold ranking
+        if (rounds <= 2) {
+            if (a.E <= 512) wave_topk<8>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
+            else wave_topk<16>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
+        } else {
+            if (a.E <= 512) wave_topk_thr<8>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr, s_cand, s_val);
+            else wave_topk_thr<16>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr, s_cand, s_val);
+        }
         if (full && lane < a.k) { a.ids[lane] = s_ids[lane]; a.weights[lane] = s_w[lane]; }
     }
     stage_lds_wait();
@@ -339,6 +355,90 @@ __global__ __launch_bounds__(1024) void k_reduce(ReduceArgs a) {
     }
 }
 
+// K3 with the weights staged through LDS: each wave streams its expert's
+// 16-row block (16 consecutive rows = 16 * RBYTES contiguous bytes) with
+// 1 KiB coalesced loads, writes the pieces to its own LDS area and runs the
+// same per-lane slot dots as k_reduce from there, P rows per pass: a pass
+// only waits for the pieces that cover its rows (loads retire in issue
+// order, and the activation slot is requested before the weights), so the
+// arithmetic of early rows overlaps the arrival of later ones. All n_tot
+// blocks of a work-group are resident at once (n_tot * 16 * RBYTES <=
+// kTileLdsMax).
+constexpr int kTileRows = 16;
+constexpr uint32_t kTileLdsMax = 152 * 1024;
+
+constexpr int kTileMaxWaves = 12;   // 3 waves per SIMD: room for a whole block in registers
+
+template <int T, int G, int RBYTES>
+__global__ __launch_bounds__(64 * kTileMaxWaves) void k_reduce_tile(ReduceArgs a) {
+    using F = Fmt<T>;
+    constexpr int P = kWave / G, RP = kTileRows / P;
+    constexpr uint32_t TB = kTileRows * RBYTES, TSTRIDE = (TB + 15) & ~15u;
+    constexpr int NV = (TB + 1023) / 1024;
+    extern __shared__ __attribute__((aligned(16))) uint8_t tiles[];
+    __shared__ float part[kMaxK + 1][kTileRows];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, sub = lane / G;
+    const int n_tot = a.k + (a.shared ? 1 : 0);
+    const int S = a.F / F::SLOT;
+    const int slot = min(lane % G, S - 1);          // lanes past S mirror the last slot ...
+    const float live = (lane % G) < S ? 1.f : 0.f;  // ... and contribute nothing
+    const int row0 = blockIdx.x * kTileRows;
+    if (wv < n_tot) {
+        const uint8_t *m = (wv < a.k) ? a.base + (uint64_t)a.ids[wv] * a.stride + a.down_off
+                                      : a.shared + a.sh_down_off;
+        typename F::X X;
+        int gi[F::NG];
+        F::groups(slot, gi);
+        load_xslot(X, a.xq_act + (uint64_t)wv * a.xq_vstride, a.F, gi);
+        const uint8_t *src = m + (uint64_t)row0 * RBYTES;
+        const uint32_t nb = (uint32_t)min(kTileRows, a.H - row0) * RBYTES;
+        // a piece that straddles the end is read from the last 16 valid bytes
+        // and written to that same position (identical bytes overlap)
+        auto pos = [&](uint32_t o) { return o + 16 <= nb ? o : nb - 16; };
+        uint4 v[NV];
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = ld16(src + pos(i * 1024 + lane * 16));
+        // keep the scheduler from sinking weight loads below the arithmetic
+        __builtin_amdgcn_sched_barrier(0);
+        uint8_t *dst = tiles + wv * TSTRIDE;
+        int written = 0;
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            const int need = ((p + 1) * P * RBYTES + 1023) / 1024;   // pieces covering rows < (p+1)*P
+#pragma unroll
+            for (int i = 0; i < NV; i++)
+                if (i >= written && i < need) *(uint4 *)(dst + pos(i * 1024 + lane * 16)) = v[i];
+            written = need;
+            const int r = p * P + sub;
+            const typename F::Raw raw = F::load(dst + r * RBYTES, slot);
+            const float d = group_sum<G>(live * F::dot(raw, slot, X));
+            if ((lane % G) == 0) part[wv][r] = d;
+        }
+    }
+    __syncthreads();
+    if (tid < kTileRows && row0 + tid < a.H) {
+        float acc = 0.f;
+        for (int e = 0; e < a.k; e++) acc = fmaf(a.weights[e], part[e][tid], acc);
+        if (a.shared) acc = fmaf(a.shared_w ? *a.shared_w : 1.0f, part[a.k][tid], acc);
+        a.out[row0 + tid] = (a.resid ? a.resid[row0 + tid] : 0.f) + acc;
+    }
+}
+
+template <int T, int G, int RBYTES>
+static hipError_t reduce_tile(const ReduceArgs &a, hipStream_t s) {
+    static bool attr = false;   // more than the 64 KiB default of dynamic LDS
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_reduce_tile<T, G, RBYTES>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTileLdsMax);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const int n_tot = a.k + (a.shared ? 1 : 0);
+    const uint32_t lds = n_tot * ((kTileRows * RBYTES + 15) & ~15u);
+    k_reduce_tile<T, G, RBYTES><<<(a.H + kTileRows - 1) / kTileRows, 64 * n_tot, lds, s>>>(a);
+    return hipGetLastError();
+}
+
 hipError_t launch_reduce(int type, const ReduceArgs &a, hipStream_t s, int n_cu) {
     (void)n_cu;
     const int slot = type == GGML_TYPE_Q8_0 ? 32 : 64;
@@ -347,6 +447,13 @@ hipError_t launch_reduce(int type, const ReduceArgs &a, hipStream_t s, int n_cu)
     const int S = a.F / slot;
     int G = 4;
     while (G < S) G <<= 1;
+    // the LDS-staged variant when all n_tot 16-row blocks fit at once
+    if (n_tot <= kTileMaxWaves && n_tot * kTileRows * a.row_bytes <= kTileLdsMax && a.H >= kTileRows &&
+        a.F == 1024) {
+        if (type == GGML_TYPE_Q6_K) return reduce_tile<GGML_TYPE_Q6_K, 16, 840>(a, s);
+        if (type == GGML_TYPE_Q4_K) return reduce_tile<GGML_TYPE_Q4_K, 16, 576>(a, s);
+        if (type == GGML_TYPE_Q5_K) return reduce_tile<GGML_TYPE_Q5_K, 16, 704>(a, s);
+    }
     constexpr int RP = 4;
     const int RB = (64 / G) * RP;
     const int grid = (a.H + RB - 1) / RB;

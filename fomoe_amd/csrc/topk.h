@@ -80,4 +80,97 @@ FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *s_ids
     if (lane < k) { s_ids[lane] = my_i; if (s_w) s_w[lane] = e * inv; }
 }
 
+// Same selection through a threshold: the 64 lane maxima are sorted across
+// the wave (a 21-step flip / half-cleaner network: DPP inside 16-lane rows,
+// three permutes across rows), so T = the k-th largest lane maximum; k lane
+// maxima are >= T, hence the top k of all E values are all >= T. The
+// candidates (every value >= T: k plus the few second-best values of the
+// same lanes) are compacted to LDS, twice in a row, and ranked exactly by
+// (value desc, index asc) against the next n-1 entries of that doubled list
+// with wave-wide DPP shifts. Falls back to k arg-max rounds when k > 16 or
+// more than 32 values tie in at T (or NaNs leave fewer than k candidates).
+// s_cand: 64 (value, index) slots, s_val: k values, both in LDS.
+template <int CTRL>
+FO_DEV float dpp_keep(float v) {   // lanes whose source is outside the row keep v
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+FO_DEV int dpp_keep_i(int v) { return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false); }
+
+template <int NV>
+FO_DEV void wave_topk_thr(const float *__restrict__ logits, int E, int k, int *s_ids, float *s_w,
+                          float2 *s_cand, float *s_val) {
+    const int lane = threadIdx.x & 63, r = lane & 15;
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = 64 * j + lane;
+        v[j] = i < E ? logits[i] : -FLT_MAX;
+    }
+    float mx = -FLT_MAX;
+#pragma unroll
+    for (int j = 0; j < NV; j++) mx = fmaxf(mx, v[j]);   // NaNs drop out
+    // descending sort of the lane maxima (lower lane = larger value)
+    auto cx = [&](float p, bool lo) { mx = lo ? fmaxf(mx, p) : fminf(mx, p); };
+    auto x4 = [&]() { const float u = dpp_keep<0x104>(mx), d = dpp_keep<0x114>(mx); cx((r & 4) ? d : u, !(r & 4)); };
+    auto x8 = [&]() { const float u = dpp_keep<0x108>(mx), d = dpp_keep<0x118>(mx); cx((r & 8) ? d : u, !(r & 8)); };
+    auto x2 = [&]() { cx(dpp_keep<0x4E>(mx), !(r & 2)); };
+    auto x1 = [&]() { cx(dpp_keep<0xB1>(mx), !(r & 1)); };
+    x1();                                                      // size 2
+    cx(dpp_keep<0x1B>(mx), !(r & 2)); x1();                    // size 4 (flip = quad mirror)
+    cx(dpp_keep<0x141>(mx), !(r & 4)); x2(); x1();             // size 8 (flip = half-row mirror)
+    cx(dpp_keep<0x140>(mx), !(r & 8)); x4(); x2(); x1();       // size 16 (flip = row mirror)
+    cx(__shfl_xor(mx, 31, kWave), !(lane & 16)); x8(); x4(); x2(); x1();                     // size 32
+    cx(__shfl_xor(mx, 63, kWave), !(lane & 32)); cx(__shfl_xor(mx, 16, kWave), !(lane & 16));
+    x8(); x4(); x2(); x1();                                    // size 64
+    bool ok = k <= 16;
+    int n = 0;
+    if (ok) {
+        const float T = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), k - 1));
+        uint64_t m[NV];
+#pragma unroll
+        for (int j = 0; j < NV; j++) { m[j] = __ballot(v[j] >= T); n += __popcll(m[j]); }
+        ok = n >= k && n <= 32;
+        if (ok) {   // candidates in (j, lane) order at [0, n) and again at [n, 2n)
+            int base = 0;
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m[j] >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m[j], 0u));
+                if (v[j] >= T) {
+                    const float2 cv = make_float2(v[j], __int_as_float(64 * j + lane));
+                    s_cand[pos] = cv;
+                    s_cand[pos + n] = cv;
+                }
+                base += __popcll(m[j]);
+            }
+        }
+    }
+    if (!ok) {
+        wave_topk<NV>(logits, E, k, s_ids, s_w);
+        return;
+    }
+    // lane l < n ranks candidate l against entries l+1 .. l+n-1 of the doubled list
+    const float2 c = lane < 2 * n ? s_cand[lane] : make_float2(-FLT_MAX, __int_as_float(0x7FFFFFFF));
+    const int ci = __float_as_int(c.y);
+    float ov = c.x;
+    int oi = ci, rank = 0;
+    for (int q = 1; q < n; q++) {
+        ov = dpp_keep<0x130>(ov);      // wave_shl:1 — lane l now sees entry l+q
+        oi = dpp_keep_i<0x130>(oi);
+        rank += (ov > c.x || (ov == c.x && oi < ci)) ? 1 : 0;
+    }
+    if (lane < n && rank < k) {
+        s_ids[rank] = (ci >= 0 && ci < E) ? ci : 0;
+        s_val[rank] = c.x;
+    }
+    if (s_w) {
+        const float my_v = lane < k ? s_val[lane] : -FLT_MAX;
+        const float m0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(my_v)));
+        const float e = lane < k ? expf(my_v - m0) : 0.f;
+        const float inv = 1.0f / group_sum<kWave>(e);
+        if (lane < k) s_w[lane] = e * inv;
+    }
+}
+
 }  // namespace fo

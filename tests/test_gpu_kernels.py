@@ -264,12 +264,62 @@ def test_moe_layer_norm_residual_gate(gpu):
     assert np.array_equal(got, (x + ffn).astype(np.float32))
 
 
+@pytest.mark.parametrize("case", ["ties", "ties40", "E300_k15", "k3"])
+def test_moe_layer_topk_ties_and_fallback(gpu, case):
+    """Expert selection inside the layer (one or two arg-max rounds per
+    work-group, the threshold ranking beyond that, its fallback when more than
+    32 values tie at the threshold) against the reference order: equal logits
+    (duplicated router rows give bit-identical logits) resolve to the lowest
+    index (reference src/tensor.c:226-252)."""
+    from fomoe_amd import synthetic as S
+    from test_oracle import moe_desc
+    E, k = (300, 15) if case == "E300_k15" else (512, 3 if case == "k3" else 10)
+    H, F = 512, 512
+    say(f"layer top-k {case}: E={E} k={k}")
+    shape = S.LayerShape(n_embd=H, inter=F, n_experts=E, k=k, shared=True)
+    L = S.build_layer(gpu, shape, 0, seed=41, zipf_s=None, norm=False)
+    router = O.synth_f32(41, S.stream(0, 0, S.ROUTER), 0.02, E * H).reshape(E, H).copy()
+    x = O.synth_f32(42, 0, 1.0, H)
+    order = np.argsort(-O.mat_vec(O.F32, router.reshape(-1), x, E, H), kind="stable")
+    if case == "ties40":     # 40 equal top logits: more ties at the threshold than lanes allow
+        router[100:140] = 3 * router[order[0]]
+    else:                    # groups of equal logits around the top and the selection boundary
+        for rank, dup in ((0, (1, 200)), (2, (3, 250, 299)), (k - 1, (0, 41, 42, 43))):
+            src = router[order[rank]].copy()
+            for d_ in dup:
+                router[d_] = src
+    router = np.ascontiguousarray(router.reshape(-1))
+    gpu.upload_to(L.desc.router, router)
+    dx, dout = gpu.upload(x), gpu.alloc(4 * H)
+    gpu.moe_layer(L.desc, dx, dout, 0)
+    got = gpu.download(dout, np.float32, H)
+    ids, w, _ = gpu.last_routing(k)
+    logits = O.mat_vec(O.F32, router, x, E, H)
+    sel, _ = O.top_k(O.softmax(logits), k)
+    experts = np.zeros((E + 1) * shape.stride, np.uint8)   # only the selected blobs are read
+    for e in list(sel) + [E]:
+        b = np.concatenate([O.synth_quant(O.Q4_K, 41, S.stream(0, e, S.GATE), 0.02, F, H),
+                            O.synth_quant(O.Q4_K, 41, S.stream(0, e, S.UP), 0.02, F, H),
+                            O.synth_quant(O.Q6_K, 41, S.stream(0, e, S.DOWN), 0.02, H, F)])
+        experts[e * shape.stride:e * shape.stride + b.size] = b
+    d = moe_desc(E, k, H, F, router, experts, shape.gate_size, shape.down_size, shared_off=E * shape.stride)
+    d.expert_stride = shape.stride
+    want, oid, ow = O.moe_layer(d, x, 0)
+    assert np.array_equal(oid, sel)
+    assert len(set(logits[oid].tolist())) < k    # ties are in play
+    assert np.array_equal(ids, oid), (ids, oid)
+    assert inf_rel(w, ow) < 1e-6
+    say(f"  inf_rel {inf_rel(got, want):.3e}")
+    assert inf_rel(got, want) < 1e-5
+
+
 @pytest.mark.parametrize("H,F,E,k,shared", [(512, 512, 16, 4, True), (1024, 1024, 24, 12, True),
                                              (512, 1024, 8, 3, False), (2048, 512, 16, 13, False)])
 def test_moe_layer_shapes_vs_fp64(gpu, H, F, E, k, shared):
-    """Layer shapes on both down-projection kernels (the tile-staged Q6_K one
-    for F = 512 / 1024 up to 13 experts per work-group), with RMSNorm and a
-    shared expert, against an fp64 recomposition and the fp32 oracle."""
+    """Layer shapes on both down-projection kernels (the LDS-staged one for
+    F = 1024 up to 12 experts per work-group, the direct one otherwise), with
+    RMSNorm and a shared expert, against an fp64 recomposition and the fp32
+    oracle."""
     from fomoe_amd import synthetic as S
     from test_oracle import moe_desc
     say(f"layer H={H} F={F} E={E} k={k} shared={shared}")
