@@ -18,7 +18,13 @@ struct MatvecArgs {
     float *y;               // y_m = y + m*y_stride
     uint64_t y_stride;
     int n_mats, M, K;
+    const float *xf;        // fp32 x_m = xf + m*xf_stride, for kernels that prepare it themselves
+    uint64_t xf_stride;
 };
+
+// True when launch_matvec's kernel for this shape prepares x itself from
+// MatvecArgs::xf (no separate activation-prep launch needed).
+bool matvec_self_prep(int type, uint64_t row_bytes, int K);
 
 // Router: logits = W_r . h (+ bias), h = rms_norm(x)*w when norm_w != NULL,
 // then (last work-group) softmax, top-k with lowest-index ties, renormalise,

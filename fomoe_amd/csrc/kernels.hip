@@ -17,18 +17,13 @@
 namespace fo {
 
 // ============================================================ activation prep
-// One thread per group of GSZ values: exponent from the group maximum, the
-// four balanced int8 limbs of X = round(x * 2^e), the scale 2^-e and the fp32
-// sum (layout in formats.h).
+// One group of GSZ values: exponent from the group maximum, the balanced int8
+// limbs of X = round(x * 2^e), the scale 2^-e and the fp32 sum (layout in
+// formats.h); limbs go to `lp` (kLimbs * GSZ bytes), {scale, sum} to `ss`.
+// Used by k_xprep (one thread per group) and by kernels that prepare their
+// own activation in LDS (one lane per group), bit-identically.
 template <int GSZ>
-__global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ x, uint64_t x_stride,
-                                               int K, int n_vec, uint8_t *__restrict__ xq,
-                                               uint64_t xq_stride) {
-    const int ng = K / GSZ;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (int64_t)ng * n_vec) return;
-    const int v = (int)(gid / ng), g = (int)(gid % ng);
-    const float *xp = x + (uint64_t)v * x_stride + (uint64_t)g * GSZ;
+FO_DEV void prep_group(const float *__restrict__ xp, uint8_t *lp8, uint8_t *ss) {
     float vals[GSZ];
     float M = 0.f, sum = 0.f;
 #pragma unroll
@@ -59,15 +54,27 @@ __global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ x, uint
         }
         limb[kLimbs - 1][i / 4] |= (uint32_t)(X & 0xFF) << (8 * (i % 4));
     }
-    uint8_t *out = xq + (uint64_t)v * xq_stride;
-    uint32_t *lp = (uint32_t *)(out + (uint64_t)g * (kLimbs * GSZ));
+    uint32_t *lp = (uint32_t *)lp8;
 #pragma unroll
     for (int L = 0; L < kLimbs; L++)
 #pragma unroll
         for (int k = 0; k < GSZ / 4; k += 4)
             *(uint4 *)(lp + L * (GSZ / 4) + k) =
                 make_uint4(limb[L][k], limb[L][k + 1], limb[L][k + 2], limb[L][k + 3]);
-    *(float2 *)(out + xq_limb_bytes(K) + (uint64_t)g * 8) = make_float2(scale, sum);
+    *(float2 *)ss = make_float2(scale, sum);
+}
+
+template <int GSZ>
+__global__ __launch_bounds__(256) void k_xprep(const float *__restrict__ x, uint64_t x_stride,
+                                               int K, int n_vec, uint8_t *__restrict__ xq,
+                                               uint64_t xq_stride) {
+    const int ng = K / GSZ;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (int64_t)ng * n_vec) return;
+    const int v = (int)(gid / ng), g = (int)(gid % ng);
+    uint8_t *out = xq + (uint64_t)v * xq_stride;
+    prep_group<GSZ>(x + (uint64_t)v * x_stride + (uint64_t)g * GSZ, out + (uint64_t)g * (kLimbs * GSZ),
+                    out + xq_limb_bytes(K) + (uint64_t)g * 8);
 }
 
 hipError_t launch_xprep(int gsz, const float *x, uint64_t x_stride, int K, int n_vec,
@@ -154,6 +161,17 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     L.init(lane, S);
     XRegs<T, U> X;
     int64_t cur = -1;
+    // Outputs collect in LDS (a wave's tasks are consecutive rows) and leave
+    // as one coalesced store per 64 rows: a 4-byte write per row between the
+    // weight reads costs read bandwidth (read/write turnarounds).
+    __shared__ float ybuf[4][kWave];
+    const int wv = threadIdx.x >> 6;
+    int64_t ym = -1;
+    int ybase = 0, ycount = 0;
+    auto flush = [&]() {
+        if (ycount > 0 && lane < ycount) a.y[ym * a.y_stride + ybase + lane] = ybuf[wv][lane];
+        ycount = 0;
+    };
     for (int64_t t = t0; t < t1; t++) {
         const int64_t m = t / tpm;
         const int rb = (int)(t - m * tpm);
@@ -166,13 +184,21 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
             const int row = min(rb * ROWS + r * P + sub, a.M - 1);
             load_row(raw[r], W + (uint64_t)row * a.row_bytes, L);
         }
+        const int row0 = rb * ROWS;
+        if (m != ym || row0 != ybase + ycount || ycount + ROWS > kWave) {
+            flush();
+            ym = m;
+            ybase = row0;
+        }
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float v = group_sum<G>(dot_row(raw[r], L, X));
-            const int row = rb * ROWS + r * P + sub;
-            if ((lane % G) == 0 && row < a.M) a.y[m * a.y_stride + row] = v;
+            const int row = row0 + r * P + sub;
+            if ((lane % G) == 0 && row < a.M) ybuf[wv][row - ybase] = v;
         }
+        ycount += min(ROWS, a.M - row0);
     }
+    flush();
 }
 
 // Slot geometry of a K-wide row: lanes per row G and slots per lane U.
@@ -235,6 +261,7 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
     constexpr uint32_t limb_bytes = 3u * K, xbytes = limb_bytes + (K / 16) * 8;
     constexpr uint32_t zoff = lds_round(xbytes);
     uint8_t *tb = sx + zoff + lds_round(limb_bytes);
+    float *ys = (float *)(tb + NV * 1024);             // [TPW * 16] results
     const uint8_t *Wm = a.W + mat * a.mat_stride;
     constexpr uint32_t rb = NSB * 210;                 // launched only for contiguous rows
     const int tile0 = blockIdx.x * TPW;
@@ -250,17 +277,23 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
 #pragma unroll
         for (int i = 0; i < NV; i++) v[i] = ld16(tp + pos(i * 1024 + lane * 16, nb));
     };
-    uint4 va[NV], vb[NV];
-    if (tile0 < ntiles) issue(va, tile0);
-    stage_lds(sx, a.xq + mat * a.x_stride, (xbytes + 15) & ~15u, 0, 1);
+    // one register buffer: tile t+1 is requested right after tile t has been
+    // copied to LDS, so its loads overlap tile t's arithmetic (measured faster
+    // than two buffers, which need more registers for no more overlap)
+    uint4 v[NV];
+    if (tile0 < ntiles) issue(v, tile0);
+    // the activation is prepared here, one lane per 16-value group (K <= 1024)
+    if (lane < K / 16) prep_group<16>(a.xf + mat * a.xf_stride + lane * 16, sx + lane * 48, sx + limb_bytes + lane * 8);
     for (uint32_t o = lane * 16; o < limb_bytes; o += 64 * 16) *(uint4 *)(sx + zoff + o) = make_uint4(0, 0, 0, 0);
-    stage_lds_wait();
+    __syncthreads();
     const int r = lane & 15, g = lane >> 4, n = g >> 1, j = g & 1, L = r & 3;
     const bool valid = (r >> 2) == g && L < 3;
     const uint8_t *abase = sx + (valid ? 0u : zoff) + (8 * n + j) * 48 + 16 * L;
     const uint8_t *ssb = sx + limb_bytes + (8 * n + j) * 8;
-    auto step = [&](uint4 (&v)[NV], int tt) {
+#pragma unroll
+    for (int tt = 0; tt < TPW; tt++) {
         const int tile = tile0 + tt;
+        if (tile >= ntiles) break;
         {
             const uint32_t nb = tile_bytes(tile);
 #pragma unroll
@@ -269,22 +302,21 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
                 *(uint4 *)(tb + (o < nb ? pos(o, nb) : o)) = v[i];
             }
         }
-        if (tt + 2 < TPW && tile + 2 < ntiles) issue(v, tile + 2);
+        if (tt + 1 < TPW && tile + 1 < ntiles) issue(v, tile + 1);
         const uint8_t *rp = tb + r * rb;
         float acc = 0.f;
 #pragma unroll
         for (int b = 0; b < NSB; b++) acc += q6k_sb_dot_mfma(rp + b * 210, abase, ssb, 16 * b, n, j);
         acc += __shfl_xor(acc, 16);
         acc += __shfl_xor(acc, 32);
-        const int row = tile * kT6Rows + r;
-        if (g == 0 && row < a.M) a.y[mat * a.y_stride + row] = acc;
-    };
-    for (int tt = 0; tt < TPW; tt += 2) {
-        if (tile0 + tt >= ntiles) break;
-        if (tt + 1 < TPW && tile0 + tt + 1 < ntiles) issue(vb, tile0 + tt + 1);
-        step(va, tt);
-        if (tt + 1 >= TPW || tile0 + tt + 1 >= ntiles) break;
-        step(vb, tt + 1);
+        if (g == 0) ys[tt * kT6Rows + r] = acc;
+    }
+    // the work-group's TPW*16 outputs leave as one contiguous store at the end:
+    // a 64-byte write per tile between the weight reads costs ~8 % of the
+    // read bandwidth (read/write turnarounds)
+    for (int q = lane; q < TPW * kT6Rows; q += 64) {
+        const int row = tile0 * kT6Rows + q;
+        if (row < a.M) a.y[mat * a.y_stride + row] = ys[q];
     }
 }
 
@@ -293,9 +325,13 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
     constexpr int TPW = 8, K = NSB * 256;
     const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
     const uint32_t lds = lds_round(xq_bytes(K, 16)) + lds_round(3u * K) +
-                         (uint32_t)((kT6Rows * NSB * 210 + 1023) / 1024) * 1024;
+                         (uint32_t)((kT6Rows * NSB * 210 + 1023) / 1024) * 1024 + TPW * kT6Rows * 4;
     k_matvec_q6k_tile<NSB, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
     return hipGetLastError();
+}
+
+bool matvec_self_prep(int type, uint64_t row_bytes, int K) {
+    return type == GGML_TYPE_Q6_K && row_bytes == (uint64_t)K / 256 * 210 && K % 256 == 0 && K >= 256 && K <= 1024;
 }
 
 hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu) {
@@ -304,7 +340,7 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
         case GGML_TYPE_Q4_K: return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q5_K: return matvec_t<GGML_TYPE_Q5_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q6_K:
-            if (a.row_bytes == (uint64_t)a.K / 256 * 210) {   // contiguous rows: tile-staged path
+            if (a.xf && matvec_self_prep(type, a.row_bytes, a.K)) {   // contiguous rows: tile-staged path
                 if (a.K == 1024) return matvec_q6k_tile<4>(a, s);
                 if (a.K == 768) return matvec_q6k_tile<3>(a, s);
                 if (a.K == 512) return matvec_q6k_tile<2>(a, s);
