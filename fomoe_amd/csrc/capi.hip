@@ -173,7 +173,7 @@ int gpu_matvec_q_batched(gpu_ctx_t *ctx, int type, const void *W, uint64_t mat_s
     if (K % fomoe_block_values(type) || (kquant(type) && K % 256) || K > 16384)
         return fail(ctx, -1, "gpu_matvec_q: K=%d not supported for type %d", K, type);
     const uint64_t rb = fomoe_row_bytes(type, K);
-    if (matvec_self_prep(type, rb, K)) {   // the kernel prepares x itself: one launch
+    if (matvec_self_prep(type, rb, K, x_stride)) {   // the kernel prepares x itself: one launch
         MatvecArgs a{(const uint8_t *)W, mat_stride, rb, nullptr, 0, y, y_stride, n_mats, M, K, x, x_stride};
         HIPC(launch_matvec(type, a, ctx->stream, ctx->n_cu));
         return 0;

@@ -23,8 +23,9 @@ struct MatvecArgs {
 };
 
 // True when launch_matvec's kernel for this shape prepares x itself from
-// MatvecArgs::xf (no separate activation-prep launch needed).
-bool matvec_self_prep(int type, uint64_t row_bytes, int K);
+// MatvecArgs::xf (no separate activation-prep launch): the Q6_K tile-staged
+// kernel always, the general kernel when every matrix shares one x.
+bool matvec_self_prep(int type, uint64_t row_bytes, int K, uint64_t x_stride);
 
 // Router: logits = W_r . h (+ bias), h = rms_norm(x)*w when norm_w != NULL,
 // then (last work-group) softmax, top-k with lowest-index ties, renormalise,

@@ -23,9 +23,11 @@ namespace fo {
 // Used by k_xprep (one thread per group) and by kernels that prepare their
 // own activation in LDS (one lane per group), bit-identically.
 template <int GSZ>
-FO_DEV void prep_group(const float *__restrict__ xp, uint8_t *lp8, uint8_t *ss) {
+FO_DEV void prep_group_regs(const float *__restrict__ xp, int (&limb)[kLimbs][GSZ / 4], float &scale,
+                            float &sum) {
     float vals[GSZ];
-    float M = 0.f, sum = 0.f;
+    float M = 0.f;
+    sum = 0.f;
 #pragma unroll
     for (int i = 0; i < GSZ; i += 4) {
         float4 t = *(const float4 *)(xp + i);
@@ -37,12 +39,12 @@ FO_DEV void prep_group(const float *__restrict__ xp, uint8_t *lp8, uint8_t *ss) 
     frexpf(M, &E);               // M < 2^E
     int e = kFixBits - E;
     if (e > 149) e = 149;        // keep 2^-e representable
-    const float scale = (M > 0.f) ? ldexpf(1.0f, -e) : 0.f;
-    uint32_t limb[kLimbs][GSZ / 4];
+    scale = (M > 0.f) ? ldexpf(1.0f, -e) : 0.f;
+    uint32_t lb[kLimbs][GSZ / 4];
 #pragma unroll
     for (int L = 0; L < kLimbs; L++)
 #pragma unroll
-        for (int k = 0; k < GSZ / 4; k++) limb[L][k] = 0;
+        for (int k = 0; k < GSZ / 4; k++) lb[L][k] = 0;
 #pragma unroll
     for (int i = 0; i < GSZ; i++) {
         int X = (M > 0.f) ? __float2int_rn(ldexpf(vals[i], e)) : 0;
@@ -50,17 +52,27 @@ FO_DEV void prep_group(const float *__restrict__ xp, uint8_t *lp8, uint8_t *ss) 
         for (int L = 0; L < kLimbs - 1; L++) {
             const int b = (int)(int8_t)(X & 0xFF);
             X = (X - b) >> 8;
-            limb[L][i / 4] |= (uint32_t)(b & 0xFF) << (8 * (i % 4));
+            lb[L][i / 4] |= (uint32_t)(b & 0xFF) << (8 * (i % 4));
         }
-        limb[kLimbs - 1][i / 4] |= (uint32_t)(X & 0xFF) << (8 * (i % 4));
+        lb[kLimbs - 1][i / 4] |= (uint32_t)(X & 0xFF) << (8 * (i % 4));
     }
+#pragma unroll
+    for (int L = 0; L < kLimbs; L++)
+#pragma unroll
+        for (int k = 0; k < GSZ / 4; k++) limb[L][k] = (int)lb[L][k];
+}
+
+template <int GSZ>
+FO_DEV void prep_group(const float *__restrict__ xp, uint8_t *lp8, uint8_t *ss) {
+    int limb[kLimbs][GSZ / 4];
+    float scale, sum;
+    prep_group_regs<GSZ>(xp, limb, scale, sum);
     uint32_t *lp = (uint32_t *)lp8;
 #pragma unroll
     for (int L = 0; L < kLimbs; L++)
 #pragma unroll
         for (int k = 0; k < GSZ / 4; k += 4)
-            *(uint4 *)(lp + L * (GSZ / 4) + k) =
-                make_uint4(limb[L][k], limb[L][k + 1], limb[L][k + 2], limb[L][k + 3]);
+            *(uint4 *)(lp + L * (GSZ / 4) + k) = make_uint4(limb[L][k], limb[L][k + 1], limb[L][k + 2], limb[L][k + 3]);
     *(float2 *)ss = make_float2(scale, sum);
 }
 
@@ -161,6 +173,19 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     L.init(lane, S);
     XRegs<T, U> X;
     int64_t cur = -1;
+    // With a shared fp32 x (xf, xf_stride 0) the work-group prepares it in LDS
+    // itself (one thread per group, bit-identical to k_xprep); otherwise x
+    // comes prepared from global memory.
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs_lds[];
+    const uint8_t *xq = a.xq;
+    if (a.xf) {
+        constexpr int GSZ = Fmt<T>::GSZ;
+        const int ng = a.K / GSZ;
+        for (int g = threadIdx.x; g < ng; g += blockDim.x)
+            prep_group<GSZ>(a.xf + g * GSZ, xs_lds + g * (kLimbs * GSZ), xs_lds + xq_limb_bytes(a.K) + g * 8);
+        __syncthreads();
+        xq = xs_lds;
+    }
     // Outputs collect in LDS (a wave's tasks are consecutive rows) and leave
     // as one coalesced store per 64 rows: a 4-byte write per row between the
     // weight reads costs read bandwidth (read/write turnarounds).
@@ -175,7 +200,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     for (int64_t t = t0; t < t1; t++) {
         const int64_t m = t / tpm;
         const int rb = (int)(t - m * tpm);
-        if (m != cur && (cur < 0 || a.x_stride)) X.load(L, a.xq + m * a.x_stride, a.K);
+        if (m != cur && (cur < 0 || a.x_stride)) X.load(L, xq + m * a.x_stride, a.K);
         cur = m;
         const uint8_t *W = a.W + m * a.mat_stride;
         RowRaw<T, U> raw[R];
@@ -227,8 +252,9 @@ static hipError_t matvec_t(const MatvecArgs &a, hipStream_t s, int n_cu) {
     const int P = 64 / G;
     const int64_t tasks = (int64_t)((a.M + P * R - 1) / (P * R)) * a.n_mats;
     const int blocks = (waves_for(tasks, n_cu, 16) + 3) / 4;
+    const size_t lds = a.xf ? lds_round(xq_bytes(a.K, Fmt<T>::GSZ)) : 0;
 #define FO_MV(GG, UU) \
-    if (G == GG && U == UU) { k_matvec<T, UU, GG, R><<<blocks, 256, 0, s>>>(a); return hipGetLastError(); }
+    if (G == GG && U == UU) { k_matvec<T, UU, GG, R><<<blocks, 256, lds, s>>>(a); return hipGetLastError(); }
     FO_MV(64, 1) FO_MV(64, 2) FO_MV(64, 3) FO_MV(64, 4)
     FO_MV(32, 1) FO_MV(16, 1) FO_MV(8, 1) FO_MV(4, 1)
 #undef FO_MV
@@ -330,8 +356,11 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-bool matvec_self_prep(int type, uint64_t row_bytes, int K) {
-    return type == GGML_TYPE_Q6_K && row_bytes == (uint64_t)K / 256 * 210 && K % 256 == 0 && K >= 256 && K <= 1024;
+bool matvec_self_prep(int type, uint64_t row_bytes, int K, uint64_t x_stride) {
+    if (type == GGML_TYPE_Q6_K && row_bytes == (uint64_t)K / 256 * 210 && K % 256 == 0 && K <= 1024)
+        return true;   // tile-staged kernel: one matrix per work-group, any x_stride
+    return x_stride == 0 && (type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K || type == GGML_TYPE_Q6_K ||
+                             type == GGML_TYPE_Q8_0 || type == GGML_TYPE_MXFP4);
 }
 
 hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu) {
@@ -340,7 +369,7 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
         case GGML_TYPE_Q4_K: return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q5_K: return matvec_t<GGML_TYPE_Q5_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q6_K:
-            if (a.xf && matvec_self_prep(type, a.row_bytes, a.K)) {   // contiguous rows: tile-staged path
+            if (a.xf && a.row_bytes == (uint64_t)a.K / 256 * 210 && a.K % 256 == 0 && a.K <= 1024) {   // tile-staged path
                 if (a.K == 1024) return matvec_q6k_tile<4>(a, s);
                 if (a.K == 768) return matvec_q6k_tile<3>(a, s);
                 if (a.K == 512) return matvec_q6k_tile<2>(a, s);
