@@ -35,16 +35,21 @@ FO_DEV uint2 ld8(const uint8_t *p) { uint2 v; __builtin_memcpy(&v, p, 8); return
 FO_DEV uint32_t ld4(const uint8_t *p) { uint32_t v; __builtin_memcpy(&v, p, 4); return v; }
 FO_DEV uint32_t ld2(const uint8_t *p) { uint16_t v; __builtin_memcpy(&v, p, 2); return v; }
 
-// Streaming weight loads: every weight byte is read exactly once per call, so
-// mark them non-temporal to keep activations resident in L2/MALL.
-FO_DEV uint4 ld16_stream(const uint8_t *p) {
-    uint4 v;
-    v.x = __builtin_nontemporal_load((const uint32_t *)p + 0);
-    v.y = __builtin_nontemporal_load((const uint32_t *)p + 1);
-    v.z = __builtin_nontemporal_load((const uint32_t *)p + 2);
-    v.w = __builtin_nontemporal_load((const uint32_t *)p + 3);
-    return v;
+// Streaming weight loads (global memory only): every weight byte is read once
+// per call, so they carry the non-temporal hint (global_load_* nt). Measured on
+// MI355X: a pure 1.77 GB read sustains 7.1 TB/s with nt loads against 6.3 TB/s
+// with plain ones. The pointer may be only 2-byte aligned (gfx950 runs in
+// unaligned-access mode); never use these on LDS addresses.
+typedef uint32_t fo_u32x4a __attribute__((ext_vector_type(4)));
+typedef fo_u32x4a fo_u32x4 __attribute__((aligned(1)));   // no alignment promised
+FO_DEV uint4 ldw16(const uint8_t *p) {
+    const fo_u32x4 t = __builtin_nontemporal_load((const fo_u32x4 *)p);
+    return make_uint4(t.x, t.y, t.z, t.w);
 }
+// Only loads that stream whole cache lines take the hint (the 1 KiB tile
+// pieces): the per-lane slot loads of the format decoders read several 16-byte
+// pieces of one line from different instructions, and with nt the line is gone
+// before the later ones arrive (Q4_K slot matvec: 5.4 -> 4.4 TB/s measured).
 
 // Stage nbytes (a multiple of 16) from global memory into LDS with gfx950's
 // direct global->LDS loads (global_load_lds_dwordx4): every wave streams

@@ -301,7 +301,7 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
         const uint32_t nb = tile_bytes(tile);
         const uint8_t *tp = Wm + (uint64_t)tile * kT6Rows * rb;
 #pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = ld16(tp + pos(i * 1024 + lane * 16, nb));
+        for (int i = 0; i < NV; i++) v[i] = ldw16(tp + pos(i * 1024 + lane * 16, nb));
     };
     // one register buffer: tile t+1 is requested right after tile t has been
     // copied to LDS, so its loads overlap tile t's arithmetic (measured faster

@@ -397,7 +397,7 @@ __global__ __launch_bounds__(64 * kTileMaxWaves) void k_reduce_tile(ReduceArgs a
         auto pos = [&](uint32_t o) { return o + 16 <= nb ? o : nb - 16; };
         uint4 v[NV];
 #pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = ld16(src + pos(i * 1024 + lane * 16));
+        for (int i = 0; i < NV; i++) v[i] = ldw16(src + pos(i * 1024 + lane * 16));
         // keep the scheduler from sinking weight loads below the arithmetic
         __builtin_amdgcn_sched_barrier(0);
         uint8_t *dst = tiles + wv * TSTRIDE;
