@@ -356,9 +356,131 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ============================================================ tile-staged slot matvec
+// k_matvec_tile<T, NSB, RT>: rows of NSB super-blocks, RT consecutive rows per
+// tile (RT * row_bytes contiguous bytes). One wave per work-group streams its
+// tiles with non-temporal 1 KiB loads (the next tile in flight while the
+// current one is computed), writes each to its LDS area and reads every lane's
+// slots back from there; lane l owns slots l%G + G*u of P = 64/G rows per pass
+// (Fmt<T> slot dots on the exact int8 limbs) and prepares its own activation
+// groups from fp32 x (prep_group_regs, bit-identical to k_xprep). Used for
+// Q4_K at K = 4096 / 8192 (the expert gate/up shape; RT * row_bytes = 18 KiB):
+// 5.5 -> 5.8-6.0 TB/s over the per-lane-load k_matvec. For Q6_K at K = 1024 the
+// same scheme measured 5.0 TB/s against 5.6 for the MFMA tile kernel above.
+// With G = 64 the RT row partials of a lane are reduced across the wave
+// together, halving the live values at each xor step.
+template <int N>
+FO_DEV float rows_sum(float (&v)[N], int lane) {   // lane ends with row (lane >> (6 - log2 N)) & (N-1)
+    int m = 32;
+#pragma unroll
+    for (int w = N; w > 1; w >>= 1, m >>= 1) {
+        const bool up = lane & m;
+#pragma unroll
+        for (int i = 0; i < w / 2; i++) {
+            const float keep = up ? v[i + w / 2] : v[i], send = up ? v[i] : v[i + w / 2];
+            v[i] = keep + __shfl_xor(send, m, kWave);
+        }
+    }
+#pragma unroll
+    for (; m >= 1; m >>= 1) v[0] += __shfl_xor(v[0], m, kWave);
+    return v[0];
+}
+
+template <int T, int NSB, int RT, int TPW>
+__global__ __launch_bounds__(64) void k_matvec_tile(MatvecArgs a) {
+    using F = Fmt<T>;
+    constexpr int S = NSB * 4;                        // 64-value slots per row
+    constexpr int G = S >= 64 ? 64 : S, P = 64 / G, U = S / G;
+    constexpr int RB = NSB * F::BLOCK, TB = RT * RB, NV = (TB + 1023) / 1024;
+    static_assert(S % G == 0 && RT % P == 0, "tile geometry");
+    extern __shared__ __attribute__((aligned(16))) uint8_t tb[];   // [NV KiB] tile + [TPW*RT] results
+    float *ys = (float *)(tb + NV * 1024);
+    const int lane = threadIdx.x, mat = blockIdx.y, sub = lane / G;
+    const uint8_t *Wm = a.W + mat * a.mat_stride;
+    const int tile0 = blockIdx.x * TPW;
+    const int ntiles = (a.M + RT - 1) / RT;
+    // a piece that straddles the end of a tile is read from the last 16 valid
+    // bytes and written to that same LDS position (identical bytes overlap)
+    auto tile_bytes = [&](int tile) { return (uint32_t)min(RT, a.M - tile * RT) * RB; };
+    auto pos = [&](uint32_t o, uint32_t nb) { return o + 16 <= nb ? o : nb - 16; };
+    auto issue = [&](uint4 (&v)[NV], int tile) {
+        const uint32_t nb = tile_bytes(tile);
+        const uint8_t *tp = Wm + (uint64_t)tile * TB;
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = ldw16(tp + pos(i * 1024 + lane * 16, nb));
+    };
+    uint4 v[NV];
+    if (tile0 < ntiles) issue(v, tile0);
+    // the lane's activation slots, prepared from fp32 x while the tile loads
+    typename F::X X[U];
+    const float *xm = a.xf + mat * a.xf_stride;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        int gi[F::NG];
+        F::groups(lane % G + G * u, gi);
+#pragma unroll
+        for (int g = 0; g < F::NG; g++)
+            prep_group_regs<F::GSZ>(xm + gi[g] * F::GSZ, X[u].l[g], X[u].sc[g], X[u].sum[g]);
+    }
+#pragma unroll
+    for (int tt = 0; tt < TPW; tt++) {
+        const int tile = tile0 + tt;
+        if (tile >= ntiles) break;
+        const uint32_t nb = tile_bytes(tile);
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const uint32_t o = i * 1024 + lane * 16;
+            *(uint4 *)(tb + (o < nb ? pos(o, nb) : o)) = v[i];
+        }
+        if (tt + 1 < TPW && tile + 1 < ntiles) issue(v, tile + 1);
+        constexpr int PASS = RT / P;
+        float part[PASS];
+#pragma unroll
+        for (int p = 0; p < PASS; p++) {
+            const uint8_t *row = tb + (p * P + sub) * RB;
+            part[p] = 0.f;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int s = lane % G + G * u;
+                part[p] += F::dot(F::load(row, s), s, X[u]);
+            }
+        }
+        if (G == 64) {
+            const float y = rows_sum<PASS>(part, lane);
+            constexpr int SH = PASS == 8 ? 3 : PASS == 4 ? 2 : PASS == 2 ? 1 : 0;
+            if ((lane & ((64 >> SH) - 1)) == 0) ys[tt * RT + (lane >> (6 - SH))] = y;
+        } else {
+#pragma unroll
+            for (int p = 0; p < PASS; p++) {
+                const float y = group_sum<G>(part[p]);
+                if (lane % G == 0) ys[tt * RT + p * P + sub] = y;
+            }
+        }
+    }
+    // outputs leave as one contiguous store per work-group
+    for (int q = lane; q < TPW * RT; q += 64) {
+        const int row = tile0 * RT + q;
+        if (row < a.M) a.y[mat * a.y_stride + row] = ys[q];
+    }
+}
+
+template <int T, int NSB, int RT>
+static hipError_t matvec_tile(const MatvecArgs &a, hipStream_t s) {
+    constexpr int TPW = 8;
+    const int ntiles = (a.M + RT - 1) / RT;
+    const uint32_t lds = (RT * NSB * Fmt<T>::BLOCK + 1023) / 1024 * 1024 + TPW * RT * 4;
+    k_matvec_tile<T, NSB, RT, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+static bool q4k_tile_shape(uint64_t row_bytes, int K) {
+    return (K == 4096 || K == 8192) && row_bytes == (uint64_t)K / 256 * 144;
+}
+
 bool matvec_self_prep(int type, uint64_t row_bytes, int K, uint64_t x_stride) {
     if (type == GGML_TYPE_Q6_K && row_bytes == (uint64_t)K / 256 * 210 && K % 256 == 0 && K <= 1024)
         return true;   // tile-staged kernel: one matrix per work-group, any x_stride
+    if (type == GGML_TYPE_Q4_K && q4k_tile_shape(row_bytes, K)) return true;
     return x_stride == 0 && (type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K || type == GGML_TYPE_Q6_K ||
                              type == GGML_TYPE_Q8_0 || type == GGML_TYPE_MXFP4);
 }
@@ -366,7 +488,12 @@ bool matvec_self_prep(int type, uint64_t row_bytes, int K, uint64_t x_stride) {
 hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu) {
     if (a.M <= 0 || a.n_mats <= 0) return hipErrorInvalidValue;
     switch (type) {
-        case GGML_TYPE_Q4_K: return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
+        case GGML_TYPE_Q4_K:
+            if (a.xf && q4k_tile_shape(a.row_bytes, a.K)) {   // tile-staged path
+                if (a.K == 4096) return matvec_tile<GGML_TYPE_Q4_K, 16, 8>(a, s);
+                return matvec_tile<GGML_TYPE_Q4_K, 32, 4>(a, s);
+            }
+            return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q5_K: return matvec_t<GGML_TYPE_Q5_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q6_K:
             if (a.xf && a.row_bytes == (uint64_t)a.K / 256 * 210 && a.K % 256 == 0 && a.K <= 1024) {   // tile-staged path

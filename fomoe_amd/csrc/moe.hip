@@ -102,7 +102,10 @@ __global__ __launch_bounds__(256) void k_route(RouteArgs a) {
     const bool has_row = row < a.E;
     const float4 *rp = (const float4 *)(a.router + (uint64_t)min(row, a.E - 1) * H) + half * (H / 8);
 #pragma unroll
-    for (int u = 0; u < UH; u++) wr[u] = rp[lane + 64 * u];
+    for (int u = 0; u < UH; u++) {   // whole 1 KiB spans per instruction: non-temporal
+        const uint4 t = ldw16((const uint8_t *)(rp + lane + 64 * u));
+        wr[u] = make_float4(__uint_as_float(t.x), __uint_as_float(t.y), __uint_as_float(t.z), __uint_as_float(t.w));
+    }
     if (a.norm_w) {
         float ss = 0.f;
 #pragma unroll

@@ -104,7 +104,8 @@ def test_matvec_baseline_configs(gpu, name, t, M, K, ws, xs):
 
 @pytest.mark.parametrize("t,M,K", [
     (O.Q4_K, 1, 256), (O.Q4_K, 3, 512), (O.Q4_K, 7, 1024), (O.Q4_K, 33, 2048), (O.Q4_K, 5, 3072),
-    (O.Q4_K, 9, 8192), (O.Q4_K, 2, 16384), (O.Q5_K, 17, 1024), (O.Q5_K, 8, 4096),
+    (O.Q4_K, 9, 8192), (O.Q4_K, 2, 16384),
+    (O.Q4_K, 1, 4096), (O.Q4_K, 13, 4096), (O.Q4_K, 70, 4096), (O.Q4_K, 5, 8192), (O.Q4_K, 12, 8192), (O.Q5_K, 17, 1024), (O.Q5_K, 8, 4096),
     (O.Q6_K, 1, 256), (O.Q6_K, 11, 768), (O.Q6_K, 17, 1024), (O.Q6_K, 40, 512), (O.Q6_K, 64, 3072),
     (O.Q6_K, 3, 16384),
     (O.Q8_0, 1, 32), (O.Q8_0, 5, 96), (O.Q8_0, 19, 4096), (O.Q8_0, 2, 8192),
@@ -154,7 +155,8 @@ def test_matvec_mxfp4(gpu, M, K):
     assert inf_rel(got, want) < 1e-5
 
 
-@pytest.mark.parametrize("t,M,K,per_x", [(O.Q4_K, 1024, 4096, False), (O.Q6_K, 4096, 1024, True),
+@pytest.mark.parametrize("t,M,K,per_x", [(O.Q4_K, 1024, 4096, False), (O.Q4_K, 1000, 4096, True),
+                                         (O.Q6_K, 4096, 1024, True),
                                          (O.Q8_0, 256, 1024, True)])
 def test_matvec_batched(gpu, t, M, K, per_x):
     say("batched", t, per_x)
