@@ -67,7 +67,7 @@ void gpu_free(gpu_ctx_t *c) {
     void *bufs[] = {c->logits, c->counter, c->ids, c->weights, c->xq_h, c->xq_act, c->act,
                     c->act2, c->vec_in, c->vec_out, c->staging, c->pf_logits, c->pf_ids,
                     c->pf_w, c->pf_pairpos, c->pf_pairtok, c->pf_tiles, c->pf_ntiles,
-                    c->pf_act, c->pf_outp};
+                    c->pf_act, c->pf_outp, c->pf_xsum};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     for (int b = 0; b < 2; b++) {
@@ -467,6 +467,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
     HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * P * F));
     HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
+    HIPC(ensure(ctx->pf_xsum, ctx->pf_xsum_cap, sizeof(float) * (size_t)T * (H / 32)));
     fo::PrefillArgs a{};
     a.E = E; a.k = k; a.H = H; a.F = F;
     a.gate_type = L->gate_type; a.up_type = L->up_type; a.down_type = L->down_type;
@@ -479,6 +480,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.logits = ctx->pf_logits; a.ids = ctx->pf_ids; a.w = ctx->pf_w; a.pairpos = ctx->pf_pairpos;
     a.pair_tok = ctx->pf_pairtok; a.tiles = ctx->pf_tiles; a.n_tiles = ctx->pf_ntiles;
     a.max_tiles = max_tiles; a.act_hi = ctx->pf_act; a.act_lo = ctx->pf_act + P * F; a.outp = ctx->pf_outp;
+    a.xsum = ctx->pf_xsum;
     HIPC(fo::launch_prefill(a, ctx->stream));
     ctx->pf_T = T;
     ctx->pf_k = k;

@@ -45,6 +45,7 @@ struct gpu_ctx {
     int32_t *pf_ntiles = nullptr;  size_t pf_ntiles_cap = 0;
     uint16_t *pf_act = nullptr;    size_t pf_act_cap = 0;   // hi plane then lo plane
     float *pf_outp = nullptr;      size_t pf_outp_cap = 0;
+    float *pf_xsum = nullptr;      size_t pf_xsum_cap = 0;
     int pf_T = 0, pf_k = 0;
 
     // pinned staging for host->device uploads of expert stores

@@ -10,7 +10,7 @@
 namespace fo {
 
 constexpr int kPfMT = 64;        // tokens per GEMM tile (4 MFMA row blocks of 16)
-constexpr int kPfGateWaves = 16;                  // gate/up work-group: 8 gate + 8 up waves
+constexpr int kPfGateWaves = 8;                   // gate/up work-group: 4 gate + 4 up waves (two per CU)
 constexpr int kPfGateRows = 32 * kPfGateWaves / 2; // F rows per gate/up work-group (32 per wave)
 
 struct PrefillArgs {
@@ -38,6 +38,7 @@ struct PrefillArgs {
     int32_t *n_tiles;            // [1]
     int max_tiles;
     uint16_t *act_hi, *act_lo;   // [P x F] SwiGLU activation as bf16 hi + lo terms
+    float *xsum;                 // [T x H/32] sums of x over 32-value sub-blocks (Q4_K gate/up path)
     float *outp;                 // [P x H] fp32, per-pair down output
 };
 

@@ -300,7 +300,7 @@ FO_DEV void pf_stage_async(uint16_t *buf, int n, int k0, RowPtr src_row) {
 // block of the tile; the up sums meet the gate sums in LDS for the SwiGLU
 // epilogue. Wide work-groups share one staged token tile among many rows.
 template <int GT, int UT>
-__global__ __launch_bounds__(kPfGateWaves * 64) void k_pf_gateup(PrefillArgs a) {
+__global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[2 * kPfTile];
     if ((int)blockIdx.y >= *a.n_tiles) return;
     const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
@@ -373,6 +373,163 @@ __global__ __launch_bounds__(kPfGateWaves * 64) void k_pf_gateup(PrefillArgs a) 
     if (!is_up) {
         // D layout: lane holds rows 4*(lane/16)+i (tokens) of column lane%16 (weight row);
         // the activation is stored as hi/lo bf16 planes for the down projection
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (b >= nb) break;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int m = 16 * b + 4 * kg + i;
+                    if (m < n) {
+                        const float g = acc[h][b][i], u = ub[m * kPfGateRows + rl + 16 * h];
+                        const float v = (g / (1.0f + expf(-g))) * u;
+                        const __bf16 hi = (__bf16)v;
+                        const __bf16 lo = (__bf16)(v - (float)hi);
+                        const uint64_t o = (uint64_t)(p0 + m) * a.F + row + 16 * h;
+                        a.act_hi[o] = __builtin_bit_cast(uint16_t, hi);
+                        a.act_lo[o] = __builtin_bit_cast(uint16_t, lo);
+                    }
+                }
+            }
+    }
+}
+
+// ------------------------------------------------------------ Q4_K gate/up, scale after the MFMA
+// A Q4_K weight is d1*q - m1 with q in 0..15 and (d1, m1) constant over a
+// 32-value sub-block, which is exactly the k-range of one
+// v_mfma_f32_16x16x32_bf16. The codes enter the MFMA as the bf16 values
+// 128 + q (bit pattern 0x4300 | q, one v_perm per two codes, exact), so
+//   sum_k x_k (d1 q_k - m1) = d1 * D' - (128 d1 + m1) * S,
+//   D' = sum_k x_k (128 + q_k) (the MFMA),  S = sum_k x_k (k_pf_xsum),
+// applied per sub-block in fp32. The weights are used exactly (no bf16
+// rounding); the cost is the cancellation of 128 d1 S inside d1 D', a few
+// 2^-24 of 128 sum|x| per sub-block (about 1e-6 of the row's output), against
+// ~7 VALU instructions per weight for dequantizing to bf16 in registers.
+__global__ __launch_bounds__(256) void k_pf_xsum(PrefillArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // (token, sub-block)
+    const int nsb = a.H / 32;
+    if (i >= (int64_t)a.T * nsb) return;
+    const uint16_t *p = a.x + i * 32;    // token t = i / nsb, sub-block i % nsb: contiguous
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint4 v = *(const uint4 *)(p + 8 * c);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) s = (s + bf2f(w[q] & 0xFFFFu)) + bf2f(w[q] >> 16);
+    }
+    a.xsum[i] = s;
+}
+
+// eight codes (two dwords of nibbles selected by sh) as bf16 128 + q
+FO_DEV u32x4 q4_codes_bf16(uint2 q, int sh) {
+    const uint32_t w0 = (q.x >> sh) & 0x0F0F0F0Fu, w1 = (q.y >> sh) & 0x0F0F0F0Fu;
+    u32x4 r;
+    r[0] = __builtin_amdgcn_perm(0x43434343u, w0, 0x04010400u);
+    r[1] = __builtin_amdgcn_perm(0x43434343u, w0, 0x04030402u);
+    r[2] = __builtin_amdgcn_perm(0x43434343u, w1, 0x04010400u);
+    r[3] = __builtin_amdgcn_perm(0x43434343u, w1, 0x04030402u);
+    return r;
+}
+
+// (d1, 128 d1 + m1) of sub-block j from a Q4_K header (reference src/quant.c:72-80)
+FO_DEV float2 q4_sub_scales(const uint4 &hdr, int j) {
+    const uint32_t sc4[3] = {hdr.y, hdr.z, hdr.w};
+    auto byte = [&](int i) -> uint32_t { return (sc4[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
+    uint32_t sc, mn;
+    if (j < 4) { sc = byte(j) & 63; mn = byte(j + 4) & 63; }
+    else {
+        sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
+        mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+    const float d1 = h2f(hdr.x) * (float)sc, m1 = h2f(hdr.x >> 16) * (float)mn;
+    return make_float2(d1, fmaf(128.f, d1, m1));
+}
+
+// Same work-group shape and staging as k_pf_gateup; per super-block the
+// tile's S values (8 sub-blocks x 64 tokens) are staged next to the tokens.
+__global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2 * kPfTile];
+    __shared__ __attribute__((aligned(16))) float ss[2][8][kPfMT];
+    if ((int)blockIdx.y >= *a.n_tiles) return;
+    const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
+    const int e = tl.x, p0 = tl.y, n = tl.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
+    const bool shared = e == a.E;
+    const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
+    constexpr int HW = kPfGateWaves / 2;
+    const bool is_up = wave >= HW;
+    const int rl = 32 * (wave % HW) + col;
+    const int row = blockIdx.x * kPfGateRows + rl;
+    const int nb = (n + 15) >> 4, NK = a.H / 256, nsb = a.H / 32;
+    const int32_t *toks = a.pair_tok + p0;
+    auto xrow = [&](int m) { return a.x + (uint64_t)toks[m] * a.H; };
+    // S of super-block kb: waves 0..7 each load one sub-block's 64 token sums
+    const float *srow = a.xsum + (uint64_t)toks[min(lane, n - 1)] * nsb;
+    auto stage_s = [&](int kb) {
+        if (wave < 8)
+            __builtin_amdgcn_global_load_lds((const void *)(srow + kb * 8 + wave),
+                                             (__attribute__((address_space(3))) void *)&ss[kb & 1][wave][0], 4, 0, 0);
+    };
+    const uint64_t up_off = shared ? a.sh_gate_size : a.gate_size;
+    const uint64_t rb = (uint64_t)NK * 144;
+    const uint8_t *w0 = blob + (is_up ? up_off : 0) + (uint64_t)row * rb, *w1 = w0 + 16 * rb;
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
+    using D = PfDec<GGML_TYPE_Q4_K>;
+    pf_stage_async(xs, n, 0, xrow);
+    stage_s(0);
+    auto s0_next = D::load(w0, kg);
+    auto s1_next = D::load(w1, kg);
+    for (int kb = 0; kb < NK; kb++) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();                              // tile kb in LDS; buffers of kb-1 free
+        const auto s0 = s0_next;
+        const auto s1 = s1_next;
+        if (kb + 1 < NK) {
+            pf_stage_async(xs + ((kb + 1) & 1) * kPfTile, n, (kb + 1) * 256, xrow);
+            stage_s(kb + 1);
+            s0_next = D::load(w0 + (uint64_t)(kb + 1) * D::BLOCK, kg);
+            s1_next = D::load(w1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
+        }
+        const uint16_t *xb = xs + (kb & 1) * kPfTile;
+#pragma unroll
+        for (int ch = 0; ch < 8; ch++) {
+            const bf16x8 b0 = as_bf16x8(q4_codes_bf16(s0.q[ch >> 1], 4 * (ch & 1)));
+            const bf16x8 b1 = as_bf16x8(q4_codes_bf16(s1.q[ch >> 1], 4 * (ch & 1)));
+            const float2 k0 = q4_sub_scales(s0.hdr, ch), k1 = q4_sub_scales(s1.hdr, ch);
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                if (b < nb) {
+                    const bf16x8 av = *(const bf16x8 *)(xb + pf_swz(16 * b + col, 4 * ch + kg));
+                    const f32x4 z = {0, 0, 0, 0};
+                    const f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b0, z, 0, 0, 0);
+                    const f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, z, 0, 0, 0);
+                    const f32x4 sv = *(const f32x4 *)&ss[kb & 1][ch][16 * b + 4 * kg];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        acc[0][b][i] = fmaf(-k0.y, sv[i], fmaf(k0.x, d0[i], acc[0][b][i]));
+                        acc[1][b][i] = fmaf(-k1.y, sv[i], fmaf(k1.x, d1[i], acc[1][b][i]));
+                    }
+                }
+        }
+    }
+    __syncthreads();                                      // all reads of xs done: reuse it
+    float *ub = (float *)xs;                              // [64 tokens][kPfGateRows] up sums
+    if (is_up) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) ub[(16 * b + 4 * kg + i) * kPfGateRows + rl + 16 * h] = acc[h][b][i];
+    }
+    __syncthreads();
+    if (!is_up) {
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
@@ -527,8 +684,14 @@ hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
     k_pf_group<<<1, 1024, 2 * (size_t)a.E * W * sizeof(uint32_t), s>>>(a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
+    if (a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K) {   // scale-after path
+        const int64_t n = (int64_t)a.T * (a.H / 32);
+        k_pf_xsum<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(a);
+        k_pf_gateup_q4<<<dim3(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
+        err = hipGetLastError();
+    }
 #define FO_GU(G, U) if (a.gate_type == G && a.up_type == U) err = launch_gateup_t<G, U>(a, s);
-    FO_GU(GGML_TYPE_Q4_K, GGML_TYPE_Q4_K) FO_GU(GGML_TYPE_Q4_K, GGML_TYPE_Q6_K)
+    FO_GU(GGML_TYPE_Q4_K, GGML_TYPE_Q6_K)
     FO_GU(GGML_TYPE_Q6_K, GGML_TYPE_Q4_K) FO_GU(GGML_TYPE_Q6_K, GGML_TYPE_Q6_K)
 #undef FO_GU
     if (err != hipSuccess) return err;

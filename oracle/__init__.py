@@ -68,6 +68,7 @@ def _load_oracle():
                                      C.c_uint64, C.c_int, C.c_int, _vp]),
         "fo_moe_layer": (None, [C.POINTER(MoeDesc), _vp, _vp, C.c_int, _vp, _vp]),
         "fo_moe_prefill": (None, [C.POINTER(MoeDesc), _vp, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp]),
+        "fo_moe_prefill_w": (None, [C.POINTER(MoeDesc), _vp, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, C.c_int]),
         "fo_fp32_to_bf16_n": (None, [_vp, _vp, C.c_int64]),
         "fo_rng_key": (C.c_uint64, [C.c_uint64, C.c_uint64]),
         "fo_rng_u64": (C.c_uint64, [C.c_uint64, C.c_uint64]),
@@ -190,14 +191,15 @@ def bf16_to_f32(b: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
-def moe_prefill(desc: MoeDesc, x_bf16: np.ndarray, t0: int, nt: int, flags: int = 0):
-    """Oracle prefill for tokens t0..t0+nt-1 of x_bf16 [T x H] (uint16 bits)."""
+def moe_prefill(desc: MoeDesc, x_bf16: np.ndarray, t0: int, nt: int, flags: int = 0, bf16_mask: int = 7):
+    """Oracle prefill for tokens t0..t0+nt-1 of x_bf16 [T x H] (uint16 bits);
+    bf16_mask picks the weight matrices rounded to bf16 (1 gate, 2 up, 4 down)."""
     x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
     H, k = desc.n_embd, desc.k
     out = np.empty((nt, H), np.float32)
     ids = np.empty((nt, k), np.int32)
     w = np.empty((nt, k + 1), np.float32)
-    lib.fo_moe_prefill(C.byref(desc), _ptr(x_bf16), t0, nt, _ptr(out), flags, _ptr(ids), _ptr(w))
+    lib.fo_moe_prefill_w(C.byref(desc), _ptr(x_bf16), t0, nt, _ptr(out), flags, _ptr(ids), _ptr(w), bf16_mask)
     return out, ids, w
 
 

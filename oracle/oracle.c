@@ -535,15 +535,17 @@ void fo_fp32_to_bf16_n(const float *x, uint16_t *y, int64_t n) {
     for (int64_t i = 0; i < n; i++) y[i] = fo_fp32_to_bf16(x[i]);
 }
 
-/* rows x cols matrix of `type` dequantized exactly, then rounded to bf16 */
-static float *deq_bf16(const uint8_t *w, int type, int rows, int cols) {
+/* rows x cols matrix of `type` dequantized exactly, then rounded to bf16
+ * when `round` is set */
+static float *deq_bf16(const uint8_t *w, int type, int rows, int cols, int round) {
     float *m = (float *)malloc(sizeof(float) * (size_t)rows * cols);
     const uint64_t rb = fomoe_row_bytes(type, cols);
 #pragma omp parallel for if (rows > 64)
     for (int r = 0; r < rows; r++) {
         float *y = m + (size_t)r * cols;
         fo_dequantize_row(type, w + (uint64_t)r * rb, y, cols);
-        for (int c = 0; c < cols; c++) y[c] = fo_bf16_to_fp32(fo_fp32_to_bf16(y[c]));
+        if (round)
+            for (int c = 0; c < cols; c++) y[c] = fo_bf16_to_fp32(fo_fp32_to_bf16(y[c]));
     }
     return m;
 }
@@ -558,25 +560,26 @@ static void matvec_f64(float *out, const float *m, const float *v, int rows, int
     }
 }
 
+/* bf16_mask: bit 0 gate, bit 1 up, bit 2 down weights rounded to bf16 */
 static void expert_ffn_bf16(const uint8_t *blob, const fo_moe_desc *L, uint64_t gs, uint64_t us,
-                            const float *x, float *out) {
+                            const float *x, float *out, int bf16_mask) {
     const int H = L->n_embd, F = L->inter;
     float *g = (float *)malloc(sizeof(float) * (size_t)F * 2), *u = g + F;
-    float *wg = deq_bf16(blob, L->gate_type, F, H);
+    float *wg = deq_bf16(blob, L->gate_type, F, H, bf16_mask & 1);
     matvec_f64(g, wg, x, F, H);
     free(wg);
-    float *wu = deq_bf16(blob + gs, L->up_type, F, H);
+    float *wu = deq_bf16(blob + gs, L->up_type, F, H, bf16_mask & 2);
     matvec_f64(u, wu, x, F, H);
     free(wu);
     for (int i = 0; i < F; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
-    float *wd = deq_bf16(blob + gs + us, L->down_type, H, F);
+    float *wd = deq_bf16(blob + gs + us, L->down_type, H, F, bf16_mask & 4);
     matvec_f64(out, wd, g, H, F);
     free(wd);
     free(g);
 }
 
-void fo_moe_prefill(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
-                    int *ids_out, float *w_out) {
+void fo_moe_prefill_w(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
+                      int *ids_out, float *w_out, int bf16_mask) {
     const int H = L->n_embd, E = L->n_experts, k = L->k;
     float *h = (float *)malloc(sizeof(float) * (size_t)H * 3);
     float *ffn = h + H, *dn = ffn + H;
@@ -594,12 +597,13 @@ void fo_moe_prefill(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, flo
         if (ssum > 0.0f) { const float inv = 1.0f / ssum; for (int i = 0; i < k; i++) sc[i] *= inv; }
         memset(ffn, 0, sizeof(float) * (size_t)H);
         for (int i = 0; i < k; i++) {
-            expert_ffn_bf16(L->experts + (uint64_t)ids[i] * L->expert_stride, L, L->gate_size, L->up_size, h, dn);
+            expert_ffn_bf16(L->experts + (uint64_t)ids[i] * L->expert_stride, L, L->gate_size, L->up_size, h, dn,
+                            bf16_mask);
             for (int j = 0; j < H; j++) ffn[j] += sc[i] * dn[j];
         }
         float gsc = 1.0f;
         if (L->shared) {
-            expert_ffn_bf16(L->shared, L, L->shared_gate_size, L->shared_up_size, h, dn);
+            expert_ffn_bf16(L->shared, L, L->shared_gate_size, L->shared_up_size, h, dn, bf16_mask);
             if (L->shared_gate_vec) {
                 float dot = 0.0f;
                 for (int j = 0; j < H; j++) dot += h[j] * L->shared_gate_vec[j];
@@ -618,6 +622,11 @@ void fo_moe_prefill(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, flo
     }
     free(h);
     free(logits);
+}
+
+void fo_moe_prefill(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
+                    int *ids_out, float *w_out) {
+    fo_moe_prefill_w(L, x, t0, nt, out, flags, ids_out, w_out, 7);
 }
 
 /* ------------------------------------------------------------------------

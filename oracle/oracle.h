@@ -107,6 +107,10 @@ void     fo_fp32_to_bf16_n(const float *x, uint16_t *y, int64_t n);
  * w [nt x (k+1)] (last = shared weight). Only FO_MOE_RESIDUAL is honoured. */
 void fo_moe_prefill(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
                     int *ids_out, float *w_out);
+/* As fo_moe_prefill with a choice of which weight matrices are rounded to
+ * bf16 (bit 0 gate, bit 1 up, bit 2 down; fo_moe_prefill = all three). */
+void fo_moe_prefill_w(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
+                      int *ids_out, float *w_out, int bf16_mask);
 
 /* ---- synthetic data (this build's own definition; no reference) ---- */
 uint64_t fo_rng_key(uint64_t seed, uint64_t stream);

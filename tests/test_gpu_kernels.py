@@ -543,6 +543,13 @@ def _prefill_host_layer(shape, layer, seed, zipf, gvec=None, experts_needed=None
 PF_PARITY, PF_INF = 1e-2, 1e-5
 
 
+def pf_bf16_mask(shape):
+    """Weight matrices the prefill path rounds to bf16: Q4_K gate/up run on the
+    scale-after MFMA path with exact weights, the rest are dequantized to bf16."""
+    q4 = shape.gate_type == O.Q4_K
+    return (0 if q4 else 3) | 4
+
+
 @pytest.mark.parametrize("T,shared,gate_vec,resid", [(200, True, True, True), (1, True, False, False),
                                                       (33, False, False, True)])
 def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid):
@@ -569,7 +576,7 @@ def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid):
         got_r = gpu.download(dout, np.float32, T * shape.n_embd).reshape(T, shape.n_embd)
         assert np.array_equal(got_r, O.bf16_to_f32(x).reshape(T, -1) + got)
     d, keep = _prefill_host_layer(shape, 0, 21, True, gv)
-    want, oids, ow = O.moe_prefill(d, x, 0, T, 0)
+    want, oids, ow = O.moe_prefill(d, x, 0, T, 0, bf16_mask=pf_bf16_mask(shape))
     assert np.array_equal(ids, oids)
     assert inf_rel(w[:, :shape.k], ow[:, :shape.k]) < 1e-5
     if shared:
@@ -611,7 +618,7 @@ def test_prefill_config5_sampled(gpu):
     dh = gpu.alloc(4 * H)
     dl = gpu.alloc(4 * H)
     for t in sample:
-        want, oids, _ = O.moe_prefill(d, x, t, 1, 0)
+        want, oids, _ = O.moe_prefill(d, x, t, 1, 0, bf16_mask=pf_bf16_mask(shape))
         assert np.array_equal(oids[0], ids[t])
         e = parity_err(got[t], want[0])
         gpu.upload_to(dh, xf[t])

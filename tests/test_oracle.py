@@ -372,22 +372,26 @@ def _prefill_inputs(seed, E, H, F, T):
     return router, x, experts, gs, ds
 
 
-def test_prefill_oracle_fp64_recomposition():
-    """Prefill oracle = numpy recomposition: bf16-rounded exact dequantized
-    weights, fp64 dots, fp32 SwiGLU activation, rank-order combine."""
+@pytest.mark.parametrize("mask", [7, 4, 0])
+def test_prefill_oracle_fp64_recomposition(mask):
+    """Prefill oracle = numpy recomposition: exact dequantized weights, rounded
+    to bf16 for the matrices in bf16_mask (1 gate, 2 up, 4 down), fp64 dots,
+    fp32 SwiGLU activation, rank-order combine."""
     E, k, H, F, T = 8, 3, 256, 256, 5
     router, x, experts, gs, ds = _prefill_inputs(41, E, H, F, T)
     stride = 2 * gs + ds
     gvec = O.synth_f32(42, 0, 0.05, H)
     d = moe_desc(E, k, H, F, router, experts, gs, ds, shared_off=E * stride, gvec=gvec)
-    out, ids, w = O.moe_prefill(d, x, 1, 3, O.MOE_RESIDUAL)
-    bf = lambda a: O.bf16_to_f32(O.to_bf16(a)).astype(np.float64)  # noqa: E731
+    out, ids, w = O.moe_prefill(d, x, 1, 3, O.MOE_RESIDUAL, bf16_mask=mask)
+
+    def bfm(a, bit):   # bf16-rounded when the matrix's bit is in the mask
+        return (O.bf16_to_f32(O.to_bf16(a)) if mask & bit else a).astype(np.float64)
 
     def ffn(off, xt):
         e = experts[off:off + stride]
-        G = bf(O.dequantize(O.Q4_K, e[:gs], F * H)).reshape(F, H)
-        U = bf(O.dequantize(O.Q4_K, e[gs:2 * gs], F * H)).reshape(F, H)
-        D = bf(O.dequantize(O.Q6_K, e[2 * gs:], H * F)).reshape(H, F)
+        G = bfm(O.dequantize(O.Q4_K, e[:gs], F * H), 1).reshape(F, H)
+        U = bfm(O.dequantize(O.Q4_K, e[gs:2 * gs], F * H), 2).reshape(F, H)
+        D = bfm(O.dequantize(O.Q6_K, e[2 * gs:], H * F), 4).reshape(H, F)
         g, u = (G @ xt).astype(np.float32), (U @ xt).astype(np.float32)
         a = ((g / (1 + np.exp(-g))) * u).astype(np.float64)
         return D @ a
