@@ -357,7 +357,7 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
 }
 
 // ============================================================ tile-staged slot matvec
-// k_matvec_tile<T, NSB, RT>: rows of NSB super-blocks, RT consecutive rows per
+// k_matvec_tile<T, K, RT>: rows of K values, RT consecutive rows per
 // tile (RT * row_bytes contiguous bytes). One wave per work-group streams its
 // tiles with non-temporal 1 KiB loads (the next tile in flight while the
 // current one is computed), writes each to its LDS area and reads every lane's
@@ -365,7 +365,8 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
 // (Fmt<T> slot dots on the exact int8 limbs) and prepares its own activation
 // groups from fp32 x (prep_group_regs, bit-identical to k_xprep). Used for
 // Q4_K at K = 4096 / 8192 (the expert gate/up shape; RT * row_bytes = 18 KiB):
-// 5.5 -> 5.8-6.0 TB/s over the per-lane-load k_matvec. For Q6_K at K = 1024 the
+// 5.5 -> 5.8-6.0 TB/s over the per-lane-load k_matvec, and for Q8_0 at K = 1024
+// / 4096 (17 KiB tiles). For Q6_K at K = 1024 the
 // same scheme measured 5.0 TB/s against 5.6 for the MFMA tile kernel above.
 // With G = 64 the RT row partials of a lane are reduced across the wave
 // together, halving the live values at each xor step.
@@ -386,12 +387,13 @@ FO_DEV float rows_sum(float (&v)[N], int lane) {   // lane ends with row (lane >
     return v[0];
 }
 
-template <int T, int NSB, int RT, int TPW>
+template <int T, int K, int RT, int TPW>
 __global__ __launch_bounds__(64) void k_matvec_tile(MatvecArgs a) {
     using F = Fmt<T>;
-    constexpr int S = NSB * 4;                        // 64-value slots per row
+    constexpr int S = K / F::SLOT;                    // slots per row
     constexpr int G = S >= 64 ? 64 : S, P = 64 / G, U = S / G;
-    constexpr int RB = NSB * F::BLOCK, TB = RT * RB, NV = (TB + 1023) / 1024;
+    constexpr int BV = F::SLOT == 64 ? 256 : 32;      // values per format block
+    constexpr int RB = K / BV * F::BLOCK, TB = RT * RB, NV = (TB + 1023) / 1024;
     static_assert(S % G == 0 && RT % P == 0, "tile geometry");
     extern __shared__ __attribute__((aligned(16))) uint8_t tb[];   // [NV KiB] tile + [TPW*RT] results
     float *ys = (float *)(tb + NV * 1024);
@@ -464,23 +466,26 @@ __global__ __launch_bounds__(64) void k_matvec_tile(MatvecArgs a) {
     }
 }
 
-template <int T, int NSB, int RT>
+template <int T, int K, int RT>
 static hipError_t matvec_tile(const MatvecArgs &a, hipStream_t s) {
-    constexpr int TPW = 8;
+    constexpr int TPW = 8, BV = Fmt<T>::SLOT == 64 ? 256 : 32;
     const int ntiles = (a.M + RT - 1) / RT;
-    const uint32_t lds = (RT * NSB * Fmt<T>::BLOCK + 1023) / 1024 * 1024 + TPW * RT * 4;
-    k_matvec_tile<T, NSB, RT, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
+    const uint32_t lds = (RT * (K / BV) * Fmt<T>::BLOCK + 1023) / 1024 * 1024 + TPW * RT * 4;
+    k_matvec_tile<T, K, RT, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
     return hipGetLastError();
 }
 
-static bool q4k_tile_shape(uint64_t row_bytes, int K) {
-    return (K == 4096 || K == 8192) && row_bytes == (uint64_t)K / 256 * 144;
+// shapes served by k_matvec_tile (contiguous rows)
+static bool tile_shape(int type, uint64_t row_bytes, int K) {
+    if (type == GGML_TYPE_Q4_K) return (K == 4096 || K == 8192) && row_bytes == (uint64_t)K / 256 * 144;
+    if (type == GGML_TYPE_Q8_0) return (K == 1024 || K == 4096) && row_bytes == (uint64_t)K / 32 * 34;
+    return false;
 }
 
 bool matvec_self_prep(int type, uint64_t row_bytes, int K, uint64_t x_stride) {
     if (type == GGML_TYPE_Q6_K && row_bytes == (uint64_t)K / 256 * 210 && K % 256 == 0 && K <= 1024)
         return true;   // tile-staged kernel: one matrix per work-group, any x_stride
-    if (type == GGML_TYPE_Q4_K && q4k_tile_shape(row_bytes, K)) return true;
+    if (tile_shape(type, row_bytes, K)) return true;
     return x_stride == 0 && (type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K || type == GGML_TYPE_Q6_K ||
                              type == GGML_TYPE_Q8_0 || type == GGML_TYPE_MXFP4);
 }
@@ -489,9 +494,9 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
     if (a.M <= 0 || a.n_mats <= 0) return hipErrorInvalidValue;
     switch (type) {
         case GGML_TYPE_Q4_K:
-            if (a.xf && q4k_tile_shape(a.row_bytes, a.K)) {   // tile-staged path
-                if (a.K == 4096) return matvec_tile<GGML_TYPE_Q4_K, 16, 8>(a, s);
-                return matvec_tile<GGML_TYPE_Q4_K, 32, 4>(a, s);
+            if (a.xf && tile_shape(type, a.row_bytes, a.K)) {   // tile-staged path
+                if (a.K == 4096) return matvec_tile<GGML_TYPE_Q4_K, 4096, 8>(a, s);
+                return matvec_tile<GGML_TYPE_Q4_K, 8192, 4>(a, s);
             }
             return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q5_K: return matvec_t<GGML_TYPE_Q5_K, 2>(a, s, n_cu);
@@ -503,7 +508,12 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
                 if (a.K == 256) return matvec_q6k_tile<1>(a, s);
             }
             return matvec_t<GGML_TYPE_Q6_K, 2>(a, s, n_cu);
-        case GGML_TYPE_Q8_0: return matvec_t<GGML_TYPE_Q8_0, 2>(a, s, n_cu);
+        case GGML_TYPE_Q8_0:
+            if (a.xf && tile_shape(type, a.row_bytes, a.K)) {   // tile-staged path
+                if (a.K == 1024) return matvec_tile<GGML_TYPE_Q8_0, 1024, 16>(a, s);
+                return matvec_tile<GGML_TYPE_Q8_0, 4096, 4>(a, s);
+            }
+            return matvec_t<GGML_TYPE_Q8_0, 2>(a, s, n_cu);
         case GGML_TYPE_MXFP4: return matvec_t<GGML_TYPE_MXFP4, 2>(a, s, n_cu);
         default: return hipErrorInvalidValue;
     }

@@ -285,7 +285,8 @@ FO_DEV int pf_swz(int m, int c) { return m * 256 + 8 * (c ^ (m & 15)); }
 template <typename RowPtr>
 FO_DEV void pf_stage_async(uint16_t *buf, int n, int k0, RowPtr src_row) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int q = wave; q < kPfMT / 2; q += nw) {
+    const int rows = (n + 15) & ~15;                           // the MFMA row blocks in use
+    for (int q = wave; q < rows / 2; q += nw) {
         const int m = 2 * q + (lane >> 5), cs = lane & 31;      // LDS slot (m, cs)
         const int c = cs ^ (m & 15);                            // global chunk stored there
         const uint16_t *src = src_row(m < n ? m : 0) + k0 + 8 * c;
@@ -578,7 +579,7 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
         uint16_t *buf = dxs + (kb & 1) * 2 * kPfTile + (wave / HW) * kPfTile;
         const uint16_t *plane = (wave / HW) ? a.act_lo : a.act_hi;
         const int lane_ = threadIdx.x & 63, w4 = wave % HW;
-        for (int q = w4; q < kPfMT / 2; q += HW) {
+        for (int q = w4; q < nb * 8; q += HW) {
             const int m = 2 * q + (lane_ >> 5), cs = lane_ & 31;
             const int c = cs ^ (m & 15);
             const uint16_t *src = plane + (uint64_t)(p0 + (m < n ? m : 0)) * a.F + kb * 256 + 8 * c;

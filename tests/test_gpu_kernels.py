@@ -109,6 +109,7 @@ def test_matvec_baseline_configs(gpu, name, t, M, K, ws, xs):
     (O.Q6_K, 1, 256), (O.Q6_K, 11, 768), (O.Q6_K, 17, 1024), (O.Q6_K, 40, 512), (O.Q6_K, 64, 3072),
     (O.Q6_K, 3, 16384),
     (O.Q8_0, 1, 32), (O.Q8_0, 5, 96), (O.Q8_0, 19, 4096), (O.Q8_0, 2, 8192),
+    (O.Q8_0, 17, 1024), (O.Q8_0, 1, 1024), (O.Q8_0, 33, 4096),
 ])
 def test_matvec_shapes(gpu, t, M, K):
     say("matvec shape", t, M, K)
