@@ -272,7 +272,7 @@ static hipError_t matvec_t(const MatvecArgs &a, hipStream_t s, int n_cu) {
 // with the 64 codes of slot (n = g>>1, j = g&1) for one t; A = the activation
 // limbs routed so that D lane (row, g) receives the three limb sums of its own
 // 16-value scale group, rows 4g..4g+2 of A being nonzero only over lane group
-// g's k-range (other lanes read a zeroed LDS region). D layout: lane holds
+// g's k-range (other lanes read a 16-byte zero slot). D layout: lane holds
 // rows 4*(lane/16)+i of column lane%16. Group scales / offsets / sub-block
 // scales are then applied per lane as in Fmt<Q6_K>.
 constexpr int kT6Rows = 16, kT6MaxNV = 14;   // 16 rows x 840 B <= 14 KiB
@@ -285,8 +285,8 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
     const int lane = threadIdx.x;
     const int mat = blockIdx.y;
     constexpr uint32_t limb_bytes = 3u * K, xbytes = limb_bytes + (K / 16) * 8;
-    constexpr uint32_t zoff = lds_round(xbytes);
-    uint8_t *tb = sx + zoff + lds_round(limb_bytes);
+    constexpr uint32_t zoff = (xbytes + 15) & ~15u;    // 16 zero bytes for the A rows of other groups
+    uint8_t *tb = sx + zoff + 16;
     float *ys = (float *)(tb + NV * 1024);             // [TPW * 16] results
     const uint8_t *Wm = a.W + mat * a.mat_stride;
     constexpr uint32_t rb = NSB * 210;                 // launched only for contiguous rows
@@ -310,11 +310,11 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
     if (tile0 < ntiles) issue(v, tile0);
     // the activation is prepared here, one lane per 16-value group (K <= 1024)
     if (lane < K / 16) prep_group<16>(a.xf + mat * a.xf_stride + lane * 16, sx + lane * 48, sx + limb_bytes + lane * 8);
-    for (uint32_t o = lane * 16; o < limb_bytes; o += 64 * 16) *(uint4 *)(sx + zoff + o) = make_uint4(0, 0, 0, 0);
+    if (lane == 0) *(uint4 *)(sx + zoff) = make_uint4(0, 0, 0, 0);
     __syncthreads();
     const int r = lane & 15, g = lane >> 4, n = g >> 1, j = g & 1, L = r & 3;
     const bool valid = (r >> 2) == g && L < 3;
-    const uint8_t *abase = sx + (valid ? 0u : zoff) + (8 * n + j) * 48 + 16 * L;
+    const uint8_t *abase = sx + (8 * n + j) * 48 + 16 * L;
     const uint8_t *ssb = sx + limb_bytes + (8 * n + j) * 8;
 #pragma unroll
     for (int tt = 0; tt < TPW; tt++) {
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
         const uint8_t *rp = tb + r * rb;
         float acc = 0.f;
 #pragma unroll
-        for (int b = 0; b < NSB; b++) acc += q6k_sb_dot_mfma(rp + b * 210, abase, ssb, 16 * b, n, j);
+        for (int b = 0; b < NSB; b++) acc += q6k_sb_dot_mfma(rp + b * 210, abase, ssb, 16 * b, n, j, valid, sx + zoff);
         acc += __shfl_xor(acc, 16);
         acc += __shfl_xor(acc, 32);
         if (g == 0) ys[tt * kT6Rows + r] = acc;
@@ -350,7 +350,7 @@ template <int NSB>
 static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
     constexpr int TPW = 8, K = NSB * 256;
     const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
-    const uint32_t lds = lds_round(xq_bytes(K, 16)) + lds_round(3u * K) +
+    const uint32_t lds = ((xq_bytes(K, 16) + 15) & ~15u) + 16 +
                          (uint32_t)((kT6Rows * NSB * 210 + 1023) / 1024) * 1024 + TPW * kT6Rows * 4;
     k_matvec_q6k_tile<NSB, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
     return hipGetLastError();

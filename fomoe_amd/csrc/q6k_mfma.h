@@ -1,5 +1,5 @@
 // q6k_mfma.h — one Q6_K super-block x 16 rows on v_mfma_i32_16x16x64_i8, the
-// shared core of the tile-staged Q6_K kernels (k_matvec_q6k_tile, k_reduce_q6t).
+// core of the tile-staged Q6_K matvec (k_matvec_q6k_tile).
 //
 // Lane (r = lane%16, g = lane/16), n = g>>1, j = g&1 owns slot (n, j) of row r:
 // the 64 values 128n + 32t + l, l in [16j, 16j+16), t = 0..3 (reference
@@ -7,7 +7,7 @@
 // form the MFMA B operand (column = weight row r). The A operand routes the
 // three activation limbs so that A rows 4g..4g+2 are nonzero only over lane
 // group g's k-range and hold limb 0..2 of activation group 16b + 8n + 2t + j
-// (lanes of other rows read a zeroed LDS region). D layout: lane holds rows
+// (lanes of other rows read a 16-byte zero slot instead). D layout: lane holds rows
 // 4*(lane/16)+i of column lane%16, i.e. lane (r, g) receives the three limb
 // sums of its own row's 16-value scale group, to which it applies the group
 // scale and offset and the sub-block scale sc[8n + 2t + j] itself.
@@ -20,10 +20,11 @@ namespace fo {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // sb: this row's super-block (any alignment, LDS or global); abase / ssb: the
-// lane's A-operand / {scale, sum} base for group offset 0; g0 = 16 * (index of
-// the super-block in the row). Returns the lane's partial of d * sum.
+// lane's A-operand / {scale, sum} base for group offset 0; zero16: 16 zero
+// bytes, read instead when !valid; g0 = 16 * (index of the super-block in the
+// row). Returns the lane's partial of d * sum.
 FO_DEV float q6k_sb_dot_mfma(const uint8_t *sb, const uint8_t *abase, const uint8_t *ssb, int g0, int n,
-                             int j) {
+                             int j, bool valid, const uint8_t *zero16) {
     uint4 l0, l1, hh;
     uint2 scb;
     uint16_t d16;
@@ -49,7 +50,7 @@ FO_DEV float q6k_sb_dot_mfma(const uint8_t *sb, const uint8_t *abase, const uint
             B[k] = (int)q;
         }
         const int go = g0 + 2 * t;                        // group g0 + 8n + 2t + j
-        const v4i A = *(const v4i *)(abase + go * 48);
+        const v4i A = *(const v4i *)(valid ? abase + go * 48 : zero16);
         const v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
         const float f = fmaf(fmaf((float)D[2], 256.f, (float)D[1]), 256.f, (float)D[0]);
         const float2 ss = *(const float2 *)(ssb + go * 8);
