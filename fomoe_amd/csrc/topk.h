@@ -46,15 +46,20 @@ FO_DEV void wave_argmax(float lb, int li, float &m, int &idx) {
     }
 }
 
-template <int NV>  // logits per lane: E <= 64*NV
-FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *s_ids, float *s_w) {
+// This lane's logits 64j + lane (-FLT_MAX past E).
+template <int NV>
+FO_DEV void wave_logits(const float *__restrict__ logits, int E, float (&v)[NV]) {
     const int lane = threadIdx.x & 63;
-    float v[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int i = 64 * j + lane;
         v[j] = i < E ? logits[i] : -FLT_MAX;
     }
+}
+
+template <int NV>  // logits per lane: E <= 64*NV; v from wave_logits (consumed)
+FO_DEV void wave_topk_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w) {
+    const int lane = threadIdx.x & 63;
     float my_v = -FLT_MAX;   // lane kk keeps selection kk (no indexed private arrays:
     int my_i = 0;            // those would put the kernel on scratch, which throttles residency)
     for (int kk = 0; kk < k; kk++) {
@@ -80,6 +85,13 @@ FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *s_ids
     if (lane < k) { s_ids[lane] = my_i; if (s_w) s_w[lane] = e * inv; }
 }
 
+template <int NV>
+FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *s_ids, float *s_w) {
+    float v[NV];
+    wave_logits<NV>(logits, E, v);
+    wave_topk_v<NV>(v, E, k, s_ids, s_w);
+}
+
 // Same selection through a threshold: the 64 lane maxima are sorted across
 // the wave (a 21-step flip / half-cleaner network: DPP inside 16-lane rows,
 // three permutes across rows), so T = the k-th largest lane maximum; k lane
@@ -98,15 +110,9 @@ template <int CTRL>
 FO_DEV int dpp_keep_i(int v) { return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false); }
 
 template <int NV>
-FO_DEV void wave_topk_thr(const float *__restrict__ logits, int E, int k, int *s_ids, float *s_w,
-                          float2 *s_cand, float *s_val) {
+FO_DEV void wave_topk_thr_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w, float2 *s_cand,
+                            float *s_val) {
     const int lane = threadIdx.x & 63, r = lane & 15;
-    float v[NV];
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-        const int i = 64 * j + lane;
-        v[j] = i < E ? logits[i] : -FLT_MAX;
-    }
     float mx = -FLT_MAX;
 #pragma unroll
     for (int j = 0; j < NV; j++) mx = fmaxf(mx, v[j]);   // NaNs drop out
@@ -147,7 +153,7 @@ FO_DEV void wave_topk_thr(const float *__restrict__ logits, int E, int k, int *s
         }
     }
     if (!ok) {
-        wave_topk<NV>(logits, E, k, s_ids, s_w);
+        wave_topk_v<NV>(v, E, k, s_ids, s_w);
         return;
     }
     // lane l < n ranks candidate l against entries l+1 .. l+n-1 of the doubled list
@@ -171,6 +177,14 @@ FO_DEV void wave_topk_thr(const float *__restrict__ logits, int E, int k, int *s
         const float inv = 1.0f / group_sum<kWave>(e);
         if (lane < k) s_w[lane] = e * inv;
     }
+}
+
+template <int NV>
+FO_DEV void wave_topk_thr(const float *__restrict__ logits, int E, int k, int *s_ids, float *s_w,
+                          float2 *s_cand, float *s_val) {
+    float v[NV];
+    wave_logits<NV>(logits, E, v);
+    wave_topk_thr_v<NV>(v, E, k, s_ids, s_w, s_cand, s_val);
 }
 
 }  // namespace fo
