@@ -58,6 +58,51 @@ template <int NG, int GSZ> struct XSlot {
     float sc[NG], sum[NG];
 };
 
+// ============================================================ activation prep
+// One group of GSZ values: exponent from the group maximum, the balanced int8
+// limbs of X = round(x * 2^e) (layout above), the scale 2^-e and the fp32
+// sum, in registers. prep_group (kernels.hip) stores them; k_xprep uses one
+// thread per group, the tile kernels one lane per group, bit-identically.
+template <int GSZ>
+FO_DEV void prep_group_regs(const float *__restrict__ xp, int (&limb)[kLimbs][GSZ / 4], float &scale,
+                            float &sum) {
+    float vals[GSZ];
+    float M = 0.f;
+    sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < GSZ; i += 4) {
+        float4 t = *(const float4 *)(xp + i);
+        vals[i] = t.x; vals[i + 1] = t.y; vals[i + 2] = t.z; vals[i + 3] = t.w;
+    }
+#pragma unroll
+    for (int i = 0; i < GSZ; i++) { M = fmaxf(M, fabsf(vals[i])); sum += vals[i]; }
+    int E = 0;
+    frexpf(M, &E);               // M < 2^E
+    int e = kFixBits - E;
+    if (e > 149) e = 149;        // keep 2^-e representable
+    scale = (M > 0.f) ? ldexpf(1.0f, -e) : 0.f;
+    uint32_t lb[kLimbs][GSZ / 4];
+#pragma unroll
+    for (int L = 0; L < kLimbs; L++)
+#pragma unroll
+        for (int k = 0; k < GSZ / 4; k++) lb[L][k] = 0;
+#pragma unroll
+    for (int i = 0; i < GSZ; i++) {
+        int X = (M > 0.f) ? __float2int_rn(ldexpf(vals[i], e)) : 0;
+#pragma unroll
+        for (int L = 0; L < kLimbs - 1; L++) {
+            const int b = (int)(int8_t)(X & 0xFF);
+            X = (X - b) >> 8;
+            lb[L][i / 4] |= (uint32_t)(b & 0xFF) << (8 * (i % 4));
+        }
+        lb[kLimbs - 1][i / 4] |= (uint32_t)(X & 0xFF) << (8 * (i % 4));
+    }
+#pragma unroll
+    for (int L = 0; L < kLimbs; L++)
+#pragma unroll
+        for (int k = 0; k < GSZ / 4; k++) limb[L][k] = (int)lb[L][k];
+}
+
 // Load the groups gi[0..NG) of a prepared vector into registers.
 template <int NG, int GSZ>
 FO_DEV void load_xslot(XSlot<NG, GSZ> &x, const uint8_t *xq, int K, const int gi[NG]) {
