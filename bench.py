@@ -9,7 +9,7 @@ matrices; value = algorithmic bytes per step / time per step, with the
 weights already resident in HBM.
 
 Also measured in the same run (reported under "extra"): the config-1 Q4_K
-rotation, the Q8_0 variant of config 2, one MoE layer (config 3) per call,
+rotation, the Q8_0 and Q5_K variants of config 2, one MoE layer (config 3) per call,
 and the 60-layer HBM-resident decode stack (config 4) replayed from a HIP
 graph, which gives the us-per-MoE-layer figure; the config-5 prefill (512
 bf16 tokens through one Zipf-routed layer on grouped bf16-MFMA GEMMs); plus
@@ -266,7 +266,7 @@ def main():
     ap.add_argument("--layer-calls", type=int, default=600)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--prefill-reps", type=int, default=10)
-    ap.add_argument("--skip", default="", help="comma list: q4k,q8_0,stack,cpu,prefill")
+    ap.add_argument("--skip", default="", help="comma list: q4k,q8_0,q5k,stack,cpu,prefill")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -290,6 +290,11 @@ def main():
         q8, keep = rotation(gpu, FA.Q8_0, 4096, 1024, 2, 3, 512, args.steps, args.warmup)
         extra["config2_q8_0"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q8.items()}
         log(f"Q8_0 rotation: {q8['GB/s']:.0f} GB/s")
+        del keep
+    if "q5k" not in skip:   # the real model's down projections are partly Q5_K (same shape as config 2)
+        q5, keep = rotation(gpu, FA.Q5_K, 4096, 1024, 2, 3, 512, args.steps, args.warmup)
+        extra["config2_q5k"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q5.items()}
+        log(f"Q5_K rotation: {q5['GB/s']:.0f} GB/s")
         del keep
     cpu = None
     if "cpu" not in skip:

@@ -322,8 +322,9 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
 // (Fmt<T> slot dots on the exact int8 limbs) and prepares its own activation
 // groups from fp32 x (prep_group_regs, bit-identical to k_xprep). Used for
 // Q4_K at K = 4096 / 8192 (the expert gate/up shape; RT * row_bytes = 18 KiB):
-// 5.5 -> 5.8-6.0 TB/s over the per-lane-load k_matvec, and for Q8_0 at K = 1024
-// / 4096 (17 KiB tiles). For Q6_K at K = 1024 the
+// 5.5 -> 5.8-6.0 TB/s over the per-lane-load k_matvec, for Q8_0 at K = 1024
+// / 4096 (17 KiB tiles), Q5_K at K = 1024 / 4096 (11 KiB) and MXFP4 at K = 4096
+// (17 KiB). For Q6_K at K = 1024 the
 // same scheme measured 5.0 TB/s against 5.6 for the MFMA tile kernel above.
 // With G = 64 the RT row partials of a lane are reduced across the wave
 // together, halving the live values at each xor step.
@@ -436,6 +437,8 @@ static hipError_t matvec_tile(const MatvecArgs &a, hipStream_t s) {
 static bool tile_shape(int type, uint64_t row_bytes, int K) {
     if (type == GGML_TYPE_Q4_K) return (K == 4096 || K == 8192) && row_bytes == (uint64_t)K / 256 * 144;
     if (type == GGML_TYPE_Q8_0) return (K == 1024 || K == 4096) && row_bytes == (uint64_t)K / 32 * 34;
+    if (type == GGML_TYPE_Q5_K) return (K == 1024 || K == 4096) && row_bytes == (uint64_t)K / 256 * 176;
+    if (type == GGML_TYPE_MXFP4) return K == 4096 && row_bytes == (uint64_t)K / 32 * 17;
     return false;
 }
 
@@ -456,7 +459,12 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
                 return matvec_tile<GGML_TYPE_Q4_K, 8192, 4>(a, s);
             }
             return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
-        case GGML_TYPE_Q5_K: return matvec_t<GGML_TYPE_Q5_K, 2>(a, s, n_cu);
+        case GGML_TYPE_Q5_K:
+            if (a.xf && tile_shape(type, a.row_bytes, a.K)) {   // tile-staged path
+                if (a.K == 1024) return matvec_tile<GGML_TYPE_Q5_K, 1024, 16>(a, s);
+                return matvec_tile<GGML_TYPE_Q5_K, 4096, 4>(a, s);
+            }
+            return matvec_t<GGML_TYPE_Q5_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q6_K:
             if (a.xf && a.row_bytes == (uint64_t)a.K / 256 * 210 && a.K % 256 == 0 && a.K <= 1024) {   // tile-staged path
                 if (a.K == 1024) return matvec_q6k_tile<4>(a, s);
@@ -471,7 +479,9 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
                 return matvec_tile<GGML_TYPE_Q8_0, 4096, 4>(a, s);
             }
             return matvec_t<GGML_TYPE_Q8_0, 2>(a, s, n_cu);
-        case GGML_TYPE_MXFP4: return matvec_t<GGML_TYPE_MXFP4, 2>(a, s, n_cu);
+        case GGML_TYPE_MXFP4:
+            if (a.xf && tile_shape(type, a.row_bytes, a.K)) return matvec_tile<GGML_TYPE_MXFP4, 4096, 8>(a, s);
+            return matvec_t<GGML_TYPE_MXFP4, 2>(a, s, n_cu);
         default: return hipErrorInvalidValue;
     }
 }

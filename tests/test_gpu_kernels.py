@@ -105,7 +105,7 @@ def test_matvec_baseline_configs(gpu, name, t, M, K, ws, xs):
 @pytest.mark.parametrize("t,M,K", [
     (O.Q4_K, 1, 256), (O.Q4_K, 3, 512), (O.Q4_K, 7, 1024), (O.Q4_K, 33, 2048), (O.Q4_K, 5, 3072),
     (O.Q4_K, 9, 8192), (O.Q4_K, 2, 16384),
-    (O.Q4_K, 1, 4096), (O.Q4_K, 13, 4096), (O.Q4_K, 70, 4096), (O.Q4_K, 5, 8192), (O.Q4_K, 12, 8192), (O.Q5_K, 17, 1024), (O.Q5_K, 8, 4096),
+    (O.Q4_K, 1, 4096), (O.Q4_K, 13, 4096), (O.Q4_K, 70, 4096), (O.Q4_K, 5, 8192), (O.Q4_K, 12, 8192), (O.Q5_K, 17, 1024), (O.Q5_K, 8, 4096), (O.Q5_K, 1, 1024), (O.Q5_K, 37, 4096),
     (O.Q6_K, 1, 256), (O.Q6_K, 11, 768), (O.Q6_K, 17, 1024), (O.Q6_K, 40, 512), (O.Q6_K, 64, 3072),
     (O.Q6_K, 3, 16384),
     (O.Q8_0, 1, 32), (O.Q8_0, 5, 96), (O.Q8_0, 19, 4096), (O.Q8_0, 2, 8192),
@@ -133,7 +133,7 @@ def test_matvec_activation_extremes(gpu):
     assert parity_err(got, ref) <= TOL
 
 
-@pytest.mark.parametrize("M,K", [(1, 32), (5, 96), (64, 4096), (33, 2880), (7, 8192)])
+@pytest.mark.parametrize("M,K", [(1, 32), (5, 96), (64, 4096), (33, 2880), (7, 8192), (13, 4096)])
 def test_matvec_mxfp4(gpu, M, K):
     """MXFP4 (E8M0 + E2M1, reference src/quant.c:290-337) matvec on random
     blocks, including NaN-exponent (0xFF) blocks that the reference zeroes."""
