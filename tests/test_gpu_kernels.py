@@ -157,6 +157,7 @@ def test_matvec_mxfp4(gpu, M, K):
 
 
 @pytest.mark.parametrize("t,M,K,per_x", [(O.Q4_K, 1024, 4096, False), (O.Q4_K, 1000, 4096, True),
+                                         (O.Q5_K, 520, 1024, True), (O.Q8_0, 100, 4096, False),
                                          (O.Q6_K, 4096, 1024, True),
                                          (O.Q8_0, 256, 1024, True)])
 def test_matvec_batched(gpu, t, M, K, per_x):
