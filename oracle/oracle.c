@@ -15,6 +15,10 @@
  *   Q8_K path          quantize bit-exact vs oracle/_ref; dots vs oracle/_ref
  *   moe layer          vs a composition of oracle/_ref's mat_vec_mul/softmax/
  *                      top_k (golden fixture) and an fp64 re-evaluation
+ *   bf16 rounding      vs torch over 1M bit patterns and every halfway case
+ *   prefill            fo_moe_prefill_w vs an fp64 numpy recomposition, for
+ *                      each bf16 weight-rounding mask; routing vs the decode
+ *                      layer's
  *   synth/quantizers   own definition: round-trip error bounds, code ranges
  */
 #include "oracle.h"
