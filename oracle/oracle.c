@@ -15,7 +15,8 @@
  *   Q8_K path          quantize bit-exact vs oracle/_ref; dots vs oracle/_ref
  *   moe layer          vs a composition of oracle/_ref's mat_vec_mul/softmax/
  *                      top_k (golden fixture) and an fp64 re-evaluation
- *   bf16 rounding      vs torch over 1M bit patterns and every halfway case
+ *   bf16 rounding      vs torch over 1M random bit patterns, 4096 halfway cases
+ *                      and the range edges
  *   prefill            fo_moe_prefill_w vs an fp64 numpy recomposition, for
  *                      each bf16 weight-rounding mask; routing vs the decode
  *                      layer's
