@@ -285,6 +285,88 @@ __global__ __launch_bounds__((ExpandShape<T, TR, U>::THREADS), 3) void k_expand(
     }
 }
 
+// K2 for Q4_K gate/up at H = 4096 (TR = 16, one 64-value slot per lane): each
+// wave's 4 gate rows and 4 up rows are two contiguous 9 KiB spans, streamed
+// with non-temporal 1 KiB loads and passed through a 9 KiB wave-private LDS
+// area (gate first, then up: the wave's reads of the gate rows precede its
+// writes of the up rows in LDS order), the slot dots reading from there.
+__global__ __launch_bounds__(256, 3) void k_expand_q4t(ExpandArgs a) {
+    constexpr int T = GGML_TYPE_Q4_K, TR = 16, G = 64, U = 1;
+    constexpr int RB = 2304, SPAN = 4 * RB, NP = SPAN / 1024;
+    using F = Fmt<T>;
+    constexpr int RW = ExpandShape<T, TR, U>::RW;       // rows per wave
+    constexpr int NW = TR / RW;                         // waves
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];   // prepared h, then NW row spans
+    __shared__ int s_ids[kMaxK];
+    __shared__ float s_w[kMaxK], s_val[kMaxK];
+    __shared__ float2 s_cand[64];
+    __shared__ float s_act[TR];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int H = a.H, F_ = a.F;
+    const int tpe = F_ / TR;
+    const int e = blockIdx.x / tpe, rb = blockIdx.x - e * tpe;
+    const bool routed = e < a.k;
+    const uint64_t xqb = xq_bytes(H, F::GSZ);
+    // the prepared h streams into LDS while wave 0 selects experts
+    stage_lds(lds, a.xq_h, (uint32_t)xqb, wv, NW);
+    // A routed WG of rank e needs only the first e+1 selections; the full
+    // top-k with weights (for K3) is computed once, by the first WG that has
+    // nothing else to wait for (the shared expert's first task, or WG 0).
+    const bool full = a.shared ? (e == a.k && rb == 0) : blockIdx.x == 0;
+    const int rounds = full ? a.k : (routed ? e + 1 : 0);
+    if (wv == 0 && rounds > 0) {
+        // one or two selections: arg-max rounds; more: the threshold ranking
+        if (rounds <= 2) {
+            if (a.E <= 512) wave_topk<8>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
+            else wave_topk<16>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr);
+        } else {
+            if (a.E <= 512) wave_topk_thr<8>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr, s_cand, s_val);
+            else wave_topk_thr<16>(a.logits, a.E, rounds, s_ids, full ? s_w : nullptr, s_cand, s_val);
+        }
+        if (full && lane < a.k) { a.ids[lane] = s_ids[lane]; a.weights[lane] = s_w[lane]; }
+    }
+    stage_lds_wait();
+    const uint8_t *blob;
+    uint64_t uo;
+    if (routed) { blob = a.base + (uint64_t)s_ids[e] * a.stride; uo = a.gate_size; }
+    else { blob = a.shared; uo = a.sh_gate_size; }
+    const uint8_t *g0 = blob + (uint64_t)(rb * TR + wv * RW) * RB, *u0 = g0 + uo;
+    uint4 vg[NP], vu[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) vg[i] = ldw16(g0 + i * 1024 + lane * 16);
+#pragma unroll
+    for (int i = 0; i < NP; i++) vu[i] = ldw16(u0 + i * 1024 + lane * 16);
+    // keep the scheduler from sinking the up loads below the gate arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+    typename F::X X;
+    {
+        int gi[F::NG];
+        F::groups(lane, gi);
+        load_xslot(X, lds, H, gi);
+    }
+    uint8_t *buf = lds + lds_round(xqb) + wv * SPAN;
+    float g[RW], v[RW];
+#pragma unroll
+    for (int i = 0; i < NP; i++) *(uint4 *)(buf + i * 1024 + lane * 16) = vg[i];
+#pragma unroll
+    for (int r = 0; r < RW; r++) g[r] = group_sum<G>(F::dot(F::load(buf + r * RB, lane), lane, X));
+#pragma unroll
+    for (int i = 0; i < NP; i++) *(uint4 *)(buf + i * 1024 + lane * 16) = vu[i];
+#pragma unroll
+    for (int r = 0; r < RW; r++) v[r] = group_sum<G>(F::dot(F::load(buf + r * RB, lane), lane, X));
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RW; r++) s_act[wv * RW + r] = (g[r] / (1.0f + expf(-g[r]))) * v[r];
+    }
+    __syncthreads();
+    if (wv == 0) {
+        const float val = lane < TR ? s_act[lane] : 0.f;
+        uint8_t *dst = a.xq_act + (uint64_t)e * a.xq_vstride;
+        prep_group_lanes<TR>(val, rb, dst, dst + xq_limb_bytes(F_));
+        if (a.act && lane < TR) a.act[(uint64_t)e * F_ + rb * TR + lane] = val;
+    }
+}
+
 hipError_t launch_expand(int type, const ExpandArgs &a, hipStream_t s, int n_cu) {
     (void)n_cu;
     const int slot = type == GGML_TYPE_Q8_0 ? 32 : 64;
@@ -300,6 +382,10 @@ hipError_t launch_expand(int type, const ExpandArgs &a, hipStream_t s, int n_cu)
     const int n_tot = a.k + (a.shared ? 1 : 0);
     const size_t lds = lds_round(xq_bytes(a.H, type == GGML_TYPE_Q6_K ? 16 : 32));
     const int grid = a.F / TR * n_tot;
+    if (type == GGML_TYPE_Q4_K && TR == 16 && G == 64 && U == 1) {   // gate/up at H = 4096: row spans through LDS
+        k_expand_q4t<<<grid, ExpandShape<GGML_TYPE_Q4_K, 16, 1>::THREADS, lds + 4 * 2304 * 4, s>>>(a);
+        return hipGetLastError();
+    }
 #define FO_K2(TT, RR, GG, UU) \
     if (type == TT && TR == RR && G == GG && U == UU) { k_expand<TT, RR, GG, UU><<<grid, ExpandShape<TT, RR, UU>::THREADS, lds, s>>>(a); return hipGetLastError(); }
 #define FO_K2T(TT) \
