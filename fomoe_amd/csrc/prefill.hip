@@ -52,46 +52,61 @@ FO_DEV uint32_t pack_bf16(float lo, float hi) {   // round to nearest even, lo i
 }
 
 // ============================================================ P1 router GEMM
-constexpr int kRT = 32, kRK = 64;   // 32 tokens x 32 experts per WG, K chunks of 64
+// 32 tokens x 32 experts per work-group (4 waves, one 16 x 16 block each) on
+// v_mfma_f32_16x16x4_f32: fp32 operands (x widened exactly from bf16), fp32
+// accumulate. K runs in chunks of 64 staged in LDS (double-buffered, rows
+// padded by 4 floats so the 16 rows an operand read touches fall on distinct
+// banks), the next chunk held in registers while the current one is multiplied.
+constexpr int kRT = 32, kRK = 64, kRKP = kRK + 4;
 
 __global__ __launch_bounds__(256) void k_pf_router(PrefillArgs a) {
-    __shared__ float xs[kRK][kRT + 1];
-    __shared__ float rs[kRK][kRT + 1];
-    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+    __shared__ __attribute__((aligned(16))) float xs[2][kRT][kRKP];
+    __shared__ __attribute__((aligned(16))) float rs[2][kRT][kRKP];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.y * kRT, e0 = blockIdx.x * kRT;
-    const int lt = tid >> 3, lk = (tid & 7) * 8;          // loader: row lt, 8 values at lk
-    const int tl = min(t0 + lt, a.T - 1), el = min(e0 + lt, a.E - 1);
-    const uint16_t *xp = a.x + (uint64_t)tl * a.H + lk;
-    const float *rp = a.router + (uint64_t)el * a.H + lk;
-    float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
-    for (int k0 = 0; k0 < a.H; k0 += kRK) {
-        const uint4 xv = *(const uint4 *)(xp + k0);
-        const float4 r0 = *(const float4 *)(rp + k0), r1 = *(const float4 *)(rp + k0 + 4);
-        __syncthreads();
+    const int lr = tid >> 3, lk = (tid & 7) * 8;          // loader: row lr, 8 values at lk
+    const uint16_t *xp = a.x + (uint64_t)min(t0 + lr, a.T - 1) * a.H + lk;
+    const float *rp = a.router + (uint64_t)min(e0 + lr, a.E - 1) * a.H + lk;
+    uint4 xv;
+    float4 r0, r1;
+    auto fetch = [&](int k0) {
+        xv = *(const uint4 *)(xp + k0);
+        r0 = *(const float4 *)(rp + k0);
+        r1 = *(const float4 *)(rp + k0 + 4);
+    };
+    auto put = [&](int b) {
         const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        float4 x0 = make_float4(bf2f(xw[0] & 0xFFFFu), bf2f(xw[0] >> 16), bf2f(xw[1] & 0xFFFFu), bf2f(xw[1] >> 16));
+        float4 x1 = make_float4(bf2f(xw[2] & 0xFFFFu), bf2f(xw[2] >> 16), bf2f(xw[3] & 0xFFFFu), bf2f(xw[3] >> 16));
+        *(float4 *)&xs[b][lr][lk] = x0;
+        *(float4 *)&xs[b][lr][lk + 4] = x1;
+        *(float4 *)&rs[b][lr][lk] = r0;
+        *(float4 *)&rs[b][lr][lk + 4] = r1;
+    };
+    const int tb = wv >> 1, eb = wv & 1, row = lane & 15, kq = lane >> 4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    put(0);
+    __syncthreads();
+    const int NKC = a.H / kRK;
+    for (int kc = 0; kc < NKC; kc++) {
+        const int b = kc & 1;
+        if (kc + 1 < NKC) fetch((kc + 1) * kRK);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            xs[lk + 2 * i][lt] = bf2f(xw[i] & 0xFFFFu);
-            xs[lk + 2 * i + 1][lt] = bf2f(xw[i] >> 16);
+        for (int kk = 0; kk < kRK; kk += 4) {
+            const float av = xs[b][16 * tb + row][kk + kq];
+            const float bv = rs[b][16 * eb + row][kk + kq];
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
         }
-        rs[lk + 0][lt] = r0.x; rs[lk + 1][lt] = r0.y; rs[lk + 2][lt] = r0.z; rs[lk + 3][lt] = r0.w;
-        rs[lk + 4][lt] = r1.x; rs[lk + 5][lt] = r1.y; rs[lk + 6][lt] = r1.z; rs[lk + 7][lt] = r1.w;
+        if (kc + 1 < NKC) put(b ^ 1);
         __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < kRK; k++) {
-            const float x0 = xs[k][2 * ty], x1 = xs[k][2 * ty + 1];
-            const float w0 = rs[k][2 * tx], w1 = rs[k][2 * tx + 1];
-            acc[0][0] = fmaf(x0, w0, acc[0][0]); acc[0][1] = fmaf(x0, w1, acc[0][1]);
-            acc[1][0] = fmaf(x1, w0, acc[1][0]); acc[1][1] = fmaf(x1, w1, acc[1][1]);
-        }
     }
+    // D layout: lane holds rows 4*(lane/16)+i (tokens) of column lane%16 (expert)
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int t = t0 + 2 * ty + i, e = e0 + 2 * tx + j;
-            if (t < a.T && e < a.E) a.logits[(uint64_t)t * a.E + e] = acc[i][j] + (a.router_bias ? a.router_bias[e] : 0.f);
-        }
+    for (int i = 0; i < 4; i++) {
+        const int t = t0 + 16 * tb + 4 * kq + i, e = e0 + 16 * eb + row;
+        if (t < a.T && e < a.E) a.logits[(uint64_t)t * a.E + e] = acc[i] + (a.router_bias ? a.router_bias[e] : 0.f);
+    }
 }
 
 // ============================================================ P2 top-k
@@ -633,16 +648,44 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
 #pragma clang fp contract(on)
 
 // ============================================================ P6 combine
+// One work-group per token; each thread owns float4 columns and requests all
+// of the token's pair rows for a column before summing them in rank order.
 __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
-    const int t = blockIdx.x, K1 = a.k + 1;
-    const int32_t *pp = a.pairpos + (uint64_t)t * K1;
-    const float *w = a.w + (uint64_t)t * K1;
-    for (int i = threadIdx.x; i < a.H; i += 256) {
-        float acc = 0.f;
-        for (int r = 0; r < a.k; r++) acc = acc + w[r] * a.outp[(uint64_t)pp[r] * a.H + i];
-        if (a.shared) acc = acc + a.outp[(uint64_t)pp[a.k] * a.H + i] * w[a.k];
-        const float x = a.residual ? bf2f(a.x[(uint64_t)t * a.H + i]) : 0.f;
-        a.out[(uint64_t)t * a.H + i] = a.residual ? x + acc : acc;
+    __shared__ int s_pp[kMaxK + 1];
+    __shared__ float s_w[kMaxK + 1];
+    const int t = blockIdx.x, K1 = a.k + 1, n = a.k + (a.shared ? 1 : 0);
+    if ((int)threadIdx.x < K1) {
+        s_pp[threadIdx.x] = a.pairpos[(uint64_t)t * K1 + threadIdx.x];
+        s_w[threadIdx.x] = a.w[(uint64_t)t * K1 + threadIdx.x];
+    }
+    __syncthreads();
+    for (int i4 = threadIdx.x; i4 < a.H / 4; i4 += 256) {
+        float4 o[kMaxK + 1];
+#pragma unroll
+        for (int r = 0; r <= kMaxK; r++)
+            if (r < n) o[r] = *(const float4 *)(a.outp + (uint64_t)s_pp[r] * a.H + 4 * i4);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int r = 0; r < kMaxK; r++)
+            if (r < a.k) {
+                acc.x = acc.x + s_w[r] * o[r].x; acc.y = acc.y + s_w[r] * o[r].y;
+                acc.z = acc.z + s_w[r] * o[r].z; acc.w = acc.w + s_w[r] * o[r].w;
+            }
+        if (a.shared) {
+            float4 sh = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int r = 0; r <= kMaxK; r++)
+                if (r == a.k) sh = o[r];
+            const float ws = s_w[a.k];
+            acc.x = acc.x + sh.x * ws; acc.y = acc.y + sh.y * ws;
+            acc.z = acc.z + sh.z * ws; acc.w = acc.w + sh.w * ws;
+        }
+        if (a.residual) {
+            const uint2 xb = *(const uint2 *)(a.x + (uint64_t)t * a.H + 4 * i4);
+            acc.x = bf2f(xb.x & 0xFFFFu) + acc.x; acc.y = bf2f(xb.x >> 16) + acc.y;
+            acc.z = bf2f(xb.y & 0xFFFFu) + acc.z; acc.w = bf2f(xb.y >> 16) + acc.w;
+        }
+        *(float4 *)(a.out + (uint64_t)t * a.H + 4 * i4) = acc;
     }
 }
 
