@@ -229,10 +229,11 @@ static hipError_t matvec_t(const MatvecArgs &a, hipStream_t s, int n_cu) {
 // with the 64 codes of slot (n = g>>1, j = g&1) for one t; A = the activation
 // limbs routed so that D lane (row, g) receives the three limb sums of its own
 // 16-value scale group, rows 4g..4g+2 of A being nonzero only over lane group
-// g's k-range (other lanes read a 16-byte zero slot). D layout: lane holds
+// g's k-range (other lanes read zeros). D layout: lane holds
 // rows 4*(lane/16)+i of column lane%16. Group scales / offsets / sub-block
 // scales are then applied per lane as in Fmt<Q6_K>.
 constexpr int kT6Rows = 16, kT6MaxNV = 14;   // 16 rows x 840 B <= 14 KiB
+constexpr uint32_t kT6Zero = 304;            // zero A operands: 16 bytes at offsets 0, 96, 192, 288
 
 template <int NSB, int TPW>
 __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
@@ -242,32 +243,50 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
     const int lane = threadIdx.x;
     const int mat = blockIdx.y;
     constexpr uint32_t limb_bytes = 3u * K, xbytes = limb_bytes + (K / 16) * 8;
-    constexpr uint32_t zoff = (xbytes + 15) & ~15u;    // 16 zero bytes for the A rows of other groups
-    uint8_t *tb = sx + zoff + 16;
+    constexpr uint32_t zoff = (xbytes + 15) & ~15u;    // zero A operands for the rows of other groups
+    uint8_t *tb = sx + zoff + kT6Zero;
     float *ys = (float *)(tb + NV * 1024);             // [TPW * 16] results
     const uint8_t *Wm = a.W + mat * a.mat_stride;
     constexpr uint32_t rb = NSB * 210;                 // launched only for contiguous rows
+    constexpr uint32_t full_bytes = kT6Rows * rb;
     const int tile0 = blockIdx.x * TPW;
     const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
     // A piece that straddles the end of a partial tile (16*rows*rb need not be a
     // multiple of 16) is read from the last 16 valid bytes and written to that
-    // same LDS position (overlapping its neighbour with identical bytes).
+    // same LDS position (overlapping its neighbour with identical bytes). A
+    // whole tile is a multiple of 16 bytes: only its last piece is clamped on
+    // the read, and every piece lands at its own offset (the staging area has
+    // NV KiB, so lanes past the end write unused bytes).
     auto tile_bytes = [&](int tile) { return (uint32_t)min(kT6Rows, a.M - tile * kT6Rows) * rb; };
     auto pos = [&](uint32_t o, uint32_t nb) { return o + 16 <= nb ? o : nb - 16; };
     auto issue = [&](uint4 (&v)[NV], int tile) {
-        const uint32_t nb = tile_bytes(tile);
         const uint8_t *tp = Wm + (uint64_t)tile * kT6Rows * rb;
+        const uint32_t nb = tile_bytes(tile);
+        if (nb == full_bytes) {
 #pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = ldw16(tp + pos(i * 1024 + lane * 16, nb));
+            for (int i = 0; i < NV; i++) v[i] = ldw16(tp + min(i * 1024u + lane * 16u, full_bytes - 16));
+        } else {
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = ldw16(tp + pos(i * 1024 + lane * 16, nb));
+        }
     };
     // one register buffer: tile t+1 is requested right after tile t has been
     // copied to LDS, so its loads overlap tile t's arithmetic (measured faster
     // than two buffers, which need more registers for no more overlap)
     uint4 v[NV];
     if (tile0 < ntiles) issue(v, tile0);
-    // the activation is prepared here, one lane per 16-value group (K <= 1024)
-    if (lane < K / 16) prep_group<16>(a.xf + mat * a.xf_stride + lane * 16, sx + lane * 48, sx + limb_bytes + lane * 8);
-    if (lane == 0) *(uint4 *)(sx + zoff) = make_uint4(0, 0, 0, 0);
+    // the activation is prepared here, one lane per 16-value group (K <= 1024);
+    // the group's {scale, -32 * sum} folds the Q6_K code offset into one fma
+    if (lane < K / 16) {
+        int limb[kLimbs][4];
+        float scale, sum;
+        prep_group_regs<16>(a.xf + mat * a.xf_stride + lane * 16, limb, scale, sum);
+#pragma unroll
+        for (int L = 0; L < kLimbs; L++)
+            *(uint4 *)(sx + lane * 48 + 16 * L) = make_uint4(limb[L][0], limb[L][1], limb[L][2], limb[L][3]);
+        *(float2 *)(sx + limb_bytes + lane * 8) = make_float2(scale, -32.f * sum);
+    }
+    if (lane < kT6Zero / 16) *(uint4 *)(sx + zoff + 16 * lane) = make_uint4(0, 0, 0, 0);
     __syncthreads();
     const int r = lane & 15, g = lane >> 4, n = g >> 1, j = g & 1, L = r & 3;
     const bool valid = (r >> 2) == g && L < 3;
@@ -279,17 +298,27 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
         if (tile >= ntiles) break;
         {
             const uint32_t nb = tile_bytes(tile);
+            if (nb == full_bytes) {
 #pragma unroll
-            for (int i = 0; i < NV; i++) {
-                const uint32_t o = i * 1024 + lane * 16;
-                *(uint4 *)(tb + (o < nb ? pos(o, nb) : o)) = v[i];
+                for (int i = 0; i < NV; i++) *(uint4 *)(tb + i * 1024 + lane * 16) = v[i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < NV; i++) {
+                    const uint32_t o = i * 1024 + lane * 16;
+                    *(uint4 *)(tb + (o < nb ? pos(o, nb) : o)) = v[i];
+                }
             }
         }
         if (tt + 1 < TPW && tile + 1 < ntiles) issue(v, tile + 1);
         const uint8_t *rp = tb + r * rb;
         float acc = 0.f;
+        // every super-block's bytes requested before the first MFMA
+        Q6kSlot qs[NSB];
 #pragma unroll
-        for (int b = 0; b < NSB; b++) acc += q6k_sb_dot_mfma(rp + b * 210, abase, ssb, 16 * b, n, j, valid, sx + zoff);
+        for (int b = 0; b < NSB; b++) q6k_slot_load(qs[b], rp + b * 210, n, j);
+#pragma unroll
+        for (int b = 0; b < NSB; b++)   // group 16b + 8n + 2t + j: limbs at +768 b, {scale, offset} at +128 b
+            acc += q6k_sb_dot_mfma(qs[b], valid ? abase + 768 * b : sx + zoff, ssb + 128 * b, j);
         acc += __shfl_xor(acc, 16);
         acc += __shfl_xor(acc, 32);
         if (g == 0) ys[tt * kT6Rows + r] = acc;
@@ -307,7 +336,7 @@ template <int NSB>
 static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
     constexpr int TPW = 8, K = NSB * 256;
     const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
-    const uint32_t lds = ((xq_bytes(K, 16) + 15) & ~15u) + 16 +
+    const uint32_t lds = ((xq_bytes(K, 16) + 15) & ~15u) + kT6Zero +
                          (uint32_t)((kT6Rows * NSB * 210 + 1023) / 1024) * 1024 + TPW * kT6Rows * 4;
     k_matvec_q6k_tile<NSB, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
     return hipGetLastError();
