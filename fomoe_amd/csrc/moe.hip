@@ -346,14 +346,23 @@ __global__ __launch_bounds__(256, 3) void k_expand_q4t(ExpandArgs a) {
     }
     uint8_t *buf = lds + lds_round(xqb) + wv * SPAN;
     float g[RW], v[RW];
+    // row by row as the pieces arrive (loads retire in issue order): row r
+    // waits only for the pieces that cover it, so the arithmetic of the early
+    // rows overlaps the arrival of the later ones
+    auto rows = [&](uint4 (&p)[NP], float (&out)[RW]) {
+        int written = 0;
 #pragma unroll
-    for (int i = 0; i < NP; i++) *(uint4 *)(buf + i * 1024 + lane * 16) = vg[i];
+        for (int r = 0; r < RW; r++) {
+            const int need = ((r + 1) * RB + 1023) / 1024;
 #pragma unroll
-    for (int r = 0; r < RW; r++) g[r] = group_sum<G>(F::dot(F::load(buf + r * RB, lane), lane, X));
-#pragma unroll
-    for (int i = 0; i < NP; i++) *(uint4 *)(buf + i * 1024 + lane * 16) = vu[i];
-#pragma unroll
-    for (int r = 0; r < RW; r++) v[r] = group_sum<G>(F::dot(F::load(buf + r * RB, lane), lane, X));
+            for (int i = 0; i < NP; i++)
+                if (i >= written && i < need) *(uint4 *)(buf + i * 1024 + lane * 16) = p[i];
+            written = need;
+            out[r] = group_sum<G>(F::dot(F::load(buf + r * RB, lane), lane, X));
+        }
+    };
+    rows(vg, g);
+    rows(vu, v);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < RW; r++) s_act[wv * RW + r] = (g[r] / (1.0f + expf(-g[r]))) * v[r];
