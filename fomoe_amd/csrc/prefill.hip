@@ -283,6 +283,18 @@ FO_DEV u32x4 pf_decode(const typename PfDec<T>::Sb &s, int ch, int kg) {
 FO_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // ============================================================ P4/P5 grouped GEMMs
+// Work-group placement: a 1-D grid of nrb * ceil8(max_tiles) work-groups,
+// numbered so that the nrb row-block work-groups of one tile have ids equal
+// mod 8. Work-group i runs on XCD i % 8 (round-robin dispatch), so all of a
+// tile's row blocks share one XCD, whose L2 serves the tile's staged
+// activation rows to every one of them (with (row block, tile) as a 2-D grid
+// each XCD held one row block of every tile and fetched every tile's rows).
+FO_DEV void pf_tile_of(int nrb, int &tile, int &rb) {
+    const int i = blockIdx.x, c = i / (8 * nrb), j = i - c * 8 * nrb;
+    tile = 8 * c + (j & 7);
+    rb = j >> 3;
+}
+inline unsigned pf_grid(int nrb, int max_tiles) { return (unsigned)(nrb * ((max_tiles + 7) & ~7)); }
 // Work-group: 4 waves, tile of <= 64 pairs (token rows) x 64 weight rows; wave
 // w owns weight rows 16w..16w+15 (MFMA columns: lane % 16) for every token
 // block. The tile's activations for one 256-value super-block sit in LDS
@@ -318,8 +330,10 @@ FO_DEV void pf_stage_async(uint16_t *buf, int n, int k0, RowPtr src_row) {
 template <int GT, int UT>
 __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[2 * kPfTile];
-    if ((int)blockIdx.y >= *a.n_tiles) return;
-    const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
+    int tile, rbk;
+    pf_tile_of(a.F / kPfGateRows, tile, rbk);
+    if (tile >= *a.n_tiles) return;
+    const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
     const int e = tl.x, p0 = tl.y, n = tl.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
     const bool shared = e == a.E;
@@ -327,7 +341,7 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup(PrefillArgs 
     constexpr int HW = kPfGateWaves / 2;
     const bool is_up = wave >= HW;
     const int rl = 32 * (wave % HW) + col;                // rows rl, rl + 16 within the WG's kPfGateRows
-    const int row = blockIdx.x * kPfGateRows + rl;
+    const int row = rbk * kPfGateRows + rl;
     const int nb = (n + 15) >> 4, NK = a.H / 256;
     const int32_t *toks = a.pair_tok + p0;
     auto xrow = [&](int m) { return a.x + (uint64_t)toks[m] * a.H; };
@@ -468,8 +482,10 @@ FO_DEV float2 q4_sub_scales(const uint4 &hdr, int j) {
 __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[2 * kPfTile];
     __shared__ __attribute__((aligned(16))) float ss[2][8][kPfMT];
-    if ((int)blockIdx.y >= *a.n_tiles) return;
-    const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
+    int tile, rbk;
+    pf_tile_of(a.F / kPfGateRows, tile, rbk);
+    if (tile >= *a.n_tiles) return;
+    const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
     const int e = tl.x, p0 = tl.y, n = tl.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
     const bool shared = e == a.E;
@@ -477,7 +493,7 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillAr
     constexpr int HW = kPfGateWaves / 2;
     const bool is_up = wave >= HW;
     const int rl = 32 * (wave % HW) + col;
-    const int row = blockIdx.x * kPfGateRows + rl;
+    const int row = rbk * kPfGateRows + rl;
     const int nb = (n + 15) >> 4, NK = a.H / 256, nsb = a.H / 32;
     const int32_t *toks = a.pair_tok + p0;
     auto xrow = [&](int m) { return a.x + (uint64_t)toks[m] * a.H; };
@@ -573,14 +589,16 @@ constexpr int kPfDownWaves = 8;                   // 8 waves x 32 rows = 256 wei
 template <int DT>
 __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t dxs[];   // 2 buffers x {hi, lo} tiles
-    if ((int)blockIdx.y >= *a.n_tiles) return;
-    const int4 tl = *(const int4 *)(a.tiles + 4 * blockIdx.y);
+    int tile, rbk;
+    pf_tile_of(a.H / (32 * kPfDownWaves), tile, rbk);
+    if (tile >= *a.n_tiles) return;
+    const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
     const int e = tl.x, p0 = tl.y, n = tl.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
     const bool shared = e == a.E;
     const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
     const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
-    const int row = blockIdx.x * (32 * kPfDownWaves) + 32 * wave + col;   // rows row, row + 16
+    const int row = rbk * (32 * kPfDownWaves) + 32 * wave + col;   // rows row, row + 16
     const uint64_t db = (uint64_t)(a.F / 256) * PfDec<DT>::BLOCK;
     const uint8_t *drow = blob + down_off + (uint64_t)row * db, *drow1 = drow + 16 * db;
     const int nb = (n + 15) >> 4, NK = a.F / 256;
@@ -703,7 +721,7 @@ hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStr
 // ============================================================ launcher
 template <int GT, int UT>
 static hipError_t launch_gateup_t(const PrefillArgs &a, hipStream_t s) {
-    k_pf_gateup<GT, UT><<<dim3(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
+    k_pf_gateup<GT, UT><<<pf_grid(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -731,7 +749,7 @@ hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
     if (a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K) {   // scale-after path
         const int64_t n = (int64_t)a.T * (a.H / 32);
         k_pf_xsum<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(a);
-        k_pf_gateup_q4<<<dim3(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
+        k_pf_gateup_q4<<<pf_grid(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
         err = hipGetLastError();
     }
 #define FO_GU(G, U) if (a.gate_type == G && a.up_type == U) err = launch_gateup_t<G, U>(a, s);
@@ -741,7 +759,7 @@ hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
     if (err != hipSuccess) return err;
     {
         const size_t lds = 4 * (size_t)kPfTile * sizeof(uint16_t);       // 128 KiB
-        const dim3 grid(a.H / (32 * kPfDownWaves), a.max_tiles);
+        const unsigned grid = pf_grid(a.H / (32 * kPfDownWaves), a.max_tiles);
         static bool down_attr = false;
         if (!down_attr) {
             hipError_t e1 = hipFuncSetAttribute((const void *)k_pf_down<GGML_TYPE_Q4_K>,
