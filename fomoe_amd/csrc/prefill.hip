@@ -322,6 +322,23 @@ FO_DEV void pf_stage_async(uint16_t *buf, int n, int k0, RowPtr src_row) {
     }
 }
 
+// Token rows of a tile: lane m of `tok` holds the token of tile row m (rows
+// past n repeat the last one). The row addresses come from it by readlane, so
+// no staging load waits for an index load (waiting for the newest load is
+// waiting for every load in flight: each row load used to drain the wave).
+FO_DEV void pf_stage_tokens(uint16_t *buf, int n, int k0, const uint16_t *x, int H, int tok) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int rows = (n + 15) & ~15;
+    for (int q = wave; q < rows / 2; q += nw) {
+        const int m = 2 * q + (lane >> 5), cs = lane & 31;
+        const int c = cs ^ (m & 15);
+        const int ta = __builtin_amdgcn_readlane(tok, 2 * q), tb = __builtin_amdgcn_readlane(tok, 2 * q + 1);
+        const uint16_t *src = x + (uint64_t)(lane < 32 ? ta : tb) * H + k0 + 8 * c;
+        __builtin_amdgcn_global_load_lds((const void *)src,
+                                         (__attribute__((address_space(3))) void *)(buf + q * 512), 16, 0, 0);
+    }
+}
+
 #pragma clang fp contract(off)
 // Work-group: kPfGateWaves waves over kPfGateRows rows of F: the first half
 // computes the gate rows, the second half the same up rows, for every token
@@ -344,7 +361,7 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup(PrefillArgs 
     const int row = rbk * kPfGateRows + rl;
     const int nb = (n + 15) >> 4, NK = a.H / 256;
     const int32_t *toks = a.pair_tok + p0;
-    auto xrow = [&](int m) { return a.x + (uint64_t)toks[m] * a.H; };
+    const int my_tok = toks[min(lane, n - 1)];
     f32x4 acc[2][4];
 #pragma unroll
     for (int h = 0; h < 2; h++)
@@ -353,7 +370,7 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup(PrefillArgs 
     auto run = [&](auto dec, const uint8_t *w0, uint64_t rowb) {
         using D = decltype(dec);
         const uint8_t *w1 = w0 + 16 * rowb;
-        pf_stage_async(xs, n, 0, xrow);
+        pf_stage_tokens(xs, n, 0, a.x, a.H, my_tok);
         auto s0_next = D::load(w0, kg);
         auto s1_next = D::load(w1, kg);
         for (int kb = 0; kb < NK; kb++) {
@@ -362,7 +379,7 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup(PrefillArgs 
             const auto s0 = s0_next;
             const auto s1 = s1_next;
             if (kb + 1 < NK) {
-                pf_stage_async(xs + ((kb + 1) & 1) * kPfTile, n, (kb + 1) * 256, xrow);
+                pf_stage_tokens(xs + ((kb + 1) & 1) * kPfTile, n, (kb + 1) * 256, a.x, a.H, my_tok);
                 s0_next = D::load(w0 + (uint64_t)(kb + 1) * D::BLOCK, kg);
                 s1_next = D::load(w1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
             }
@@ -496,9 +513,9 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillAr
     const int row = rbk * kPfGateRows + rl;
     const int nb = (n + 15) >> 4, NK = a.H / 256, nsb = a.H / 32;
     const int32_t *toks = a.pair_tok + p0;
-    auto xrow = [&](int m) { return a.x + (uint64_t)toks[m] * a.H; };
+    const int my_tok = toks[min(lane, n - 1)];
     // S of super-block kb: waves 0..7 each load one sub-block's 64 token sums
-    const float *srow = a.xsum + (uint64_t)toks[min(lane, n - 1)] * nsb;
+    const float *srow = a.xsum + (uint64_t)my_tok * nsb;
     auto stage_s = [&](int kb) {
         if (wave < 8)
             __builtin_amdgcn_global_load_lds((const void *)(srow + kb * 8 + wave),
@@ -513,7 +530,7 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillAr
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
     using D = PfDec<GGML_TYPE_Q4_K>;
-    pf_stage_async(xs, n, 0, xrow);
+    pf_stage_tokens(xs, n, 0, a.x, a.H, my_tok);
     stage_s(0);
     auto s0_next = D::load(w0, kg);
     auto s1_next = D::load(w1, kg);
@@ -523,7 +540,7 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillAr
         const auto s0 = s0_next;
         const auto s1 = s1_next;
         if (kb + 1 < NK) {
-            pf_stage_async(xs + ((kb + 1) & 1) * kPfTile, n, (kb + 1) * 256, xrow);
+            pf_stage_tokens(xs + ((kb + 1) & 1) * kPfTile, n, (kb + 1) * 256, a.x, a.H, my_tok);
             stage_s(kb + 1);
             s0_next = D::load(w0 + (uint64_t)(kb + 1) * D::BLOCK, kg);
             s1_next = D::load(w1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
