@@ -12,6 +12,7 @@
 
 #include "formats.h"
 #include "kernels.h"
+#include "q4k_mfma.h"
 #include "q6k_mfma.h"
 
 namespace fo {
@@ -232,7 +233,7 @@ static hipError_t matvec_t(const MatvecArgs &a, hipStream_t s, int n_cu) {
 // g's k-range (other lanes read zeros). D layout: lane holds
 // rows 4*(lane/16)+i of column lane%16. Group scales / offsets / sub-block
 // scales are then applied per lane as in Fmt<Q6_K>.
-constexpr int kT6Rows = 16, kT6MaxNV = 14;   // 16 rows x 840 B <= 14 KiB
+constexpr int kT6Rows = 16;                  // 16 rows x 840 B <= 14 KiB per tile
 constexpr uint32_t kT6Zero = 304;            // zero A operands: 16 bytes at offsets 0, 96, 192, 288
 
 template <int NSB, int TPW>
@@ -339,6 +340,127 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
     const uint32_t lds = ((xq_bytes(K, 16) + 15) & ~15u) + kT6Zero +
                          (uint32_t)((kT6Rows * NSB * 210 + 1023) / 1024) * 1024 + TPW * kT6Rows * 4;
     k_matvec_q6k_tile<NSB, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+// ============================================================ Q4_K matvec, tile-staged MFMA
+// For Q4_K rows of K = 4096 (the expert gate/up shape). Four-wave work-groups
+// share one prepared x (13 KiB of LDS); each wave streams its own blocks of
+// 16 rows in chunks of 4 super-blocks (16 x 576 bytes = 9 KiB loaded as nine
+// 1 KiB wave pieces; each lane's 16 bytes lie within one row's 576-byte
+// segment, row segments 2304 bytes apart), the next chunk's loads in flight
+// while the current one is multiplied, writes each chunk to its LDS area and
+// runs the integer dots of all 16 rows on v_mfma_i32_16x16x64_i8 (q4k_mfma.h):
+// 16 MFMAs and ~300 VALU instructions per chunk against ~370 VALU for the same
+// bytes as per-lane slot dots. 51 KiB of LDS per work-group: 12 waves per CU. One block per
+// wave (the work-group's four blocks = 64 consecutive rows) measured fastest:
+// 6.50 TB/s against 6.34 / 6.27 / 6.24 with 2 / 4 / 8 blocks per wave. Chunks
+// 0 and 2 of a row end in the middle of a 128-byte line that chunks 1 and 3
+// begin with: those chunks load without the non-temporal hint, so the line
+// stays in L2 for the next chunk (HBM fetch 1.084 -> 1.000 x the algorithmic
+// bytes, 6.50 -> 6.85 TB/s).
+constexpr int kQ4Waves = 4, kQ4Tpw = 1;             // blocks of 16 rows per wave (2, 4, 8: slower)
+constexpr uint32_t kQ4K = 4096, kQ4Row = 2304, kQ4Chunk = 576, kQ4ChunkBytes = 16 * kQ4Chunk;
+constexpr uint32_t kQ4X = 3 * kQ4K + (kQ4K / 32) * 8;   // prepared x: limbs, then {scale, sum}
+constexpr uint32_t kQ4Zero = 416;                       // zero A operands (>= 384 + 16)
+constexpr uint32_t kQ4Lds = kQ4X + kQ4Zero + kQ4Waves * kQ4ChunkBytes + kQ4Waves * kQ4Tpw * 16 * 4;
+
+__global__ __launch_bounds__(64 * kQ4Waves, 3) void k_matvec_q4k_mfma(MatvecArgs a) {   // 3 WGs per CU
+    extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
+    constexpr int NP = kQ4ChunkBytes / 1024;             // 9 pieces per chunk
+    constexpr int NC = kQ4K / 1024;                      // 4 chunks per block (4 super-blocks each)
+    // wv through readfirstlane: the compiler then treats the wave's block
+    // addresses as uniform (SGPR base + per-lane 32-bit offset)
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), mat = blockIdx.y;
+    uint8_t *zero = sx + kQ4X;
+    uint8_t *tb = zero + kQ4Zero + wv * kQ4ChunkBytes;
+    float *ys = (float *)(sx + kQ4X + kQ4Zero + kQ4Waves * kQ4ChunkBytes);   // [waves][kQ4Tpw * 16]
+    const uint8_t *Wm = a.W + mat * a.mat_stride;
+    const int nblk = (a.M + 15) / 16;
+    const int blk0 = (blockIdx.x * kQ4Waves + wv) * kQ4Tpw;
+    // piece i of a chunk, lane l: chunk byte o = 1024 i + 16 l of row o / 576
+    uint32_t goff[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const uint32_t o = i * 1024 + lane * 16;
+        goff[i] = (o / kQ4Chunk) * kQ4Row + o % kQ4Chunk;
+    }
+    // unit u = (block t = u / NC, chunk c = u % NC) of this wave; a partial
+    // last block (M >= 16) is read as rows M-16 .. M-1, its results shifted
+    auto first_row = [&](int blk) { return min(blk * 16, a.M - 16); };
+    auto issue = [&](uint4 (&v)[NP], int u) {
+        const int blk = blk0 + u / NC, c = u % NC;
+        const uint8_t *base = Wm + (uint64_t)first_row(blk) * kQ4Row + c * kQ4Chunk;
+        if (c & 1) {
+#pragma unroll
+            for (int i = 0; i < NP; i++) v[i] = ldw16(base + goff[i]);
+        } else {   // chunks 0, 2 end mid-line: plain loads keep that line in L2 for chunks 1, 3
+#pragma unroll
+            for (int i = 0; i < NP; i++) v[i] = ld16(base + goff[i]);
+        }
+    };
+    const int nunits = min(kQ4Tpw, nblk - blk0) * NC;
+    uint4 v[NP];
+    if (nunits > 0) issue(v, 0);
+    // the work-group's x, prepared by threads 0..127 (one 32-value group each)
+    if (threadIdx.x < kQ4K / 32) {
+        const int gi = threadIdx.x;
+        int limb[kLimbs][8];
+        float scale, sum;
+        prep_group_regs<32>(a.xf + mat * a.xf_stride + gi * 32, limb, scale, sum);
+#pragma unroll
+        for (int L = 0; L < kLimbs; L++) {
+            *(uint4 *)(sx + gi * 96 + 32 * L) = make_uint4(limb[L][0], limb[L][1], limb[L][2], limb[L][3]);
+            *(uint4 *)(sx + gi * 96 + 32 * L + 16) = make_uint4(limb[L][4], limb[L][5], limb[L][6], limb[L][7]);
+        }
+        *(float2 *)(sx + 3 * kQ4K + gi * 8) = make_float2(scale, sum);
+    } else if (threadIdx.x < kQ4K / 32 + kQ4Zero / 16) {
+        *(uint4 *)(zero + 16 * (threadIdx.x - kQ4K / 32)) = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    const Q4kLane q = q4k_lane(lane);
+    const int n = lane & 15, g = lane >> 4;
+    const uint8_t *ssl = sx + 3 * kQ4K + q.jg * 8;
+#pragma unroll 1
+    for (int t = 0; t < kQ4Tpw; t++) {
+        if (t * NC >= nunits) break;
+        float y = 0.f;
+#pragma unroll 1
+        for (int c = 0; c < NC; c++) {
+            const int u = t * NC + c;
+#pragma unroll
+            for (int i = 0; i < NP; i++) *(uint4 *)(tb + i * 1024 + lane * 16) = v[i];
+            if (u + 1 < nunits) issue(v, u + 1);
+            const uint8_t *rp = tb + n * kQ4Chunk;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int sb = 4 * c + b;                    // super-block of the row: groups 8 sb ..
+                const uint8_t *xa = sx + sb * 768 + q.aoff;
+                y = q4k_sb_dot_mfma(rp + b * 144, q.valid1 ? xa : zero, q.valid2 ? xa : zero, ssl + sb * 64, q, y);
+            }
+        }
+        y += __shfl_xor(y, 16);
+        y += __shfl_xor(y, 32);
+        const int shift = (blk0 + t) * 16 - first_row(blk0 + t);
+        if (g == 0 && n >= shift) ys[(wv * kQ4Tpw + t) * 16 + n - shift] = y;
+    }
+    __syncthreads();
+    // the work-group's rows [16 * blk0(wave 0), + 16 * kQ4Waves * kQ4Tpw) leave as one store
+    const int row0 = blockIdx.x * kQ4Waves * kQ4Tpw * 16;
+    for (int r = threadIdx.x; r < kQ4Waves * kQ4Tpw * 16; r += 64 * kQ4Waves)
+        if (row0 + r < a.M) a.y[mat * a.y_stride + row0 + r] = ys[r];
+}
+
+static hipError_t matvec_q4k_mfma(const MatvecArgs &a, hipStream_t s) {
+    static bool attr = false;   // more than the 64 KiB default of dynamic LDS
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_matvec_q4k_mfma,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ4Lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const int nblk = (a.M + 15) / 16, per_wg = kQ4Waves * kQ4Tpw;
+    k_matvec_q4k_mfma<<<dim3((nblk + per_wg - 1) / per_wg, a.n_mats), 64 * kQ4Waves, kQ4Lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -484,6 +606,7 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
     switch (type) {
         case GGML_TYPE_Q4_K:
             if (a.xf && tile_shape(type, a.row_bytes, a.K)) {   // tile-staged path
+                if (a.K == 4096 && a.M >= 16) return matvec_q4k_mfma(a, s);
                 if (a.K == 4096) return matvec_tile<GGML_TYPE_Q4_K, 4096, 8>(a, s);
                 return matvec_tile<GGML_TYPE_Q4_K, 8192, 4>(a, s);
             }
