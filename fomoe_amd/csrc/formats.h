@@ -40,10 +40,10 @@ constexpr int kFixBits = 22;   // |X| < 2^22: limbs X0, X1 in [-128,127], X2 in 
 // In memory a vector of K values is [K/GSZ groups][kLimbs][GSZ/4] int32 limb
 // dwords followed by K/GSZ float2 {scale, sum} (xq_bytes in common.h).
 
+// a2 * 256 + a1 is formed exactly in int32 (|a| < 2^20 for every format) and
+// rounded once on conversion, as fmaf(a2, 256, a1) would round it
 FO_DEV float combine(const int a[kLimbs]) {
-    float f = (float)a[2];
-    f = fmaf(f, 256.f, (float)a[1]);
-    return fmaf(f, 256.f, (float)a[0]);
+    return fmaf((float)((a[2] << 8) + a[1]), 256.f, (float)a[0]);
 }
 
 FO_DEV int dot4(uint32_t codes, int limbs, int acc) {
