@@ -27,6 +27,7 @@
 
 #include "formats.h"
 #include "moe.h"
+#include "q4k_mfma.h"
 #include "topk.h"
 
 namespace fo {
@@ -285,22 +286,23 @@ __global__ __launch_bounds__((ExpandShape<T, TR, U>::THREADS), 3) void k_expand(
     }
 }
 
-// K2 for Q4_K gate/up at H = 4096 (TR = 16, one 64-value slot per lane): each
-// wave's 4 gate rows and 4 up rows are two contiguous 9 KiB spans, streamed
-// with non-temporal 1 KiB loads and passed through a 9 KiB wave-private LDS
-// area (gate first, then up: the wave's reads of the gate rows precede its
-// writes of the up rows in LDS order), the slot dots reading from there.
+// K2 for Q4_K gate/up at H = 4096 (TR = 16) on the integer MFMA of the Q4_K
+// matvec (q4k_mfma.h): wave w takes K-chunk w (4 super-blocks, 576 bytes per
+// row) of the work-group's 16 gate rows and 16 up rows, two 9 KiB pieces of
+// the 2304-byte rows streamed with non-temporal 1 KiB loads and passed
+// through a 9 KiB wave-private LDS area (gate first, then up); the four
+// waves' partial row sums meet in LDS for the SwiGLU.
 __global__ __launch_bounds__(256, 3) void k_expand_q4t(ExpandArgs a) {
-    constexpr int T = GGML_TYPE_Q4_K, TR = 16, G = 64, U = 1;
-    constexpr int RB = 2304, SPAN = 4 * RB, NP = SPAN / 1024;
+    constexpr int T = GGML_TYPE_Q4_K, TR = 16;
+    constexpr int RB = 2304, SPAN = 16 * 576, NP = SPAN / 1024;
     using F = Fmt<T>;
-    constexpr int RW = ExpandShape<T, TR, U>::RW;       // rows per wave
-    constexpr int NW = TR / RW;                         // waves
+    constexpr int NW = 4;                               // waves: one K-chunk each
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];   // prepared h, then NW row spans
     __shared__ int s_ids[kMaxK];
     __shared__ float s_w[kMaxK], s_val[kMaxK];
     __shared__ float2 s_cand[64];
     __shared__ float s_act[TR];
+    __shared__ double s_part[2][4][TR];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int H = a.H, F_ = a.F;
     const int tpe = F_ / TR;
@@ -330,42 +332,48 @@ __global__ __launch_bounds__(256, 3) void k_expand_q4t(ExpandArgs a) {
     uint64_t uo;
     if (routed) { blob = a.base + (uint64_t)s_ids[e] * a.stride; uo = a.gate_size; }
     else { blob = a.shared; uo = a.sh_gate_size; }
-    const uint8_t *g0 = blob + (uint64_t)(rb * TR + wv * RW) * RB, *u0 = g0 + uo;
+    // piece i of chunk wv, lane l: chunk byte o = 1024 i + 16 l of row o / 576
+    const uint8_t *g0 = blob + (uint64_t)(rb * TR) * RB + wv * 576, *u0 = g0 + uo;
     uint4 vg[NP], vu[NP];
 #pragma unroll
-    for (int i = 0; i < NP; i++) vg[i] = ldw16(g0 + i * 1024 + lane * 16);
-#pragma unroll
-    for (int i = 0; i < NP; i++) vu[i] = ldw16(u0 + i * 1024 + lane * 16);
+    for (int i = 0; i < NP; i++) {
+        const uint32_t o = i * 1024 + lane * 16, go = (o / 576) * RB + o % 576;
+        vg[i] = ldw16(g0 + go);
+        vu[i] = ldw16(u0 + go);
+    }
     // keep the scheduler from sinking the up loads below the gate arithmetic
     __builtin_amdgcn_sched_barrier(0);
-    typename F::X X;
-    {
-        int gi[F::NG];
-        F::groups(lane, gi);
-        load_xslot(X, lds, H, gi);
-    }
-    uint8_t *buf = lds + lds_round(xqb) + wv * SPAN;
-    float g[RW], v[RW];
-    // row by row as the pieces arrive (loads retire in issue order): row r
-    // waits only for the pieces that cover it, so the arithmetic of the early
-    // rows overlaps the arrival of the later ones
-    auto rows = [&](uint4 (&p)[NP], float (&out)[RW]) {
-        int written = 0;
+    uint8_t *zero = lds + lds_round(xqb), *buf = zero + 512 + wv * SPAN;
+    if (wv == 0 && lane < 32) *(uint4 *)(zero + 16 * lane) = make_uint4(0, 0, 0, 0);
+    const Q4kLane q = q4k_lane(lane);
+    const int n = lane & 15, g = lane >> 4;
+    const uint8_t *ssl = lds + 3 * 4096 + q.jg * 8;
+    __syncthreads();                                   // the zero area
+    // the row sums accumulate in fp64 (fp64 fma issues at the fp32 rate here):
+    // the layer's parity margin at near-zero outputs is a few per cent
+    auto chunk = [&](uint4 (&p)[NP]) {
 #pragma unroll
-        for (int r = 0; r < RW; r++) {
-            const int need = ((r + 1) * RB + 1023) / 1024;
+        for (int i = 0; i < NP; i++) *(uint4 *)(buf + i * 1024 + lane * 16) = p[i];
+        double y = 0.0;
 #pragma unroll
-            for (int i = 0; i < NP; i++)
-                if (i >= written && i < need) *(uint4 *)(buf + i * 1024 + lane * 16) = p[i];
-            written = need;
-            out[r] = group_sum<G>(F::dot(F::load(buf + r * RB, lane), lane, X));
+        for (int b = 0; b < 4; b++) {
+            const int sb = 4 * wv + b;                 // super-block of the row: groups 8 sb ..
+            const uint8_t *xa = lds + sb * 768 + q.aoff;
+            y = q4k_sb_dot_mfma(buf + n * 576 + b * 144, q.valid1 ? xa : zero, q.valid2 ? xa : zero,
+                                ssl + sb * 64, q, y);
         }
+        y += __shfl_xor(y, 16);
+        y += __shfl_xor(y, 32);
+        return y;
     };
-    rows(vg, g);
-    rows(vu, v);
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < RW; r++) s_act[wv * RW + r] = (g[r] / (1.0f + expf(-g[r]))) * v[r];
+    const double yg = chunk(vg);
+    const double yu = chunk(vu);
+    if (g == 0) { s_part[0][wv][n] = yg; s_part[1][wv][n] = yu; }
+    __syncthreads();
+    if (wv == 0 && lane < TR) {
+        const float gs = (float)((s_part[0][0][lane] + s_part[0][1][lane]) + (s_part[0][2][lane] + s_part[0][3][lane]));
+        const float us = (float)((s_part[1][0][lane] + s_part[1][1][lane]) + (s_part[1][2][lane] + s_part[1][3][lane]));
+        s_act[lane] = (gs / (1.0f + expf(-gs))) * us;
     }
     __syncthreads();
     if (wv == 0) {
@@ -392,7 +400,7 @@ hipError_t launch_expand(int type, const ExpandArgs &a, hipStream_t s, int n_cu)
     const size_t lds = lds_round(xq_bytes(a.H, type == GGML_TYPE_Q6_K ? 16 : 32));
     const int grid = a.F / TR * n_tot;
     if (type == GGML_TYPE_Q4_K && TR == 16 && G == 64 && U == 1) {   // gate/up at H = 4096: row spans through LDS
-        k_expand_q4t<<<grid, ExpandShape<GGML_TYPE_Q4_K, 16, 1>::THREADS, lds + 4 * 2304 * 4, s>>>(a);
+        k_expand_q4t<<<grid, 256, lds + 512 + 4 * 16 * 576, s>>>(a);
         return hipGetLastError();
     }
 #define FO_K2(TT, RR, GG, UU) \

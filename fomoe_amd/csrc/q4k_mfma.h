@@ -46,9 +46,12 @@ FO_DEV Q4kLane q4k_lane(int lane) {
 // operands of this super-block's first / second MFMAs for pair 0 (pair 1 at
 // +384), or a zero area of at least 400 bytes; ssb: {scale, sum} of the
 // lane's pair-0 group (pair 1 at +32). Adds the lane's share of
-// d * sum_j sc_j (q . x)_j - dmin * sum_j m_j (sum x)_j to y.
-FO_DEV float q4k_sb_dot_mfma(const uint8_t *sb, const uint8_t *a1, const uint8_t *a2, const uint8_t *ssb,
-                             const Q4kLane &q, float y) {
+// d * sum_j sc_j (q . x)_j - dmin * sum_j m_j (sum x)_j to y (in float: the
+// limb combination rounds once, as the slot dots' does; in double: exact up
+// to the accumulation).
+template <typename Acc>   // float, or double where a layer's parity margin needs it
+FO_DEV Acc q4k_sb_dot_mfma(const uint8_t *sb, const uint8_t *a1, const uint8_t *a2, const uint8_t *ssb,
+                           const Q4kLane &q, Acc y) {
     const uint4 hdr = *(const uint4 *)sb;
     const uint4 c0 = *(const uint4 *)(sb + q.boff);
     const uint4 c1 = *(const uint4 *)(sb + q.boff + 64);
@@ -70,10 +73,11 @@ FO_DEV float q4k_sb_dot_mfma(const uint8_t *sb, const uint8_t *a1, const uint8_t
         v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, lo, (v4i){0, 0, 0, 0}, 0, 0, 0);
         D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, hi, D, 0, 0, 0);
         // limb sums of a 32-value sub-block: |D| < 2^16, so D2 * 256 + D1 is exact in fp32
-        const float f = fmaf((float)((D[2] << 8) + D[1]), 256.f, (float)D[0]);
+        // (the whole limb combination is exact in fp64); d * sc and dmin * m are exact
+        const Acc f = (Acc)((D[2] << 8) + D[1]) * (Acc)256 + (Acc)D[0];
         const float2 ss = *(const float2 *)(ssb + 32 * p);
-        y = fmaf(sc[p], f * ss.x, y);
-        y = fmaf(-mn[p], ss.y, y);
+        y = fma((Acc)sc[p], f * (Acc)ss.x, y);
+        y = fma(-(Acc)mn[p], (Acc)ss.y, y);
     }
     return y;
 }
