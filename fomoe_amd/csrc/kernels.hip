@@ -343,6 +343,97 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ============================================================ Q8_0 matvec, tile-staged MFMA (K = 1024)
+// The Q6_K tile kernel's stream (one wave per work-group, tiles of 16 rows =
+// 16 x 1088 contiguous bytes = 17 KiB, 1 KiB non-temporal loads, the next
+// tile in flight) with the codes fed to v_mfma_i32_16x16x64_i8 as they are
+// (int8): per pair of MFMAs, lane (n = row, g) reads the 16 codes of block
+// 4p + (g>>1) (first) and 4p + 2 + (g>>1) (second), half g&1; the A operand
+// routes the 32-value groups' limbs so that D lane group g receives the three
+// limb sums of block 4p + g of row n, scaled by its d. ~70 VALU instructions
+// per tile and lane against ~280 for the slot dots.
+constexpr uint32_t kQ8Row = 1088, kQ8X = 3 * 1024 + (1024 / 32) * 8, kQ8Zero = 416;
+
+template <int TPW>
+__global__ __launch_bounds__(64) void k_matvec_q80_mfma(MatvecArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
+    constexpr uint32_t TB = 16 * kQ8Row;
+    constexpr int NV = TB / 1024;                               // 17 pieces, whole
+    const int lane = threadIdx.x, mat = blockIdx.y;
+    uint8_t *zero = sx + kQ8X, *tb = zero + kQ8Zero;
+    float *ys = (float *)(tb + NV * 1024);                      // [TPW * 16]
+    const uint8_t *Wm = a.W + mat * a.mat_stride;
+    const int tile0 = blockIdx.x * TPW, ntiles = (a.M + 15) / 16;
+    // a partial last tile (M >= 16) is read as rows M-16 .. M-1, its results shifted
+    auto first_row = [&](int tile) { return min(tile * 16, a.M - 16); };
+    auto issue = [&](uint4 (&v)[NV], int tile) {
+        const uint8_t *tp = Wm + (uint64_t)first_row(tile) * kQ8Row;
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = ldw16(tp + i * 1024 + lane * 16);
+    };
+    uint4 v[NV];
+    if (tile0 < ntiles) issue(v, tile0);
+    if (lane < 1024 / 32) {   // the wave's x: one lane per 32-value group
+        int limb[kLimbs][8];
+        float scale, sum;
+        prep_group_regs<32>(a.xf + mat * a.xf_stride + lane * 32, limb, scale, sum);
+#pragma unroll
+        for (int L = 0; L < kLimbs; L++) {
+            *(uint4 *)(sx + lane * 96 + 32 * L) = make_uint4(limb[L][0], limb[L][1], limb[L][2], limb[L][3]);
+            *(uint4 *)(sx + lane * 96 + 32 * L + 16) = make_uint4(limb[L][4], limb[L][5], limb[L][6], limb[L][7]);
+        }
+        *(float2 *)(sx + 3 * 1024 + lane * 8) = make_float2(scale, sum);
+    } else if (lane < 32 + kQ8Zero / 16) {
+        *(uint4 *)(zero + 16 * (lane - 32)) = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    const int n = lane & 15, g = lane >> 4, mb = n >> 2, L = n & 3;
+    const bool valid1 = mb == (g >> 1) && L < 3, valid2 = mb == 2 + (g >> 1) && L < 3;
+    const uint8_t *xa = sx + mb * 96 + 32 * L + 16 * (g & 1);   // + 384 p: group 4p + mb
+    const uint8_t *a1 = valid1 ? xa : zero, *a2 = valid2 ? xa : zero;
+    const int s1 = valid1 ? 384 : 0, s2 = valid2 ? 384 : 0;   // zero lanes stay on the zero area
+    const float2 *ssl = (const float2 *)(sx + 3 * 1024) + g;  // group 4p + g
+#pragma unroll
+    for (int tt = 0; tt < TPW; tt++) {
+        const int tile = tile0 + tt;
+        if (tile >= ntiles) break;
+#pragma unroll
+        for (int i = 0; i < NV; i++) *(uint4 *)(tb + i * 1024 + lane * 16) = v[i];
+        if (tt + 1 < TPW && tile + 1 < ntiles) issue(v, tile + 1);
+        const uint8_t *rp = tb + n * kQ8Row;
+        float y = 0.f;
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            v4i B1, B2;
+            __builtin_memcpy(&B1, rp + 34 * (4 * p + (g >> 1)) + 2 + 16 * (g & 1), 16);
+            __builtin_memcpy(&B2, rp + 34 * (4 * p + 2 + (g >> 1)) + 2 + 16 * (g & 1), 16);
+            uint16_t d16;
+            __builtin_memcpy(&d16, rp + 34 * (4 * p + g), 2);
+            const v4i A1 = *(const v4i *)(a1 + s1 * p), A2 = *(const v4i *)(a2 + s2 * p);
+            v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, D, 0, 0, 0);
+            const float f = fmaf((float)((D[2] << 8) + D[1]), 256.f, (float)D[0]);
+            y = fmaf(h2f(d16), f * ssl[4 * p].x, y);
+        }
+        y += __shfl_xor(y, 16);
+        y += __shfl_xor(y, 32);
+        const int shift = tile * 16 - first_row(tile);
+        if (g == 0 && n >= shift) ys[tt * 16 + n - shift] = y;
+    }
+    for (int q = lane; q < TPW * 16; q += 64) {
+        const int row = tile0 * 16 + q;
+        if (row < a.M) a.y[mat * a.y_stride + row] = ys[q];
+    }
+}
+
+static hipError_t matvec_q80_mfma(const MatvecArgs &a, hipStream_t s) {
+    constexpr int TPW = 8;
+    const int ntiles = (a.M + 15) / 16;
+    const uint32_t lds = kQ8X + kQ8Zero + 16 * kQ8Row + TPW * 16 * 4;
+    k_matvec_q80_mfma<TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
+    return hipGetLastError();
+}
+
 // ============================================================ Q4_K matvec, tile-staged MFMA
 // For Q4_K rows of K = 4096 (the expert gate/up shape). Four-wave work-groups
 // share one prepared x (13 KiB of LDS); each wave streams its own blocks of
@@ -627,6 +718,7 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
             return matvec_t<GGML_TYPE_Q6_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q8_0:
             if (a.xf && tile_shape(type, a.row_bytes, a.K)) {   // tile-staged path
+                if (a.K == 1024 && a.M >= 16) return matvec_q80_mfma(a, s);
                 if (a.K == 1024) return matvec_tile<GGML_TYPE_Q8_0, 1024, 16>(a, s);
                 return matvec_tile<GGML_TYPE_Q8_0, 4096, 4>(a, s);
             }
