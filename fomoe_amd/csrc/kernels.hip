@@ -434,6 +434,80 @@ static hipError_t matvec_q80_mfma(const MatvecArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ============================================================ Q5_K matvec, tile-staged MFMA (K = 1024)
+// The Q8_0 MFMA kernel's stream (one wave per work-group, 16-row tiles =
+// 16 x 704 contiguous bytes = 11 KiB, the next tile in flight) with the Q5_K
+// super-block dot of q4k_mfma.h (Q4_K's code routing plus the fifth bit).
+constexpr uint32_t kQ5Row = 704, kQ5X = 3 * 1024 + (1024 / 32) * 8, kQ5Zero = 416;
+
+template <int TPW>
+__global__ __launch_bounds__(64) void k_matvec_q5k_mfma(MatvecArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
+    constexpr uint32_t TB = 16 * kQ5Row;
+    constexpr int NV = TB / 1024;                               // 11 pieces, whole
+    const int lane = threadIdx.x, mat = blockIdx.y;
+    uint8_t *zero = sx + kQ5X, *tb = zero + kQ5Zero;
+    float *ys = (float *)(tb + NV * 1024);                      // [TPW * 16]
+    const uint8_t *Wm = a.W + mat * a.mat_stride;
+    const int tile0 = blockIdx.x * TPW, ntiles = (a.M + 15) / 16;
+    auto first_row = [&](int tile) { return min(tile * 16, a.M - 16); };
+    auto issue = [&](uint4 (&v)[NV], int tile) {
+        const uint8_t *tp = Wm + (uint64_t)first_row(tile) * kQ5Row;
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = ldw16(tp + i * 1024 + lane * 16);
+    };
+    uint4 v[NV];
+    if (tile0 < ntiles) issue(v, tile0);
+    if (lane < 1024 / 32) {   // the wave's x: one lane per 32-value group
+        int limb[kLimbs][8];
+        float scale, sum;
+        prep_group_regs<32>(a.xf + mat * a.xf_stride + lane * 32, limb, scale, sum);
+#pragma unroll
+        for (int L = 0; L < kLimbs; L++) {
+            *(uint4 *)(sx + lane * 96 + 32 * L) = make_uint4(limb[L][0], limb[L][1], limb[L][2], limb[L][3]);
+            *(uint4 *)(sx + lane * 96 + 32 * L + 16) = make_uint4(limb[L][4], limb[L][5], limb[L][6], limb[L][7]);
+        }
+        *(float2 *)(sx + 3 * 1024 + lane * 8) = make_float2(scale, sum);
+    } else if (lane < 32 + kQ5Zero / 16) {
+        *(uint4 *)(zero + 16 * (lane - 32)) = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    const Q4kLane q = q4k_lane(lane);
+    const int n = lane & 15, g = lane >> 4;
+    const uint8_t *ssl = sx + 3 * 1024 + q.jg * 8;
+#pragma unroll
+    for (int tt = 0; tt < TPW; tt++) {
+        const int tile = tile0 + tt;
+        if (tile >= ntiles) break;
+#pragma unroll
+        for (int i = 0; i < NV; i++) *(uint4 *)(tb + i * 1024 + lane * 16) = v[i];
+        if (tt + 1 < TPW && tile + 1 < ntiles) issue(v, tile + 1);
+        const uint8_t *rp = tb + n * kQ5Row;
+        float y = 0.f;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint8_t *xa = sx + b * 768 + q.aoff;
+            y = q5k_sb_dot_mfma(rp + b * 176, q.valid1 ? xa : zero, q.valid2 ? xa : zero, ssl + b * 64, q, g, y);
+        }
+        y += __shfl_xor(y, 16);
+        y += __shfl_xor(y, 32);
+        const int shift = tile * 16 - first_row(tile);
+        if (g == 0 && n >= shift) ys[tt * 16 + n - shift] = y;
+    }
+    for (int r = lane; r < TPW * 16; r += 64) {
+        const int row = tile0 * 16 + r;
+        if (row < a.M) a.y[mat * a.y_stride + row] = ys[r];
+    }
+}
+
+static hipError_t matvec_q5k_mfma(const MatvecArgs &a, hipStream_t s) {
+    constexpr int TPW = 8;
+    const int ntiles = (a.M + 15) / 16;
+    const uint32_t lds = kQ5X + kQ5Zero + 16 * kQ5Row + TPW * 16 * 4;
+    k_matvec_q5k_mfma<TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
+    return hipGetLastError();
+}
+
 // ============================================================ Q4_K matvec, tile-staged MFMA
 // For Q4_K rows of K = 4096 (the expert gate/up shape). Four-wave work-groups
 // share one prepared x (13 KiB of LDS); each wave streams its own blocks of
@@ -704,6 +778,7 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
             return matvec_t<GGML_TYPE_Q4_K, 2>(a, s, n_cu);
         case GGML_TYPE_Q5_K:
             if (a.xf && tile_shape(type, a.row_bytes, a.K)) {   // tile-staged path
+                if (a.K == 1024 && a.M >= 16) return matvec_q5k_mfma(a, s);
                 if (a.K == 1024) return matvec_tile<GGML_TYPE_Q5_K, 1024, 16>(a, s);
                 return matvec_tile<GGML_TYPE_Q5_K, 4096, 4>(a, s);
             }

@@ -82,4 +82,45 @@ FO_DEV Acc q4k_sb_dot_mfma(const uint8_t *sb, const uint8_t *a1, const uint8_t *
     return y;
 }
 
+// Q5_K super-block (176 bytes: header, qh[32], qs[128]; reference
+// src/quant.c:216-262): as Q4_K with a fifth bit per value, bit 2c of qh[l]
+// for value 64c + l and bit 2c+1 for value 64c + 32 + l (c = 0..3). The lane
+// reads the qh bytes of its 16 code positions (qh[16(g&1) ..]) next to the
+// code bytes; the code routing and the per-sub-block scaling are Q4_K's.
+FO_DEV float q5k_sb_dot_mfma(const uint8_t *sb, const uint8_t *a1, const uint8_t *a2, const uint8_t *ssb,
+                             const Q4kLane &q, int g, float y) {
+    const uint4 hdr = *(const uint4 *)sb;
+    const uint4 hb = *(const uint4 *)(sb + 16 + 16 * (g & 1));
+    const uint4 c0 = *(const uint4 *)(sb + 32 + q.boff);
+    const uint4 c1 = *(const uint4 *)(sb + 32 + q.boff + 64);
+    const uint32_t sh = 8 * q.jg;
+    const uint32_t b0 = (hdr.y >> sh) & 0xFFu, b4 = (hdr.z >> sh) & 0xFFu, b8 = (hdr.w >> sh) & 0xFFu;
+    const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
+    const float sc[2] = {d * (float)(b0 & 63), d * (float)((b8 & 0xF) | ((b0 >> 6) << 4))};
+    const float mn[2] = {dmin * (float)(b4 & 63), dmin * (float)((b8 >> 4) | ((b4 >> 6) << 4))};
+    const uint32_t H[4] = {hb.x, hb.y, hb.z, hb.w};
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const uint4 w = p ? c1 : c0;
+        const uint32_t W[4] = {w.x, w.y, w.z, w.w};
+        const int c = 2 * p + (g >> 1);               // the 64-value chunk of these code bytes
+        v4i lo, hi;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t hl = (H[k] >> (2 * c)) & 0x01010101u, hh = (H[k] >> (2 * c + 1)) & 0x01010101u;
+            lo[k] = (int)((W[k] & 0x0F0F0F0Fu) | (hl << 4));
+            hi[k] = (int)(((W[k] >> 4) & 0x0F0F0F0Fu) | (hh << 4));
+        }
+        const v4i A1 = *(const v4i *)(a1 + 384 * p);
+        const v4i A2 = *(const v4i *)(a2 + 384 * p);
+        v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, lo, (v4i){0, 0, 0, 0}, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, hi, D, 0, 0, 0);
+        const float f = fmaf((float)((D[2] << 8) + D[1]), 256.f, (float)D[0]);
+        const float2 ss = *(const float2 *)(ssb + 32 * p);
+        y = fmaf(sc[p], f * ss.x, y);
+        y = fmaf(-mn[p], ss.y, y);
+    }
+    return y;
+}
+
 }  // namespace fo
