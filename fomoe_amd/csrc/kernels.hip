@@ -637,11 +637,12 @@ static hipError_t matvec_q4k_mfma(const MatvecArgs &a, hipStream_t s) {
 // slots back from there; lane l owns slots l%G + G*u of P = 64/G rows per pass
 // (Fmt<T> slot dots on the exact int8 limbs) and prepares its own activation
 // groups from fp32 x (prep_group_regs, bit-identical to k_xprep). Used for
-// Q4_K at K = 4096 / 8192 (the expert gate/up shape; RT * row_bytes = 18 KiB):
-// 5.5 -> 5.8-6.0 TB/s over the per-lane-load k_matvec, for Q8_0 at K = 1024
-// / 4096 (17 KiB tiles), Q5_K at K = 1024 / 4096 (11 KiB) and MXFP4 at K = 4096
-// (17 KiB). For Q6_K at K = 1024 the
-// same scheme measured 5.0 TB/s against 5.6 for the MFMA tile kernel above.
+// Q4_K at K = 8192 (and K = 4096 with fewer than 16 rows; RT * row_bytes =
+// 18 KiB), Q8_0 at K = 4096 (17 KiB tiles), Q5_K at K = 4096 (11 KiB), MXFP4
+// at K = 4096 (17 KiB), and the K = 1024 Q8_0 / Q5_K shapes with fewer than 16
+// rows; the MFMA kernels above serve the rest. Over the per-lane-load
+// k_matvec this scheme took Q4_K at K = 4096 from 5.5 to 5.8-6.0 TB/s; for
+// Q6_K at K = 1024 it measured 5.0 TB/s against 5.6 for the MFMA tile kernel.
 // With G = 64 the RT row partials of a lane are reduced across the wave
 // together, halving the live values at each xor step.
 template <int N>
