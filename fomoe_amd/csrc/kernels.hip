@@ -240,13 +240,14 @@ template <int NSB, int TPW>
 __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
     constexpr int NV = (kT6Rows * NSB * 210 + 1023) / 1024;
+    constexpr uint32_t TBYTES = (kT6Rows * NSB * 210 + 15) & ~15u;   // the tile's LDS area
     constexpr int K = NSB * 256;
     const int lane = threadIdx.x;
     const int mat = blockIdx.y;
     constexpr uint32_t limb_bytes = 3u * K, xbytes = limb_bytes + (K / 16) * 8;
     constexpr uint32_t zoff = (xbytes + 15) & ~15u;    // zero A operands for the rows of other groups
     uint8_t *tb = sx + zoff + kT6Zero;
-    float *ys = (float *)(tb + NV * 1024);             // [TPW * 16] results
+    float *ys = (float *)(tb + TBYTES);                // [TPW * 16] results
     const uint8_t *Wm = a.W + mat * a.mat_stride;
     constexpr uint32_t rb = NSB * 210;                 // launched only for contiguous rows
     constexpr uint32_t full_bytes = kT6Rows * rb;
@@ -255,9 +256,9 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
     // A piece that straddles the end of a partial tile (16*rows*rb need not be a
     // multiple of 16) is read from the last 16 valid bytes and written to that
     // same LDS position (overlapping its neighbour with identical bytes). A
-    // whole tile is a multiple of 16 bytes: only its last piece is clamped on
-    // the read, and every piece lands at its own offset (the staging area has
-    // NV KiB, so lanes past the end write unused bytes).
+    // whole tile is a multiple of 16 bytes: only its last piece is clamped,
+    // on the read and on the write (lanes past the end of the tile write the
+    // tile's last 16 bytes again, so the LDS area is just the tile's size).
     auto tile_bytes = [&](int tile) { return (uint32_t)min(kT6Rows, a.M - tile * kT6Rows) * rb; };
     auto pos = [&](uint32_t o, uint32_t nb) { return o + 16 <= nb ? o : nb - 16; };
     auto issue = [&](uint4 (&v)[NV], int tile) {
@@ -301,13 +302,10 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
             const uint32_t nb = tile_bytes(tile);
             if (nb == full_bytes) {
 #pragma unroll
-                for (int i = 0; i < NV; i++) *(uint4 *)(tb + i * 1024 + lane * 16) = v[i];
+                for (int i = 0; i < NV; i++) *(uint4 *)(tb + min(i * 1024u + lane * 16u, full_bytes - 16)) = v[i];
             } else {
 #pragma unroll
-                for (int i = 0; i < NV; i++) {
-                    const uint32_t o = i * 1024 + lane * 16;
-                    *(uint4 *)(tb + (o < nb ? pos(o, nb) : o)) = v[i];
-                }
+                for (int i = 0; i < NV; i++) *(uint4 *)(tb + pos(i * 1024 + lane * 16, nb)) = v[i];
             }
         }
         if (tt + 1 < TPW && tile + 1 < ntiles) issue(v, tile + 1);
@@ -338,7 +336,7 @@ static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
     constexpr int TPW = 8, K = NSB * 256;
     const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
     const uint32_t lds = ((xq_bytes(K, 16) + 15) & ~15u) + kT6Zero +
-                         (uint32_t)((kT6Rows * NSB * 210 + 1023) / 1024) * 1024 + TPW * kT6Rows * 4;
+                         ((kT6Rows * NSB * 210 + 15) & ~15u) + TPW * kT6Rows * 4;
     k_matvec_q6k_tile<NSB, TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
     return hipGetLastError();
 }
