@@ -117,10 +117,13 @@ def test_matvec_shapes(gpu, t, M, K):
     assert parity_err(got, want) <= TOL
 
 
-def test_matvec_activation_extremes(gpu):
+@pytest.mark.parametrize("t,K", [(O.Q4_K, 4096), (O.Q6_K, 1024), (O.Q8_0, 1024), (O.Q5_K, 1024)])
+def test_matvec_activation_extremes(gpu, t, K):
     """Activations spanning many binades, exact zeros and a zero group: the
-    block-fixed-point path keeps fp32-level accuracy."""
-    t, M, K = O.Q4_K, 64, 4096
+    block-fixed-point path keeps fp32-level accuracy (each shape is one that
+    runs on the integer MFMA kernels)."""
+    M = 64
+    say("matvec extremes", t, M, K)
     W = O.synth_quant(t, 31, 0, 0.02, M, K)
     rng = np.random.default_rng(0)
     x = (rng.standard_normal(K) * np.exp2(rng.integers(-20, 20, K))).astype(np.float32)
