@@ -76,46 +76,114 @@ def rotation(gpu, t, M, K, wseed, xseed, n_mats, steps, warmup):
     return res, keep
 
 
-def cpu_baseline(gpu, dW, stride, M, K, t, seconds):
-    """Reference CPU matvec (quant.c mat_vec_mul_fast: Q8_K activations, AVX2
-    integer dots, OpenMP over rows — the cpu_expert.c engine's kernel) timed on
-    a bounded sample of the same matrices."""
-    import ctypes as C
-    import oracle as O
-    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
-    os.environ.setdefault("OMP_PROC_BIND", "close")
-    R = O.load_ref()
-    kind = "reference"
-    n_s = 8
-    rb = FA.row_bytes(t, K) * M
-    mats = [gpu.download(dW.offset(m * stride), np.uint8, rb) for m in range(n_s)]
-    x = O.synth_f32(3, 0, 1.0, K)
-    y = np.empty(M, np.float32)
-    if R is None:   # the oracle's restatement of the same path
-        kind = "port"
-        q8 = O.quantize_q8_K(x)
-        fn = lambda W: O.lib.fo_matvec_q8(y.ctypes.data, W.ctypes.data, t, q8.ctypes.data, M, K)  # noqa: E731
-    else:
-        fn = lambda W: R.mat_vec_mul_fast(y.ctypes.data, W.ctypes.data, t, x.ctypes.data, M, K)  # noqa: E731
-    fn(mats[0])
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        fn(mats[n % n_s])
-        n += 1
-    dt = time.perf_counter() - t0
-    gbs = n * (rb + 4 * K + 4 * M) / dt / 1e9
-    cpu = "unknown"
+def cpu_env():
+    """Pin the CPU legs before any OpenMP runtime starts: OMP_NUM_THREADS =
+    the physical cores this process may run on (capped at 16, the host share
+    of one GPU on the box, unless the caller set it), OMP_PROC_BIND=close.
+    Returns what is reported with every CPU figure."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        try:
+            base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            cores.add((open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    if "OMP_NUM_THREADS" not in os.environ:
+        os.environ["OMP_NUM_THREADS"] = str(max(1, min(16, len(cores))))
+    os.environ["OMP_PROC_BIND"] = "close"
+    model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
+                model = line.split(":", 1)[1].strip()
                 break
     except OSError:
         pass
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{n} Q6_K 4096x1024 matvecs (mat_vec_mul_fast, Q8_K activations) over "
-                      f"{n_s} of the rotation's matrices, {dt:.1f} s; CPU {cpu}"}
+    return {"cpu_model": model, "logical_cpus_allowed": len(cpus), "physical_cores_allowed": len(cores)}
+
+
+def omp_threads():
+    """Threads the OpenMP runtime of the CPU libraries actually uses."""
+    import ctypes as C
+    try:
+        return int(C.CDLL("libgomp.so.1").omp_get_max_threads())
+    except OSError:
+        return None
+
+
+def _time_loop(fn, n_items, seconds):
+    fn(0)
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        fn(n % n_items)
+        n += 1
+    return n, time.perf_counter() - t0
+
+
+def cpu_matvec_baselines(gpu, keeps, seconds, env):
+    """CPU matvec legs on this host, each over a rotation of the same device
+    matrices large enough (>= 200 MB) not to stay in the CPU's caches:
+    - the cpu_expert.c engine (reference quant.c mat_vec_mul_fast: Q8_K
+      activations, AVX2 integer dots, OpenMP over rows; quant.c:343-607,
+      cpu_expert.c:52-72) for Q6_K (config 2, the headline's cpu_baseline)
+      and Q4_K (config 1);
+    - the reference fp32 path (tensor.c mat_vec_mul: quant.c vec_dot_*_f32,
+      tensor.c:102-173): Q8_0 (config 2', cpu_expert has no Q8_0) and Q6_K
+      (the parity path);
+    - this build's C restatement of the same engines (oracle/, kind "port"),
+      beside them.
+    The reference library is oracle/_ref, compiled from the reference's
+    sources in the build container; without it only the port legs run."""
+    import oracle as O
+    R = O.load_ref()
+    threads = omp_threads()
+    out = {}
+    for name, t, M, K, xseed in (("q6k", FA.Q6_K, 4096, 1024, 3), ("q4k", FA.Q4_K, 1024, 4096, 1),
+                                 ("q8_0", FA.Q8_0, 4096, 1024, 3)):
+        if name not in keeps:
+            continue
+        dW, stride = keeps[name]
+        rb = FA.row_bytes(t, K) * M
+        n_s = max(8, (200 << 20) // rb + 1)
+        mats = [gpu.download(dW.offset(m * stride), np.uint8, rb) for m in range(n_s)]
+        x = O.synth_f32(xseed, 0, 1.0, K)
+        y = np.empty(M, np.float32)
+        unit = rb + 4 * K + 4 * M
+        legs = {}
+        if R is not None and t != FA.Q8_0:
+            legs["reference_q8k"] = lambda i: R.mat_vec_mul_fast(y.ctypes.data, mats[i].ctypes.data, t,  # noqa: E731
+                                                                 x.ctypes.data, M, K)
+        if R is not None:
+            legs["reference_fp32"] = lambda i: R.mat_vec_mul(y.ctypes.data, mats[i].ctypes.data, t,  # noqa: E731
+                                                             x.ctypes.data, M, K)
+        if t != FA.Q8_0:
+            q8 = O.quantize_q8_K(x)
+            legs["port_q8k"] = lambda i: O.lib.fo_matvec_q8(y.ctypes.data, mats[i].ctypes.data, t,  # noqa: E731
+                                                            q8.ctypes.data, M, K)
+        legs["port_fp32"] = lambda i: O.lib.fo_mat_vec_mul(y.ctypes.data, mats[i].ctypes.data, t,  # noqa: E731
+                                                           x.ctypes.data, M, K)
+        res = {"matrices": n_s, "working_set_MB": round(n_s * rb / 1e6, 1)}
+        for leg, fn in legs.items():
+            sec = seconds if (name == "q6k" and leg == "reference_q8k") else max(2.0, seconds / 4)
+            n, dt = _time_loop(fn, n_s, sec)
+            res[leg + "_GB/s"] = round(n * unit / dt / 1e9, 3)
+            res[leg + "_us"] = round(dt / n * 1e6, 1)
+        out[name] = res
+        del mats
+    cpu = None
+    q6 = out.get("q6k", {})
+    kind, key = ("reference", "reference_q8k_GB/s") if "reference_q8k_GB/s" in q6 else ("port", "port_q8k_GB/s")
+    if key in q6:
+        cpu = {"value": q6[key], "unit": "GB/s", "cores": threads, "kind": kind,
+               "sample": (f"Q6_K 4096x1024 matvecs with Q8_K activations (the cpu_expert.c engine, "
+                          f"{'reference mat_vec_mul_fast from oracle/_ref' if kind == 'reference' else 'oracle/ restatement'}) "
+                          f"rotating over {q6['matrices']} of the GPU rotation's matrices "
+                          f"({q6['working_set_MB']} MB), about {seconds:.0f} s; OpenMP threads {threads} "
+                          f"(OMP_PROC_BIND=close) on {env['physical_cores_allowed']} physical cores "
+                          f"allowed; CPU {env['cpu_model']}")}
+    return cpu, {"cpu_threads": threads, **env, "cpu_matvec": out}
 
 
 def cpu_layer_baseline(gpu, layers, shape, seconds, n_sample=4):
@@ -171,8 +239,14 @@ def cpu_layer_baseline(gpu, layers, shape, seconds, n_sample=4):
         n += 1
     dt = time.perf_counter() - t0
     R.cpu_expert_free(ctx)
-    return {"cpu_layer_us": round(dt / n * 1e6, 1), "cpu_layer_calls": n, "cpu_layer_sample_layers": len(sample),
-            "cpu_layer_threads": int(os.environ.get("OMP_NUM_THREADS", "16"))}
+    us = dt / n * 1e6
+    # the decode stack on the CPU, from the sampled layers: each of the 60
+    # layers does the same work (router + 10 routed + 1 shared expert)
+    return {"cpu_layer_us": round(us, 1), "cpu_layer_calls": n, "cpu_layer_sample_layers": len(sample),
+            "cpu_layer_threads": omp_threads(),
+            "cpu_stack_tok_per_s_sampled": round(1e6 / (us * len(layers)), 3),
+            "cpu_stack_note": f"60-layer stack estimated as {len(layers)} x the mean time of "
+                              f"{len(sample)} sampled layers (reference cpu_expert engine)"}
 
 
 def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0, cpu_seconds=0.0):
@@ -273,24 +347,27 @@ def main():
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         sys.exit(2)
     skip = set(filter(None, args.skip.split(",")))
+    env = cpu_env()   # before any OpenMP runtime is loaded
     gpu = FA.Gpu()
     log(f"device {gpu.arch}: {gpu.n_cu} CUs, {gpu.hbm / 1e9:.1f} GB")
     extra = {}
+    keeps = {}
     t_wall = time.perf_counter()
     q6, keep6 = rotation(gpu, FA.Q6_K, 4096, 1024, 2, 3, 512, args.steps, args.warmup)
     log(f"Q6_K rotation: {q6['GB/s']:.0f} GB/s ({q6['frac_hbm'] * 100:.1f}% of HBM)")
     wall_steps = time.perf_counter() - t_wall
+    keeps["q6k"] = (keep6[0], keep6[3])
     extra["config2_q6k"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q6.items()}
     if "q4k" not in skip:
         q4, keep = rotation(gpu, FA.Q4_K, 1024, 4096, 0, 1, 512, args.steps, args.warmup)
         extra["config1_q4k"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q4.items()}
         log(f"Q4_K rotation: {q4['GB/s']:.0f} GB/s")
-        del keep
+        keeps["q4k"] = (keep[0], keep[3])
     if "q8_0" not in skip:
         q8, keep = rotation(gpu, FA.Q8_0, 4096, 1024, 2, 3, 512, args.steps, args.warmup)
         extra["config2_q8_0"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q8.items()}
         log(f"Q8_0 rotation: {q8['GB/s']:.0f} GB/s")
-        del keep
+        keeps["q8_0"] = (keep[0], keep[3])
     if "q5k" not in skip:   # the real model's down projections are partly Q5_K (same shape as config 2)
         q5, keep = rotation(gpu, FA.Q5_K, 4096, 1024, 2, 3, 512, args.steps, args.warmup)
         extra["config2_q5k"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q5.items()}
@@ -298,11 +375,12 @@ def main():
         del keep
     cpu = None
     if "cpu" not in skip:
-        dW, dx, dy, stride = keep6
-        cpu = cpu_baseline(gpu, dW, stride, 4096, 1024, FA.Q6_K, args.cpu_seconds)
-        log(f"CPU baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['kind']})")
+        cpu, cinfo = cpu_matvec_baselines(gpu, keeps, args.cpu_seconds, env)
+        extra.update(cinfo)
+        if cpu:
+            log(f"CPU baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['kind']})")
+    del keeps, keep6
     if "stack" not in skip and args.stack_layers > 0:
-        del keep6
         extra.update(moe_layer_and_stack(gpu, args.stack_layers, args.stack_steps, args.layer_calls,
                                          0 if "prefill" in skip else args.prefill_reps,
                                          0.0 if "cpu" in skip else args.cpu_seconds / 2))

@@ -29,6 +29,18 @@ SIGNATURES = {
     "gpu_free": (None, [_vp]),
     "gpu_expert_ffn": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_uint64,
                                  C.c_uint64, C.c_uint64, C.c_int, C.c_int, C.c_int, _vp]),
+    "gpu_register_buffers": (None, [_vp, _vp, C.c_int, C.c_uint64]),
+    "gpu_unregister_buffers": (None, [_vp, _vp, C.c_int]),
+    "gpu_upload_model": (C.c_int, [_vp, _vp]),
+    "gpu_set_ram_cache_mb": (None, [_vp, C.c_int]),
+    "gpu_set_vram_cache_mb": (None, [_vp, C.c_int]),
+    "gpu_forward": (_vp, [_vp, _vp, C.c_int, C.c_int]),
+    "gpu_reset_state": (None, [_vp]),
+    "gpu_seed_vram_cache": (C.c_int, [_vp, _vp, C.c_char_p]),
+    "gpu_enable_expert_freq": (None, [_vp]),
+    "gpu_get_expert_freq": (_vp, [_vp]),
+    "gpu_get_expert_dims": (None, [_vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "gpu_get_pingpong_relay_stats": (None, [_vp] + [C.POINTER(C.c_uint64)] * 5),
     "gpu_alloc": (_vp, [_vp, C.c_uint64]),
     "gpu_dealloc": (None, [_vp, _vp]),
     "gpu_upload": (C.c_int, [_vp, _vp, _vp, C.c_uint64]),

@@ -339,6 +339,39 @@ int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_la
     return 0;
 }
 
+// ------------------------------------------------------------------ reference lifecycle
+// The reference's whole-model entry points (include/gpu.h:19-66). This library
+// has no whole-model forward, so each returns the reference's "not available"
+// result and the reference's caller falls back to its CPU path
+// (model.c:411-431, inference.c:425-431, main.c:569-580, 951-956).
+void gpu_register_buffers(gpu_ctx_t *, void **, int, uint64_t) {}
+void gpu_unregister_buffers(gpu_ctx_t *, void **, int) {}
+int gpu_upload_model(gpu_ctx_t *ctx, const void *) {
+    return fail(ctx, -1, "gpu_upload_model: no whole-model forward in this library");
+}
+void gpu_set_ram_cache_mb(gpu_ctx_t *ctx, int mb) { if (ctx) ctx->ram_cache_mb = mb; }
+void gpu_set_vram_cache_mb(gpu_ctx_t *ctx, int mb) { if (ctx) ctx->vram_cache_mb = mb; }
+float *gpu_forward(gpu_ctx_t *ctx, void *, int, int) {
+    fail(ctx, -1, "gpu_forward: no whole-model forward in this library");
+    return nullptr;
+}
+void gpu_reset_state(gpu_ctx_t *) {}
+int gpu_seed_vram_cache(gpu_ctx_t *ctx, void *, const char *) {
+    return fail(ctx, -1, "gpu_seed_vram_cache: no expert cache tiers in this library");
+}
+void gpu_enable_expert_freq(gpu_ctx_t *) {}
+const uint32_t *gpu_get_expert_freq(gpu_ctx_t *) { return nullptr; }
+void gpu_get_expert_dims(gpu_ctx_t *, int *n_layers, int *n_experts) {
+    if (n_layers) *n_layers = 0;
+    if (n_experts) *n_experts = 0;
+}
+void gpu_get_pingpong_relay_stats(gpu_ctx_t *, uint64_t *handoffs, uint64_t *payload, uint64_t *d2h,
+                                  uint64_t *h2d, uint64_t *dma) {
+    uint64_t *outs[] = {handoffs, payload, d2h, h2d, dma};
+    for (uint64_t *p : outs)
+        if (p) *p = 0;
+}
+
 // ------------------------------------------------------------------ legacy FFN
 // Reference gpu_kernels.hip:8385-8488: same argument checks and -1 fallbacks
 // (limits MAX_EXPERTS 10, MAX_N_EMBD 4096, MAX_INTERMEDIATE 2048,
@@ -362,7 +395,9 @@ int gpu_expert_ffn(gpu_ctx_t *ctx, const float *h, void **expert_buffers, const 
         ensure(ctx->vec_out, ctx->vec_out_cap, sizeof(float) * (size_t)H) != hipSuccess ||
         ensure(ctx->act, ctx->act_cap, sizeof(float) * (size_t)n * F) != hipSuccess ||
         ensure(ctx->act2, ctx->act2_cap, sizeof(float) * (size_t)n * F) != hipSuccess ||
-        ensure(ctx->xq_h, ctx->xq_h_cap, xq_stride(H, 16) + xq_stride(H, 32)) != hipSuccess ||
+        // room for two prepared copies of h at the widest layout (gsz 16):
+        // gate and up may be prepared in different group sizes below
+        ensure(ctx->xq_h, ctx->xq_h_cap, 2 * xq_stride(H, 16)) != hipSuccess ||
         ensure(ctx->xq_act, ctx->xq_act_cap, xq_stride(F, 16) * (size_t)n) != hipSuccess)
         return fail(ctx, -1, "gpu_expert_ffn: scratch allocation failed");
     if (hipMemcpyAsync(ctx->vec_in, h, sizeof(float) * H, hipMemcpyHostToDevice, s) != hipSuccess)

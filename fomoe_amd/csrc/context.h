@@ -52,6 +52,9 @@ struct gpu_ctx {
     uint8_t *pin[2] = {nullptr, nullptr};
     hipEvent_t pin_ev[2] = {nullptr, nullptr};
 
+    // values given to gpu_set_{ram,vram}_cache_mb (recorded; no cache tiers here)
+    int ram_cache_mb = -1, vram_cache_mb = -1;
+
     // captured stack-decode graph
     hipGraphExec_t graph_exec = nullptr;
 };

@@ -5,7 +5,9 @@
  * Drop-in part: gpu_ctx_t, gpu_init, gpu_free and gpu_expert_ffn keep the
  * reference's signatures, ownership and -1 "fall back to CPU" semantics
  * (reference include/gpu.h:10-16, 68-83; implementation
- * src/gpu_kernels.hip:8385-8488), so src/inference.c:544 links unchanged.
+ * src/gpu_kernels.hip:8385-8488). Every other function of the reference's
+ * gpu.h is exported too (section "reference lifecycle"), so a -DQMOE_GPU build
+ * of the reference links against this library.
  *
  * HBM-resident extensions (no reference counterpart; the reference copies
  * every expert host-to-device per call, which defeats residency): explicit
@@ -57,6 +59,41 @@ int gpu_expert_ffn(gpu_ctx_t *ctx,
                    int up_type,
                    int down_type,
                    float *ffn_out);
+
+/* ---------------------------------------------------------------- reference lifecycle
+ * The rest of the reference's gpu.h, with the same signatures, so that a
+ * reference build with -DQMOE_GPU links against this library. This build has
+ * no whole-model forward (attention, embeddings, KV cache and the expert cache
+ * tiers are outside its scope), so each entry point returns the reference's
+ * own "not available" result and the reference's caller takes its CPU path:
+ *   gpu_register_buffers / gpu_unregister_buffers (reference gpu.h:19-22):
+ *     no-ops; gpu_expert_ffn copies from pageable host memory.
+ *   gpu_upload_model (gpu.h:26): -1 (model.c:423 prints "GPU upload failed,
+ *     CPU fallback").
+ *   gpu_set_ram_cache_mb / gpu_set_vram_cache_mb (gpu.h:30, 34): recorded,
+ *     no effect (all experts are HBM-resident through gpu_moe_layer).
+ *   gpu_forward (gpu.h:38): NULL (inference.c:427-431 frees the context and
+ *     runs the CPU forward).
+ *   gpu_reset_state (gpu.h:41): no-op (this build keeps no KV / SSM state).
+ *   gpu_seed_vram_cache (gpu.h:46): -1 (model.c:429-431 warns and goes on).
+ *   gpu_enable_expert_freq / gpu_get_expert_freq / gpu_get_expert_dims
+ *     (gpu.h:50-57): counting is never active; the getter returns NULL and the
+ *     dims are 0, which main.c:956 treats as "no profile".
+ *   gpu_get_pingpong_relay_stats (gpu.h:61-66): all zero, the reference's
+ *     single-GPU answer. */
+void gpu_register_buffers(gpu_ctx_t *ctx, void **buffers, int n, uint64_t size);
+void gpu_unregister_buffers(gpu_ctx_t *ctx, void **buffers, int n);
+int gpu_upload_model(gpu_ctx_t *ctx, const void *model);
+void gpu_set_ram_cache_mb(gpu_ctx_t *ctx, int mb);
+void gpu_set_vram_cache_mb(gpu_ctx_t *ctx, int mb);
+float *gpu_forward(gpu_ctx_t *ctx, void *model, int token_id, int pos);
+void gpu_reset_state(gpu_ctx_t *ctx);
+int gpu_seed_vram_cache(gpu_ctx_t *ctx, void *model, const char *freq_profile_path);
+void gpu_enable_expert_freq(gpu_ctx_t *ctx);
+const uint32_t *gpu_get_expert_freq(gpu_ctx_t *ctx);
+void gpu_get_expert_dims(gpu_ctx_t *ctx, int *n_layers, int *n_experts);
+void gpu_get_pingpong_relay_stats(gpu_ctx_t *ctx, uint64_t *handoffs, uint64_t *payload_bytes,
+                                  uint64_t *d2h_bytes, uint64_t *h2d_bytes, uint64_t *dma_bytes);
 
 /* ---------------------------------------------------------------- device memory */
 void *gpu_alloc(gpu_ctx_t *ctx, uint64_t bytes);               /* NULL on failure */

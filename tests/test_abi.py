@@ -3,6 +3,9 @@ and its host-only paths behave as specified — CPU only, no device calls."""
 import ctypes as C
 import os
 import re
+import subprocess
+
+import pytest
 
 import numpy as np
 
@@ -26,6 +29,62 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # and the Python binding covers each of them with a signature
     assert sorted(fomoe_amd.SIGNATURES) == names
+
+
+# Every function the reference's include/gpu.h declares (reference
+# include/gpu.h:13-83); a -DQMOE_GPU build of the reference calls all of them
+# (model.c:411-431, 505, 580; inference.c:427, 544; main.c:571, 882, 953-954).
+REFERENCE_GPU_H = [
+    "gpu_init", "gpu_free", "gpu_register_buffers", "gpu_unregister_buffers", "gpu_upload_model",
+    "gpu_set_ram_cache_mb", "gpu_set_vram_cache_mb", "gpu_forward", "gpu_reset_state",
+    "gpu_seed_vram_cache", "gpu_enable_expert_freq", "gpu_get_expert_freq", "gpu_get_expert_dims",
+    "gpu_get_pingpong_relay_stats", "gpu_expert_ffn",
+]
+REF_GPU_H = "/root/reference/include/gpu.h"
+
+
+def test_reference_gpu_h_names_are_exported():
+    lib = C.CDLL(fomoe_amd.LIB_PATH)
+    missing = [n for n in REFERENCE_GPU_H if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(REFERENCE_GPU_H) <= set(declared_symbols())
+
+
+@pytest.mark.skipif(not os.path.exists(REF_GPU_H), reason="reference sources absent")
+def test_reference_gpu_h_list_is_complete_and_signatures_agree(tmp_path):
+    """The committed name list covers the reference header, and a C unit that
+    includes both headers compiles: any signature that differs between the two
+    declarations is a conflicting-types error."""
+    src = re.sub(r"//[^\n]*", "", open(REF_GPU_H).read())
+    names = set(re.findall(r"\b(gpu_[a-z0-9_]+)\s*\(", src))
+    assert names == set(REFERENCE_GPU_H)
+    unit = tmp_path / "both.c"
+    unit.write_text(f'#include "{REF_GPU_H}"\n#include "{os.path.join(ROOT, "include", "gpu.h")}"\n')
+    r = subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-fsyntax-only", str(unit)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_reference_lifecycle_stubs_report_not_available():
+    """Host-only: the whole-model entry points give the reference's fallback
+    answers (no device needed for a NULL context)."""
+    lib = fomoe_amd.load_library()
+    assert lib.gpu_upload_model(None, None) == -1
+    assert lib.gpu_forward(None, None, 0, 0) is None
+    assert lib.gpu_seed_vram_cache(None, None, b"x") == -1
+    assert lib.gpu_get_expert_freq(None) is None
+    nl, ne = C.c_int(7), C.c_int(7)
+    lib.gpu_get_expert_dims(None, C.byref(nl), C.byref(ne))
+    assert nl.value == 0 and ne.value == 0
+    v = [C.c_uint64(9) for _ in range(5)]
+    lib.gpu_get_pingpong_relay_stats(None, *[C.byref(x) for x in v])
+    assert all(x.value == 0 for x in v)
+    lib.gpu_register_buffers(None, None, 0, 0)
+    lib.gpu_unregister_buffers(None, None, 0)
+    lib.gpu_set_ram_cache_mb(None, 1)
+    lib.gpu_set_vram_cache_mb(None, 1)
+    lib.gpu_reset_state(None)
+    lib.gpu_enable_expert_freq(None)
 
 
 def test_library_is_gfx950_only():

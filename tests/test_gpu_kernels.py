@@ -449,7 +449,10 @@ def _ffn_oracle(blobs, h, scores, H, F, gs, us, types):
 
 @pytest.mark.parametrize("types,H,F,n", [((O.Q4_K, O.Q4_K, O.Q6_K), 4096, 1024, 10),
                                          ((O.Q4_K, O.Q5_K, O.Q5_K), 1024, 512, 3),
-                                         ((O.Q6_K, O.Q6_K, O.Q4_K), 2048, 2048, 1)])
+                                         ((O.Q6_K, O.Q6_K, O.Q4_K), 2048, 2048, 1),
+                                         # gate and up prepared at different group sizes
+                                         ((O.Q4_K, O.Q6_K, O.Q4_K), 4096, 1024, 2),
+                                         ((O.Q6_K, O.Q5_K, O.Q6_K), 4096, 512, 2)])
 def test_expert_ffn_reference_abi(gpu, types, H, F, n):
     say("expert_ffn", types, H, F, n)
     blobs, gs, us, stride = _ffn_blobs(n, H, F, 50 + n, types)
