@@ -63,32 +63,54 @@ template <int NG, int GSZ> struct XSlot {
 // limbs of X = round(x * 2^e) (layout above), the scale 2^-e and the fp32
 // sum, in registers. prep_group (kernels.hip) stores them; k_xprep uses one
 // thread per group, the tile kernels one lane per group, bit-identically.
+// Scale and sum of a prepared group. The sum is that of the quantized values,
+// sum_i X_i * 2^-e, from the exact integer sum with one rounding: it enters
+// the dots as the Q4_K/Q5_K min term (dmin * m * sum) and the Q6_K offset
+// (-32 * sum), where it cancels against the code sums, so a sequential fp32
+// sum of x (up to GSZ roundings of partial sums) would cost several times the
+// reference's own rounding error. A group holding a NaN or an infinity gets
+// NaN for both, so that the non-finite value reaches every output it touches,
+// as in the reference's fp32 dot (the limbs of such a group are meaningless).
+FO_DEV void group_scale_sum(float M, float chk, int e, int isum, float &scale, float &sum) {
+    if (chk != 0.f) {   // chk = sum of v * 0: NaN exactly when some v is NaN or infinite
+        scale = sum = __int_as_float(0x7FC00000);
+        return;
+    }
+    scale = (M > 0.f) ? ldexpf(1.0f, -e) : 0.f;
+    sum = (float)isum * scale;
+}
+
+// One group of GSZ values: exponent from the group maximum, the balanced int8
+// limbs of X = round(x * 2^e) (layout above), the scale 2^-e and the group
+// sum (group_scale_sum), in registers. prep_group (kernels.hip) stores them;
+// k_xprep uses one thread per group, the tile kernels one lane per group,
+// bit-identically.
 template <int GSZ>
 FO_DEV void prep_group_regs(const float *__restrict__ xp, int (&limb)[kLimbs][GSZ / 4], float &scale,
                             float &sum) {
     float vals[GSZ];
-    float M = 0.f;
-    sum = 0.f;
+    float M = 0.f, chk = 0.f;
 #pragma unroll
     for (int i = 0; i < GSZ; i += 4) {
         float4 t = *(const float4 *)(xp + i);
         vals[i] = t.x; vals[i + 1] = t.y; vals[i + 2] = t.z; vals[i + 3] = t.w;
     }
 #pragma unroll
-    for (int i = 0; i < GSZ; i++) { M = fmaxf(M, fabsf(vals[i])); sum += vals[i]; }
+    for (int i = 0; i < GSZ; i++) { M = fmaxf(M, fabsf(vals[i])); chk += vals[i] * 0.f; }
     int E = 0;
     frexpf(M, &E);               // M < 2^E
     int e = kFixBits - E;
     if (e > 149) e = 149;        // keep 2^-e representable
-    scale = (M > 0.f) ? ldexpf(1.0f, -e) : 0.f;
     uint32_t lb[kLimbs][GSZ / 4];
 #pragma unroll
     for (int L = 0; L < kLimbs; L++)
 #pragma unroll
         for (int k = 0; k < GSZ / 4; k++) lb[L][k] = 0;
+    int isum = 0;                // |isum| < GSZ * 2^22: exact in int32
 #pragma unroll
     for (int i = 0; i < GSZ; i++) {
-        int X = (M > 0.f) ? __float2int_rn(ldexpf(vals[i], e)) : 0;
+        int X = (M > 0.f && chk == 0.f) ? __float2int_rn(ldexpf(vals[i], e)) : 0;
+        isum += X;
 #pragma unroll
         for (int L = 0; L < kLimbs - 1; L++) {
             const int b = (int)(int8_t)(X & 0xFF);
@@ -97,6 +119,7 @@ FO_DEV void prep_group_regs(const float *__restrict__ xp, int (&limb)[kLimbs][GS
         }
         lb[kLimbs - 1][i / 4] |= (uint32_t)(X & 0xFF) << (8 * (i % 4));
     }
+    group_scale_sum(M, chk, e, isum, scale, sum);
 #pragma unroll
     for (int L = 0; L < kLimbs; L++)
 #pragma unroll

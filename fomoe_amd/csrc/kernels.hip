@@ -840,17 +840,19 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a, uint8_t *__restric
             const int g = blockIdx.x * per + j;
             if (g >= ng) break;
             const float *xp = sh + g * gsz;
-            float M = 0.f, sum = 0.f;
-            for (int i = 0; i < gsz; i++) { M = fmaxf(M, fabsf(xp[i])); sum += xp[i]; }
+            float M = 0.f, chk = 0.f;
+            for (int i = 0; i < gsz; i++) { M = fmaxf(M, fabsf(xp[i])); chk += xp[i] * 0.f; }
             int E = 0;
             frexpf(M, &E);
             int e = kFixBits - E;
             if (e > 149) e = 149;
             uint32_t *lp = (uint32_t *)(xq_h + (uint64_t)g * (kLimbs * gsz));
+            int isum = 0;
             for (int k = 0; k < gsz / 4; k++) {
                 uint32_t lb[kLimbs] = {};
                 for (int b = 0; b < 4; b++) {
-                    int X = (M > 0.f) ? __float2int_rn(ldexpf(xp[4 * k + b], e)) : 0;
+                    int X = (M > 0.f && chk == 0.f) ? __float2int_rn(ldexpf(xp[4 * k + b], e)) : 0;
+                    isum += X;
                     for (int L = 0; L < kLimbs - 1; L++) {
                         const int v = (int)(int8_t)(X & 0xFF);
                         X = (X - v) >> 8;
@@ -860,8 +862,9 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a, uint8_t *__restric
                 }
                 for (int L = 0; L < kLimbs; L++) lp[L * (gsz / 4) + k] = lb[L];
             }
-            *(float2 *)(xq_h + xq_limb_bytes(H) + (uint64_t)g * 8) =
-                make_float2((M > 0.f) ? ldexpf(1.0f, -e) : 0.f, sum);
+            float scale, sum;
+            group_scale_sum(M, chk, e, isum, scale, sum);
+            *(float2 *)(xq_h + xq_limb_bytes(H) + (uint64_t)g * 8) = make_float2(scale, sum);
         }
     }
     // one row per wave

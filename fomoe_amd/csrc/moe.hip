@@ -37,23 +37,28 @@ FO_DEV float wave_sum_dpp(float v) { return group_sum<kWave>(v); }
 
 // Prepare one group of G values held one per lane in lanes [0, G) of a wave
 // (G = 16 or 32): exponent from the group maximum, three balanced int8 limbs
-// per value packed four values per dword, {2^-e, fp32 sum}. Layout as in
+// per value packed four values per dword, {2^-e, group sum} (group_scale_sum). Layout as in
 // formats.h. `dst` points at the vector's limb area, `ss` at its {scale,sum}
 // area, g is the group index.
 template <int G>
 FO_DEV void prep_group_lanes(float val, int g, uint8_t *__restrict__ dst, uint8_t *__restrict__ ss) {
     const int lane = threadIdx.x & 63;
-    float a = fabsf(val), s = val;
+    float a = fabsf(val), chk = val * 0.f;
 #pragma unroll
     for (int o = 1; o < G; o <<= 1) {
         a = fmaxf(a, __shfl_xor(a, o, 64));
-        s += __shfl_xor(s, o, 64);
+        chk += __shfl_xor(chk, o, 64);
     }
     int E = 0;
     frexpf(a, &E);
     int e = kFixBits - E;
     if (e > 149) e = 149;
-    int X = (a > 0.f) ? __float2int_rn(ldexpf(val, e)) : 0;
+    int X = (a > 0.f && chk == 0.f) ? __float2int_rn(ldexpf(val, e)) : 0;
+    int isum = X;
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) isum += __shfl_xor(isum, o, 64);
+    float scale, sum;
+    group_scale_sum(a, chk, e, isum, scale, sum);
     uint32_t limb[kLimbs];
 #pragma unroll
     for (int L = 0; L < kLimbs - 1; L++) {
@@ -75,7 +80,7 @@ FO_DEV void prep_group_lanes(float val, int g, uint8_t *__restrict__ dst, uint8_
 #pragma unroll
         for (int L = 0; L < kLimbs; L++) p[L * (G / 4) + (lane >> 2)] = limb[L];
     }
-    if (lane == 0) *(float2 *)(ss + (uint64_t)g * 8) = make_float2(a > 0.f ? ldexpf(1.0f, -e) : 0.f, s);
+    if (lane == 0) *(float2 *)(ss + (uint64_t)g * 8) = make_float2(scale, sum);
 }
 
 // ============================================================ K1: route

@@ -17,6 +17,8 @@ from conftest import inf_rel, parity_err
 pytestmark = pytest.mark.gpu
 GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
 TOL = 1e-3
+# the full config-3 layer keeps at least 2x margin under TOL (worst measured seed 3.4e-4)
+PARITY_MARGIN_BAR = 5e-4
 
 
 def say(*a):
@@ -134,6 +136,35 @@ def test_matvec_activation_extremes(gpu, t, K):
     got = gpu.download(dy, np.float32, M)
     ref = O.dequantize(t, W, M * K).reshape(M, K).astype(np.float64) @ x.astype(np.float64)
     assert parity_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("t,M,K", [(O.Q4_K, 64, 4096), (O.Q6_K, 64, 1024), (O.Q8_0, 64, 1024),
+                                   (O.Q5_K, 64, 1024), (O.Q4_K, 5, 1024), (O.Q6_K, 3, 2048),
+                                   (O.Q8_0, 5, 96), (O.MXFP4, 7, 4096)])
+@pytest.mark.parametrize("bad", ["nan", "inf", "-inf"])
+def test_matvec_nonfinite_activation(gpu, t, M, K, bad):
+    """One NaN or infinite activation makes every output non-finite, as in
+    the reference's fp32 dot (every row has a weight on that value), and the
+    other groups' outputs of a clean second vector are unaffected."""
+    say("matvec nonfinite", t, M, K, bad)
+    W = O.synth_quant(t, 33, 0, 0.02, M, K) if t != O.MXFP4 else \
+        np.frombuffer(np.random.default_rng(3).integers(0, 255, M * K // 32 * 17, dtype=np.uint8).tobytes(),
+                      np.uint8).copy()
+    if t == O.MXFP4:
+        W.reshape(-1, 17)[:, 0] = 120 + W.reshape(-1, 17)[:, 0] % 15   # finite block scales
+    x = O.synth_f32(34, 0, 1.0, K)
+    x[K // 3] = float(bad)
+    dW, dx, dy = gpu.upload(W), gpu.upload(x), gpu.alloc(4 * M)
+    gpu.matvec(t, dW, dx, dy, M, K)
+    got = gpu.download(dy, np.float32, M)
+    want = O.mat_vec(t, W, x, M, K)
+    assert not np.isfinite(want).any()
+    assert not np.isfinite(got).any(), got
+    # the same launch shape with a finite vector is unaffected by the previous call
+    x2 = O.synth_f32(35, 0, 1.0, K)
+    gpu.upload_to(dx, x2)
+    gpu.matvec(t, dW, dx, dy, M, K)
+    assert parity_err(gpu.download(dy, np.float32, M), O.mat_vec(t, W, x2, M, K)) <= TOL
 
 
 @pytest.mark.parametrize("M,K", [(1, 32), (5, 96), (64, 4096), (33, 2880), (7, 8192), (13, 4096)])
@@ -367,23 +398,25 @@ def test_moe_layer_shapes_vs_fp64(gpu, H, F, E, k, shared):
     assert inf_rel(got, want) < 1e-5
 
 
-def test_moe_layer_config3_full(gpu):
+@pytest.mark.parametrize("seed", [4, 5, 6])
+def test_moe_layer_config3_full(gpu, seed):
     """BASELINE config 3 at full size: 512 experts (Q4_K gate/up 1024x4096, Q6_K
     down 4096x1024) + shared, top-10, generated in HBM; the oracle rebuilds the
-    router and only the selected experts on the CPU."""
+    router and only the selected experts on the CPU. Seed 4 is the BASELINE
+    one; 5 and 6 are further samples of the same workload."""
     from fomoe_amd import synthetic as S
-    say("moe config3 full")
+    say("moe config3 full, seed", seed)
     shape = S.LayerShape()
-    layer = S.build_layer(gpu, shape, layer=0, seed=4, norm=False)
-    dh = S.hidden(gpu, shape.n_embd)
+    layer = S.build_layer(gpu, shape, layer=0, seed=seed, norm=False)
+    dh = S.hidden(gpu, shape.n_embd, seed=seed)
     dout = gpu.alloc(4 * shape.n_embd)
     gpu.moe_layer(layer.desc, dh, dout, 0)
     out = gpu.download(dout, np.float32, shape.n_embd)
     ids, w, sw = gpu.last_routing(shape.k)
     E, H, F, k = shape.n_experts, shape.n_embd, shape.inter, shape.k
-    h = O.synth_f32(4, S.stream(0, 0, S.HIDDEN), 1.0, H)
+    h = O.synth_f32(seed, S.stream(0, 0, S.HIDDEN), 1.0, H)
     assert np.array_equal(gpu.download(dh, np.float32, H), h)
-    router = O.synth_f32(4, S.stream(0, 0, S.ROUTER), 0.02, E * H)
+    router = O.synth_f32(seed, S.stream(0, 0, S.ROUTER), 0.02, E * H)
     p = O.softmax(O.mat_vec(O.F32, router, h, E, H))
     oi, ov = O.top_k(p, k)
     assert np.array_equal(ids, oi)
@@ -391,9 +424,9 @@ def test_moe_layer_config3_full(gpu):
     stride = shape.stride
     table = np.zeros((E + 1) * stride, np.uint8)
     for e in [int(v) for v in oi] + [E]:
-        blob = np.concatenate([O.synth_quant(O.Q4_K, 4, S.stream(0, e, S.GATE), 0.02, F, H),
-                               O.synth_quant(O.Q4_K, 4, S.stream(0, e, S.UP), 0.02, F, H),
-                               O.synth_quant(O.Q6_K, 4, S.stream(0, e, S.DOWN), 0.02, H, F)])
+        blob = np.concatenate([O.synth_quant(O.Q4_K, seed, S.stream(0, e, S.GATE), 0.02, F, H),
+                               O.synth_quant(O.Q4_K, seed, S.stream(0, e, S.UP), 0.02, F, H),
+                               O.synth_quant(O.Q6_K, seed, S.stream(0, e, S.DOWN), 0.02, H, F)])
         table[e * stride:e * stride + blob.size] = blob
         # the device holds the same bytes
         dev = gpu.download(layer.desc.experts + e * stride, np.uint8, blob.size)
@@ -403,26 +436,33 @@ def test_moe_layer_config3_full(gpu):
     d.expert_stride = stride
     want, _, ow = O.moe_layer(d, h, 0)
     assert inf_rel(w, ow) < 1e-5
-    # parity against an fp64 recomposition of the same dequantized weights (the
-    # fp32 oracle itself carries ~1e-6 relative rounding, which at the 1e-3
-    # floor of parity_err is the same size as the bar); the fp32 oracle is
-    # checked by inf_rel
+    # parity against the exact layer: an fp64 recomposition of the same
+    # dequantized weights with fp64 router logits, softmax and renormalised
+    # weights. (The fp32 oracle's routing weights are themselves ~2e-6 off the
+    # exact ones, which at the 1e-3 floor of parity_err is larger than the
+    # GPU path's own error, so the oracle is compared by inf_rel instead.)
     x = h.astype(np.float64)
-    ref = np.zeros(H)
-    for r, ei in enumerate(list(oi) + [E]):
+    ys = []
+    for ei in list(oi) + [E]:
         blob = table[int(ei) * stride:]
         G = O.dequantize(O.Q4_K, blob[:shape.gate_size], F * H).reshape(F, H).astype(np.float64)
         U = O.dequantize(O.Q4_K, blob[shape.gate_size:2 * shape.gate_size], F * H).reshape(F, H).astype(np.float64)
         D = O.dequantize(O.Q6_K, blob[2 * shape.gate_size:2 * shape.gate_size + shape.down_size],
                          H * F).reshape(H, F).astype(np.float64)
         g = G @ x
-        y = D @ (g / (1 + np.exp(-g)) * (U @ x))
-        ref += (float(ow[r]) if r < k else 1.0) * y
+        ys.append(D @ (g / (1 + np.exp(-g)) * (U @ x)))
+    lg = router.astype(np.float64).reshape(E, H) @ x
+    p64 = np.exp(lg - lg.max())
+    p64 /= p64.sum()
+    w64 = p64[oi] / p64[oi].sum()
+    ref = sum(float(w64[r]) * ys[r] for r in range(k)) + ys[k]
     e = parity_err(out, ref)
-    say(f"  parity_err(fp64) {e:.3e} inf_rel(fp32 oracle) {inf_rel(out, want):.3e} "
-        f"oracle vs fp64 parity {parity_err(want, ref):.3e}")
+    say(f"  PARITY config3 seed {seed}: gpu parity_err(exact) {e:.3e} inf_rel(fp32 oracle) "
+        f"{inf_rel(out, want):.3e}; fp32 oracle parity_err(exact) {parity_err(want, ref):.3e}; "
+        f"routing weights inf_rel vs exact: gpu {inf_rel(w, w64):.3e} oracle {inf_rel(ow, w64):.3e}")
+    assert inf_rel(w, w64) < 1e-6
     assert inf_rel(out, want) < 1e-5
-    assert e <= TOL
+    assert e <= PARITY_MARGIN_BAR
 
 
 # ------------------------------------------------------------------ reference ABI
