@@ -34,6 +34,8 @@ struct gpu_ctx {
     uint8_t *staging = nullptr;    size_t staging_cap = 0;
     int last_k = 0;
     bool last_fast = false;      // routing of the last layer came from the K1-K3 path
+    const int32_t *last_ids = nullptr;   // where the last layer call left its routing
+    const float *last_weights = nullptr;
 
     // prefill workspace (grown on demand)
     float *pf_logits = nullptr;    size_t pf_logits_cap = 0;

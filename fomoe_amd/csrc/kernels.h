@@ -93,6 +93,8 @@ hipError_t launch_down(int type, const DownArgs &a, const uint8_t *xq_act, uint6
                        hipStream_t s, int n_cu);
 hipError_t launch_dequant(int type, const uint8_t *src, float *dst, int64_t n, hipStream_t s);
 hipError_t launch_silu_mul(float *g, const float *u, int64_t n, hipStream_t s);
+// p[0..n) = 0 with a kernel (usable inside captured graphs, unlike a memset node)
+hipError_t launch_zero_u32(uint32_t *p, int n, hipStream_t s);
 
 // Synthetic data (bit-identical to the CPU generator in oracle/).
 hipError_t launch_synth_f32(uint64_t seed, uint64_t stream, float std, float *out,

@@ -813,7 +813,7 @@ hipError_t launch_matvec(int type, const MatvecArgs &a, hipStream_t s, int n_cu)
 // renormalisation (reference src/inference.c:486-502, src/tensor.c:186-252).
 constexpr int kRouterMaxE = 1024;
 
-template <int UH>  // H = 256*UH; a lane holds 4*UH values of h
+template <int UH>  // H = 256*UH; a lane holds 4*UH values of h (UH = 0: any H, a multiple of 256)
 __global__ __launch_bounds__(256) void k_router(RouterArgs a, uint8_t *__restrict__ xq_h, int gsz) {
     extern __shared__ float sh[];  // H floats
     __shared__ float red[4];
@@ -871,17 +871,28 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a, uint8_t *__restric
     const int e = blockIdx.x * 4 + wv;
     if (e < a.E) {
         const float *row = a.W + (uint64_t)e * H;
-        float4 wv4[UH];
-#pragma unroll
-        for (int u = 0; u < UH; u++) wv4[u] = *((const float4 *)row + lane + 64 * u);
         float acc = 0.f;
+        if constexpr (UH > 0) {   // all of the row's loads in flight at once
+            float4 wv4[UH];
 #pragma unroll
-        for (int u = 0; u < UH; u++) {
-            const float4 hv = *(const float4 *)(sh + 4 * (lane + 64 * u));
-            acc = fmaf(wv4[u].x, hv.x, acc);
-            acc = fmaf(wv4[u].y, hv.y, acc);
-            acc = fmaf(wv4[u].z, hv.z, acc);
-            acc = fmaf(wv4[u].w, hv.w, acc);
+            for (int u = 0; u < UH; u++) wv4[u] = *((const float4 *)row + lane + 64 * u);
+#pragma unroll
+            for (int u = 0; u < UH; u++) {
+                const float4 hv = *(const float4 *)(sh + 4 * (lane + 64 * u));
+                acc = fmaf(wv4[u].x, hv.x, acc);
+                acc = fmaf(wv4[u].y, hv.y, acc);
+                acc = fmaf(wv4[u].z, hv.z, acc);
+                acc = fmaf(wv4[u].w, hv.w, acc);
+            }
+        } else {                  // any H = 256 * n: the same sums, one float4 at a time
+            for (int u = 0; u < H / 256; u++) {
+                const float4 w4 = *((const float4 *)row + lane + 64 * u);
+                const float4 hv = *(const float4 *)(sh + 4 * (lane + 64 * u));
+                acc = fmaf(w4.x, hv.x, acc);
+                acc = fmaf(w4.y, hv.y, acc);
+                acc = fmaf(w4.z, hv.z, acc);
+                acc = fmaf(w4.w, hv.w, acc);
+            }
         }
         acc = wave_sum(acc);
         if (lane == 0) a.logits[e] = acc + (a.bias ? a.bias[e] : 0.f);
@@ -971,6 +982,10 @@ hipError_t launch_router(const RouterArgs &a, uint8_t *xq_h, int gsz, hipStream_
     if (a.H == 256 * UU) { k_router<UU><<<blocks, 256, lds, s>>>(a, xq_h, gsz); return hipGetLastError(); }
     FO_RT(1) FO_RT(2) FO_RT(4) FO_RT(8) FO_RT(12) FO_RT(16) FO_RT(24) FO_RT(32)
 #undef FO_RT
+    if (a.H <= 8192) {
+        k_router<0><<<blocks, 256, lds, s>>>(a, xq_h, gsz);
+        return hipGetLastError();
+    }
     return hipErrorInvalidValue;
 }
 
@@ -1194,6 +1209,16 @@ __global__ void k_silu_mul(float *g, const float *u, int64_t n) {
 
 hipError_t launch_silu_mul(float *g, const float *u, int64_t n, hipStream_t s) {
     k_silu_mul<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(g, u, n);
+    return hipGetLastError();
+}
+
+__global__ void k_zero_u32(uint32_t *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+hipError_t launch_zero_u32(uint32_t *p, int n, hipStream_t s) {
+    k_zero_u32<<<(n + 255) / 256, 256, 0, s>>>(p, n);
     return hipGetLastError();
 }
 

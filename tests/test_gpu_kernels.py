@@ -352,7 +352,9 @@ def test_moe_layer_topk_ties_and_fallback(gpu, case):
 
 
 @pytest.mark.parametrize("H,F,E,k,shared", [(512, 512, 16, 4, True), (1024, 1024, 24, 12, True),
-                                             (512, 1024, 8, 3, False), (2048, 512, 16, 13, False)])
+                                             (512, 1024, 8, 3, False), (2048, 512, 16, 13, False),
+                                             # general path: n_embd = 256 * odd (any-H router)
+                                             (768, 256, 8, 2, True), (1280, 512, 12, 3, False)])
 def test_moe_layer_shapes_vs_fp64(gpu, H, F, E, k, shared):
     """Layer shapes on both down-projection kernels (the LDS-staged one for
     F = 1024 up to 12 experts per work-group, the direct one otherwise), with
