@@ -53,6 +53,7 @@ SIGNATURES = {
     "gpu_matvec_q_batched": (C.c_int, [_vp, C.c_int, _vp, C.c_uint64, C.c_int, _vp, C.c_uint64,
                                        _vp, C.c_uint64, C.c_int, C.c_int]),
     "gpu_moe_layer": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int]),
+    "gpu_moe_layer_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int]),
     "gpu_moe_last_routing": (C.c_int, [_vp, _vp, _vp, _vp]),
     "gpu_router_topk": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_float, C.c_int, C.c_int, C.c_int,
                                   _vp, _vp]),
@@ -329,6 +330,11 @@ class Gpu:
     def moe_layer(self, layer: MoeLayer, x, out, flags: int):
         self.check(self.lib.gpu_moe_layer(self.ctx, C.byref(layer), _p(x), _p(out), flags),
                    "gpu_moe_layer")
+
+    def moe_layer_noalloc(self, layer: MoeLayer, x, out, flags: int) -> int:
+        """gpu_moe_layer_noalloc; returns its code (0, or -1 for a layer whose
+        scratch exceeds the static area)."""
+        return self.lib.gpu_moe_layer_noalloc(self.ctx, C.byref(layer), _p(x), _p(out), flags)
 
     def last_routing(self, k: int):
         ids = np.empty(k, np.int32)

@@ -25,6 +25,28 @@
 
 using namespace fo;
 
+// ------------------------------------------------------------------ no-allocation scratch
+// The device scratch of gpu_moe_layer_noalloc: one static array per device,
+// held until the process ends. Host code never passes `fo_noalloc_scratch`
+// itself to a kernel (in host code the name is a host-side stand-in): its
+// device address is looked up once per device with hipGetSymbolAddress in
+// gpu_init and kept in g_noalloc_ptr.
+static constexpr size_t kNoAllocBytes = 1u << 20;   // GPU_MOE_NOALLOC_SCRATCH_BYTES
+static_assert(kNoAllocBytes == GPU_MOE_NOALLOC_SCRATCH_BYTES, "header and library agree");
+static __device__ __align__(256) uint8_t fo_noalloc_scratch[kNoAllocBytes];
+static constexpr int kMaxDevices = 64;
+static void *g_noalloc_ptr[kMaxDevices];
+
+static hipError_t noalloc_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (g_noalloc_ptr[device]) return hipSuccess;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(fo_noalloc_scratch));
+    if (e != hipSuccess || !p) return e != hipSuccess ? e : hipErrorInvalidSymbol;
+    g_noalloc_ptr[device] = p;
+    return hipSuccess;
+}
+
 extern "C" {
 
 gpu_ctx_t *gpu_init(void) {
@@ -52,6 +74,7 @@ gpu_ctx_t *gpu_init(void) {
               hipMalloc((void **)&c->weights, 64 * sizeof(float)) == hipSuccess &&
               hipMemset(c->counter, 0, 256) == hipSuccess &&
               hipMemset(c->ids, 0, 64 * sizeof(int32_t)) == hipSuccess &&
+              noalloc_setup(c->device) == hipSuccess &&
               hipDeviceSynchronize() == hipSuccess;
     if (!ok) {
         gpu_free(c);
@@ -228,52 +251,73 @@ static bool fast_layer(const gpu_moe_layer_t *L) {
     return L->n_embd % 512 == 0 && L->n_embd <= 8192 && L->inter / dslot <= 64 && n_tot <= 16;
 }
 
-static constexpr int kSharedW = 32;   // ctx->weights[32] holds the shared-expert weight
+static constexpr int kSharedW = 32;   // weights[32] holds the shared-expert weight
 
-static int enqueue_layer_fast(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float *in, float *out,
-                              int flags, const float *norm_w) {
+// Device scratch of one layer call: the context's grown buffers, or the
+// carve-up of the static no-allocation area.
+struct LayerScratch {
+    float *logits;       // [1024]
+    unsigned *counter;   // general router's completion counter (zero between calls)
+    int32_t *ids;        // [64]
+    float *weights;      // [64]
+    uint8_t *xq_h;       // prepared h
+    uint8_t *xq_act;     // n_tot prepared activations
+    float *act;          // [n_tot x F] fp32 activations (general path)
+};
+
+static LayerScratch ctx_scratch(gpu_ctx_t *ctx) {
+    return LayerScratch{ctx->logits, ctx->counter, ctx->ids, ctx->weights, ctx->xq_h, ctx->xq_act, ctx->act};
+}
+
+static int enqueue_layer_fast(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_moe_layer_t *L,
+                              const float *in, float *out, int flags, const float *norm_w) {
     const int H = L->n_embd, F = L->inter;
     const int dg = gsz_of(L->down_type);
     const uint64_t xs = xq_stride(F, dg);
     const uint8_t *base = (const uint8_t *)L->experts, *sh = (const uint8_t *)L->shared;
-    float *shared_w = ctx->weights + kSharedW;
-    RouteArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, ctx->logits,
-                 ctx->xq_h, gsz_of(L->gate_type), L->shared_gate_vec, shared_w};
+    float *shared_w = sc.weights + kSharedW;
+    RouteArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, sc.logits,
+                 sc.xq_h, gsz_of(L->gate_type), L->shared_gate_vec, shared_w};
     HIPC(launch_route(ra, ctx->stream));
-    ExpandArgs ea{ctx->logits, L->n_experts, L->k, ctx->ids, ctx->weights, base, L->expert_stride,
+    ExpandArgs ea{sc.logits, L->n_experts, L->k, sc.ids, sc.weights, base, L->expert_stride,
                   L->gate_size, sh, L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H),
-                  ctx->xq_h, ctx->xq_act, xs, dg, nullptr};
+                  sc.xq_h, sc.xq_act, xs, dg, nullptr};
     HIPC(launch_expand(L->gate_type, ea, ctx->stream, ctx->n_cu));
-    ReduceArgs da{ctx->ids, ctx->weights, sh ? shared_w : nullptr, L->k, base, L->expert_stride,
+    ReduceArgs da{sc.ids, sc.weights, sh ? shared_w : nullptr, L->k, base, L->expert_stride,
                   L->gate_size + L->up_size, sh, L->shared_gate_size + L->shared_up_size, F, H,
-                  fomoe_row_bytes(L->down_type, F), ctx->xq_act, xs,
+                  fomoe_row_bytes(L->down_type, F), sc.xq_act, xs,
                   (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out};
     HIPC(launch_reduce(L->down_type, da, ctx->stream, ctx->n_cu));
     return 0;
 }
 
-static int enqueue_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float *in, float *out,
-                         int flags) {
+static int enqueue_layer(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_moe_layer_t *L,
+                         const float *in, float *out, int flags) {
     const int H = L->n_embd, F = L->inter, n_tot = L->k + (L->shared ? 1 : 0);
     const float *norm_w = (flags & GPU_MOE_NORM) ? L->norm_w : nullptr;
     if ((flags & GPU_MOE_NORM) && !norm_w) return fail(ctx, -1, "moe layer: GPU_MOE_NORM without norm_w");
-    ctx->last_fast = fast_layer(L);
-    if (ctx->last_fast) return enqueue_layer_fast(ctx, L, in, out, flags, norm_w);
+    const bool fast = fast_layer(L);
+    if (fast) {
+        const int rc = enqueue_layer_fast(ctx, sc, L, in, out, flags, norm_w);
+        if (!rc) ctx->last_fast = true;
+        return rc;
+    }
+    ctx->last_fast = false;
     RouterArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, L->k,
-                  ctx->logits, ctx->counter, ctx->ids, ctx->weights, L->shared_gate_vec};
-    HIPC(launch_router(ra, ctx->xq_h, gsz_of(L->gate_type), ctx->stream));
+                  sc.logits, sc.counter, sc.ids, sc.weights, L->shared_gate_vec};
+    HIPC(launch_router(ra, sc.xq_h, gsz_of(L->gate_type), ctx->stream));
     const uint8_t *base = (const uint8_t *)L->experts, *sh = (const uint8_t *)L->shared;
-    GateUpArgs ga{ctx->ids, L->k, base, L->expert_stride, 0, L->gate_size, sh, 0,
+    GateUpArgs ga{sc.ids, L->k, base, L->expert_stride, 0, L->gate_size, sh, 0,
                   L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H), in, norm_w,
-                  L->eps, ctx->act};
-    HIPC(launch_gateup(L->gate_type, ga, ctx->xq_h, ctx->stream, ctx->n_cu));
+                  L->eps, sc.act};
+    HIPC(launch_gateup(L->gate_type, ga, sc.xq_h, ctx->stream, ctx->n_cu));
     const int gsz = gsz_of(L->down_type);
     const uint64_t xs = xq_stride(F, gsz);
-    HIPC(launch_xprep(gsz, ctx->act, (uint64_t)F, F, n_tot, ctx->xq_act, xs, ctx->stream));
-    DownArgs da{ctx->ids, ctx->weights, L->k, base, L->expert_stride, L->gate_size + L->up_size,
-                sh, L->shared_gate_size + L->shared_up_size, ctx->act, H, F,
+    HIPC(launch_xprep(gsz, sc.act, (uint64_t)F, F, n_tot, sc.xq_act, xs, ctx->stream));
+    DownArgs da{sc.ids, sc.weights, L->k, base, L->expert_stride, L->gate_size + L->up_size,
+                sh, L->shared_gate_size + L->shared_up_size, sc.act, H, F,
                 fomoe_row_bytes(L->down_type, F), (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out};
-    HIPC(launch_down(L->down_type, da, ctx->xq_act, xs, ctx->stream, ctx->n_cu));
+    HIPC(launch_down(L->down_type, da, sc.xq_act, xs, ctx->stream, ctx->n_cu));
     return 0;
 }
 
@@ -281,8 +325,55 @@ int gpu_moe_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float *in, flo
     if (!ctx || !in || !out) return fail(ctx, -1, "gpu_moe_layer: null pointer");
     int rc = check_layer(ctx, L);
     if (!rc) rc = size_layer(ctx, L);
-    if (!rc) rc = enqueue_layer(ctx, L, in, out, flags);
-    if (!rc) ctx->last_k = L->k;
+    if (!rc) rc = enqueue_layer(ctx, ctx_scratch(ctx), L, in, out, flags);
+    if (!rc) {
+        ctx->last_k = L->k;
+        ctx->last_ids = ctx->ids;
+        ctx->last_weights = ctx->weights;
+    }
+    return rc;
+}
+
+// Byte layout of the no-allocation scratch for one layer (256-byte aligned
+// pieces); returns the bytes needed.
+static size_t noalloc_layout(const gpu_moe_layer_t *L, uint8_t *base, LayerScratch *sc) {
+    const int n_tot = L->k + (L->shared ? 1 : 0);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t *p = base + off;
+        off += (bytes + 255) & ~(size_t)255;
+        return p;
+    };
+    uint8_t *logits = take(1024 * sizeof(float)), *counter = take(256), *ids = take(64 * sizeof(int32_t)),
+            *weights = take(64 * sizeof(float)), *xq_h = take(xq_stride(L->n_embd, gsz_of(L->gate_type))),
+            *xq_act = take(xq_stride(L->inter, gsz_of(L->down_type)) * (size_t)n_tot),
+            *act = take(sizeof(float) * (size_t)n_tot * L->inter);
+    if (sc)
+        *sc = LayerScratch{(float *)logits, (unsigned *)counter, (int32_t *)ids, (float *)weights, xq_h, xq_act,
+                           (float *)act};
+    return off;
+}
+
+int gpu_moe_layer_noalloc(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float *in, float *out, int flags) {
+    if (!ctx || !in || !out) return fail(ctx, -1, "gpu_moe_layer_noalloc: null pointer");
+    if (int rc = check_layer(ctx, L)) return rc;
+    const size_t need = noalloc_layout(L, nullptr, nullptr);
+    if (need > kNoAllocBytes)
+        return fail(ctx, -1, "gpu_moe_layer_noalloc: layer needs %zu bytes of scratch, the static area holds %zu",
+                    need, kNoAllocBytes);
+    uint8_t *base = (ctx->device >= 0 && ctx->device < kMaxDevices) ? (uint8_t *)g_noalloc_ptr[ctx->device] : nullptr;
+    if (!base) return fail(ctx, -2, "gpu_moe_layer_noalloc: scratch address of device %d unknown", ctx->device);
+    LayerScratch sc;
+    noalloc_layout(L, base, &sc);
+    // the area keeps the previous call's contents: the general router's
+    // completion counter must start at zero (a kernel fill, not a memset node)
+    if (!fast_layer(L)) HIPC(launch_zero_u32(sc.counter, 64, ctx->stream));
+    const int rc = enqueue_layer(ctx, sc, L, in, out, flags);
+    if (!rc) {
+        ctx->last_k = L->k;
+        ctx->last_ids = sc.ids;
+        ctx->last_weights = sc.weights;
+    }
     return rc;
 }
 
@@ -290,8 +381,8 @@ int gpu_moe_last_routing(gpu_ctx_t *ctx, int32_t *ids, float *w, float *shared_w
     if (!ctx || ctx->last_k <= 0) return fail(ctx, -1, "no routing recorded");
     float tmp[64];
     HIPC(hipStreamSynchronize(ctx->stream));
-    if (ids) HIPC(hipMemcpy(ids, ctx->ids, sizeof(int32_t) * ctx->last_k, hipMemcpyDeviceToHost));
-    HIPC(hipMemcpy(tmp, ctx->weights, sizeof(float) * (kSharedW + 1), hipMemcpyDeviceToHost));
+    if (ids) HIPC(hipMemcpy(ids, ctx->last_ids, sizeof(int32_t) * ctx->last_k, hipMemcpyDeviceToHost));
+    HIPC(hipMemcpy(tmp, ctx->last_weights, sizeof(float) * (kSharedW + 1), hipMemcpyDeviceToHost));
     if (w) memcpy(w, tmp, sizeof(float) * ctx->last_k);
     if (shared_w) *shared_w = ctx->last_fast ? tmp[kSharedW] : tmp[ctx->last_k];
     return 0;
@@ -326,7 +417,7 @@ int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_la
     HIPC(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     int rc = 0;
     for (int l = 0; l < n_layers && !rc; l++)
-        rc = enqueue_layer(ctx, &layers[l], x, x, GPU_MOE_NORM | GPU_MOE_RESIDUAL);
+        rc = enqueue_layer(ctx, ctx_scratch(ctx), &layers[l], x, x, GPU_MOE_NORM | GPU_MOE_RESIDUAL);
     hipGraph_t g = nullptr;
     hipError_t ce = hipStreamEndCapture(ctx->stream, &g);
     if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
@@ -336,6 +427,8 @@ int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_la
     if (ie != hipSuccess) return fail(ctx, -2, "graph instantiate failed: %s", hipGetErrorString(ie));
     for (int s = 0; s < n_steps; s++) HIPC(hipGraphLaunch(ctx->graph_exec, ctx->stream));
     ctx->last_k = layers[n_layers - 1].k;
+    ctx->last_ids = ctx->ids;
+    ctx->last_weights = ctx->weights;
     return 0;
 }
 

@@ -151,6 +151,19 @@ typedef struct {
  * src/inference.c:481-606; gpu_kernels.hip 5514-5528, 7405-7435, 7740). */
 int gpu_moe_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *layer, const float *d_in,
                   float *d_out, int flags);
+/* gpu_moe_layer without any device allocation: no hipMalloc, hipFree or
+ * allocating library call on any path (async, same semantics and kernels as
+ * gpu_moe_layer, bit-identical results). No counterpart in the reference; it
+ * is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation). Its scratch is one static
+ * device area of GPU_MOE_NOALLOC_SCRATCH_BYTES per device, held until the
+ * process ends; a layer whose scratch (router logits, routing, prepared h, the
+ * k+1 activations) does not fit returns -1 with a message. Every call on a
+ * device shares that area: calls that overlap on one device (two contexts,
+ * or two host threads) race. gpu_moe_last_routing reports its routing too. */
+#define GPU_MOE_NOALLOC_SCRATCH_BYTES (1u << 20)
+int gpu_moe_layer_noalloc(gpu_ctx_t *ctx, const gpu_moe_layer_t *layer, const float *d_in,
+                          float *d_out, int flags);
 /* Routing of the most recent gpu_moe_layer call (sync): k ids, k weights
  * and the shared-expert weight. */
 int gpu_moe_last_routing(gpu_ctx_t *ctx, int32_t *ids, float *weights, float *shared_weight);
