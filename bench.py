@@ -123,8 +123,8 @@ def _time_loop(fn, n_items, seconds):
 
 
 def cpu_matvec_baselines(gpu, keeps, seconds, env):
-    """CPU matvec legs on this host, each over a rotation of the same device
-    matrices large enough (>= 200 MB) not to stay in the CPU's caches:
+    """CPU matvec legs on this host, each over the same rotation of 512
+    matrices as the GPU leg (1.2-2.3 GB, beyond any CPU cache):
     - the cpu_expert.c engine (reference quant.c mat_vec_mul_fast: Q8_K
       activations, AVX2 integer dots, OpenMP over rows; quant.c:343-607,
       cpu_expert.c:52-72) for Q6_K (config 2, the headline's cpu_baseline)
@@ -146,7 +146,7 @@ def cpu_matvec_baselines(gpu, keeps, seconds, env):
             continue
         dW, stride = keeps[name]
         rb = FA.row_bytes(t, K) * M
-        n_s = max(8, (200 << 20) // rb + 1)
+        n_s = 512
         mats = [gpu.download(dW.offset(m * stride), np.uint8, rb) for m in range(n_s)]
         x = O.synth_f32(xseed, 0, 1.0, K)
         y = np.empty(M, np.float32)
