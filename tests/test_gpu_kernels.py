@@ -588,9 +588,11 @@ def _prefill_host_layer(shape, layer, seed, zipf, gvec=None, experts_needed=None
 # the fp32 SwiGLU activation to the bf16 MFMA as hi + lo bf16 terms, which
 # carry it to within 2^-18 relative, so outputs differ from the oracle's
 # (fp32 activation, fp64 sums) by ~2^-18 of sum |w*a| per output: inf_rel
-# ~1e-6, i.e. parity_err (1e-3*||ref|| floor) up to ~1e-3. Bar: parity_err
-# <= 1e-2 and inf_rel <= 1e-5 (the decode path keeps the 1e-3 parity bar).
-PF_PARITY, PF_INF = 1e-2, 1e-5
+# ~1e-6, i.e. parity_err (1e-3*||ref|| floor) of a few 1e-3 (measured worst
+# token: 2.9e-3 at T = 200, 1.4e-3 at config 5; the fp32 routing weights of
+# the oracle add ~1e-6 of their own). Bar: 2x the measured worst, parity_err
+# <= 6e-3, and inf_rel <= 1e-5 (the decode path keeps the 1e-3 parity bar).
+PF_PARITY, PF_INF = 6e-3, 1e-5
 
 
 def pf_bf16_mask(shape):
