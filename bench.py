@@ -60,9 +60,9 @@ def rotation(gpu, t, M, K, wseed, xseed, n_mats, steps, warmup):
     for _ in range(steps):
         gpu.matvec_batched(t, dW, stride, n_mats, dx, 0, dy, M, M, K)
     ms = gpu.timer_stop() / steps
-    # per-launch spread, from separately timed launches after the timed region
+    # per-launch spread, from >= 100 separately timed launches after the timed region
     each = []
-    for _ in range(max(steps, 10)):
+    for _ in range(max(steps, 100)):
         gpu.timer_start()
         gpu.matvec_batched(t, dW, stride, n_mats, dx, 0, dy, M, M, K)
         each.append(gpu.timer_stop())
