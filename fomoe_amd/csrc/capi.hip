@@ -595,7 +595,9 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
     HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * P * F));
     HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
-    HIPC(ensure(ctx->pf_xsum, ctx->pf_xsum_cap, sizeof(float) * (size_t)T * (H / 32)));
+    // xsum [T x H/32] fp32, then x16 [T x H] fp16, then xexp [T] int32
+    const size_t xs_bytes = sizeof(float) * (size_t)T * (H / 32), x16_bytes = 2 * (size_t)T * H;
+    HIPC(ensure(ctx->pf_xsum, ctx->pf_xsum_cap, xs_bytes + x16_bytes + sizeof(int32_t) * (size_t)T));
     fo::PrefillArgs a{};
     a.E = E; a.k = k; a.H = H; a.F = F;
     a.gate_type = L->gate_type; a.up_type = L->up_type; a.down_type = L->down_type;
@@ -609,6 +611,8 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.pair_tok = ctx->pf_pairtok; a.tiles = ctx->pf_tiles; a.n_tiles = ctx->pf_ntiles;
     a.max_tiles = max_tiles; a.act_hi = ctx->pf_act; a.act_lo = ctx->pf_act + P * F; a.outp = ctx->pf_outp;
     a.xsum = ctx->pf_xsum;
+    a.x16 = (uint16_t *)((uint8_t *)ctx->pf_xsum + xs_bytes);
+    a.xexp = (int32_t *)((uint8_t *)ctx->pf_xsum + xs_bytes + x16_bytes);
     HIPC(fo::launch_prefill(a, ctx->stream));
     ctx->pf_T = T;
     ctx->pf_k = k;

@@ -35,10 +35,12 @@ struct PrefillArgs {
     int32_t *pairpos;            // [T x (k+1)]: pair slot of (token, rank); rank k = shared
     int32_t *pair_tok;           // [P] token of each pair slot, grouped by expert
     int32_t *tiles;              // [max_tiles x 4] {expert (E = shared), first pair, n, 0}
-    int32_t *n_tiles;            // [1]
+    int32_t *n_tiles;            // [3]: tiles, -, work counter of the gate/up kernel
     int max_tiles;
     uint16_t *act_hi, *act_lo;   // [P x F] SwiGLU activation as bf16 hi + lo terms
     float *xsum;                 // [T x H/32] sums of x over 32-value sub-blocks (Q4_K gate/up path)
+    uint16_t *x16;               // [T x H] fp16(x * 2^-xexp[t]) (Q4_K gate/up path)
+    int32_t *xexp;               // [T] per-token power-of-two scale of x16
     float *outp;                 // [P x H] fp32, per-pair down output
 };
 

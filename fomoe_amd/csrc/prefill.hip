@@ -35,6 +35,8 @@
 // (oracle/oracle.c fo_moe_prefill: bf16 weights, fp32 activation).
 #include <float.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "prefill.h"
 #include "topk.h"
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
             tp[0] = tid; tp[1] = off + kPfMT * i; tp[2] = min(kPfMT, cnt - kPfMT * i); tp[3] = 0;
         }
     }
-    if (tid == 1023) *a.n_tiles = toff + nt;
+    if (tid == 1023) { a.n_tiles[0] = toff + nt; a.n_tiles[2] = 0; }   // [2]: k_pf_gateup_f16 work counter
     // pair offsets of each expert for the placement pass
     __shared__ int s_off[1025];
     if (tid <= E) s_off[tid] = off;
@@ -601,6 +603,279 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillAr
     }
 }
 
+// ------------------------------------------------------------ Q4_K gate/up on exact fp16 MFMA operands
+// A Q4_K weight is d * sc_j * q - dmin * m_j (q 4-bit, sc_j / m_j 6-bit
+// per 32-value sub-block j, d / dmin fp16 per super-block). sc_j * q <= 945
+// is an exact fp16 integer, so the B operand of v_mfma_f32_16x16x32_f16 is
+// built as fp16(sc_j * q) (v_perm of the code bytes under 0x64 gives
+// 1024 + q, one v_pk_fma_f16 (1024 + q) * sc - 1024 * sc gives sc * q
+// exactly) and the MFMA accumulates a whole super-block: per output
+// acc += d * D with D = sum_k x_k sc_j q_k, one fma per super-block instead
+// of one scale per 32 values. The min term -sum_j (dmin m_j) S_j (S_j the
+// token's sub-block sums, fp32) runs on v_mfma_f32_16x16x4_f32 into the same
+// accumulator. The token rows (and their sums) enter scaled by a per-token
+// power of two (k_pf_xprep: the row maximum lands in [2^14, 2^15), so the
+// fp16 rows are exact for every value above 2^-28 of the row maximum and off
+// by at most 2^-39 of it below), which the epilogue undoes.
+//
+// Work item = (tile, 128 rows of F); work-group = 8 waves, wave w owns the
+// 16 gate and 16 up rows 16w..16w+15 of the item. K runs in steps of 512
+// values (two super-blocks): per step a wave streams its rows' 288-byte
+// pieces (9 KiB, 1 KiB coalesced loads, the next step's in flight while this
+// one is multiplied) through a wave-private LDS area into MFMA layout, and
+// the whole work-group shares the step's token rows (<= 64 x 512 fp16,
+// swizzled) and sub-block sums, staged with direct global->LDS loads; tiles
+// of <= 32 tokens double-buffer them, larger ones stage after a barrier.
+// Work-groups take items from a counter (reset by k_pf_group) one item
+// ahead, so an item's first weights stream in during the previous one.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+constexpr int kWsWaves = 8;
+constexpr int kWsRows = 16 * kWsWaves;                // F rows per item
+constexpr int kWsKC = 512;                            // K values per step
+constexpr int kWsW = 2 * 16 * 288;                    // one wave's gate + up bytes per step
+constexpr int kWsPieces = kWsW / 1024;                // 9
+constexpr uint32_t kWsA = kPfMT * kWsKC * 2;          // token region: 64 KiB (two 32 KiB buffers or one)
+constexpr uint32_t kWsS = 16 * kPfMT * 4;             // sub-block sums of a step: [16][64] fp32
+constexpr uint32_t kWsLds = kWsA + 2 * kWsS + kWsWaves * kWsW;   // 64 + 8 + 72 KiB
+
+// Token prep for the fp16 path, one work-group per token: s = the power of
+// two that brings max|x| into [2^14, 2^15) (large and tiny rows alike),
+// x16 = fp16(x * 2^-s), the fp32 sums of the bf16 values over 32-value
+// sub-blocks (sequential) times 2^-s, and s.
+__global__ __launch_bounds__(256) void k_pf_xprep(PrefillArgs a) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x, H = a.H;
+    const uint16_t *xr = a.x + (uint64_t)t * H;
+    float m = 0.f;
+    for (int i = tid; i < H; i += 256) m = fmaxf(m, fabsf(bf2f(xr[i])));
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int E = 0;
+    frexpf(m, &E);                                         // 2^(E-1) <= m < 2^E (m finite, nonzero)
+    const int sx = E - 15;
+    uint16_t *x16 = a.x16 + (uint64_t)t * H;
+    for (int i = tid; i < H; i += 256)
+        x16[i] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(bf2f(xr[i]), -sx));
+    const int nsb = H / 32;
+    for (int j = tid; j < nsb; j += 256) {
+        const uint16_t *p = xr + 32 * j;
+        float sum = 0.f;
+        for (int q = 0; q < 32; q++) sum = sum + bf2f(p[q]);
+        a.xsum[(uint64_t)t * nsb + j] = ldexpf(sum, -sx);
+    }
+    if (tid == 0) a.xexp[t] = sx;
+}
+
+// 6-bit (scale, min) of sub-block j from the 12 scale bytes (words y, z, w
+// of a Q4_K header; reference src/quant.c:72-80)
+FO_DEV void q4_scale_min(const uint4 &hdr, int j, uint32_t &sc, uint32_t &mn) {
+    const int jj = j & 3;
+    const uint32_t b0 = (hdr.y >> (8 * jj)) & 0xFFu, b4 = (hdr.z >> (8 * jj)) & 0xFFu, b8 = (hdr.w >> (8 * jj)) & 0xFFu;
+    if (j < 4) { sc = b0 & 63; mn = b4 & 63; }
+    else { sc = (b8 & 0xF) | ((b0 >> 6) << 4); mn = (b8 >> 4) | ((b4 >> 6) << 4); }
+}
+
+// eight codes (bytes of q selected by nibble sh) times sc as exact fp16
+FO_DEV f16x8 q4_codes_f16(uint2 q, int sh, f16x2 sc, f16x2 nsc) {
+    const uint32_t w0 = (q.x >> sh) & 0x0F0F0F0Fu, w1 = (q.y >> sh) & 0x0F0F0F0Fu;
+    const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u)};
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++)   // (1024 + q) sc - 1024 sc, one rounding: exact
+        r[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p[i]), sc, nsc));
+    return __builtin_bit_cast(f16x8, r);
+}
+
+__global__ __launch_bounds__(64 * kWsWaves, 1) void k_pf_gateup_f16(PrefillArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t ws_lds[];
+    __shared__ int s_item[2];
+    __shared__ int s_exp[kPfMT];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, kg = lane >> 4;
+    uint16_t *abase = (uint16_t *)ws_lds;
+    float *sbase = (float *)(ws_lds + kWsA);
+    uint8_t *wb = ws_lds + kWsA + 2 * kWsS + w * kWsW;    // [gate 16 x 288 | up 16 x 288]
+    const int H = a.H, nsb = H / 32, NQ = H / kWsKC, nfg = a.F / kWsRows;
+    const uint32_t rowb = (uint32_t)(H / 256) * 144;
+    const int n_items = *a.n_tiles * nfg;
+    // per-lane byte offsets of the weight pieces of a step (piece i, lane l:
+    // byte o = 1024 i + 16 l of [gate | up] pieces, row (o mod 4608) / 288)
+    uint32_t woff[kWsPieces];
+#pragma unroll
+    for (int i = 0; i < kWsPieces; i++) {
+        const uint32_t o = i * 1024u + lane * 16u, oo = o < 4608u ? o : o - 4608u;
+        woff[i] = (oo / 288) * rowb + oo % 288;
+    }
+    struct Item { int p0, n, fg; const uint8_t *w0; uint32_t up_off; };
+    auto describe = [&](int it) {
+        const int tile = it / nfg, fg = it - tile * nfg;
+        const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
+        const bool shared = tl.x == a.E;
+        const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)tl.x * a.stride;
+        return Item{tl.y, tl.z, fg, blob + (uint64_t)(fg * kWsRows + 16 * w) * rowb,
+                    (uint32_t)(shared ? a.sh_gate_size : a.gate_size)};
+    };
+    uint4 v[kWsPieces];
+    auto issue_w = [&](const Item &t, int q) {
+#pragma unroll
+        for (int i = 0; i < kWsPieces; i++) {   // pieces 0-3 are gate rows, 5-8 up rows, 4 both
+            const bool up = i > 4 || (i == 4 && lane >= 32);
+            v[i] = ld16(t.w0 + (woff[i] + (up ? t.up_off : 0u) + 288u * q));
+        }
+    };
+    if (tid == 0) { s_item[0] = atomicAdd(a.n_tiles + 2, 1); s_item[1] = atomicAdd(a.n_tiles + 2, 1); }
+    __syncthreads();
+    int item = s_item[0], next = s_item[1];
+    if (item >= n_items) return;
+    Item cur = describe(item);
+    issue_w(cur, 0);
+    const f16x2 m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+    for (;;) {
+        const int p0 = cur.p0, n = cur.n, nb = (n + 15) >> 4;
+        const bool dbl = nb <= 2;
+        const int tok = a.pair_tok[p0 + min(lane, n - 1)];    // token of tile row lane
+        if (w == 0) s_exp[lane] = a.xexp[tok];
+        // stage the token rows and sub-block sums of step q into buffer b
+        auto stage = [&](int q, int b) {
+            uint16_t *ab = abase + (dbl ? b * (kWsA / 4) : 0);   // 32 KiB buffers (kWsA / 4 elements)
+            float *sb = sbase + b * (kWsS / 4);
+            for (int m = w; m < 16 * nb; m += kWsWaves) {        // one token row per wave instruction
+                const int c = lane ^ (m & 15);
+                const uint16_t *src = a.x16 + (uint64_t)__builtin_amdgcn_readlane(tok, m) * H + q * kWsKC + 8 * c;
+                __builtin_amdgcn_global_load_lds((const void *)src,
+                                                 (__attribute__((address_space(3))) void *)(ab + m * kWsKC), 16, 0, 0);
+            }
+            for (int j = w; j < 16; j += kWsWaves)               // one sub-block's token sums per instruction
+                __builtin_amdgcn_global_load_lds((const void *)(a.xsum + (uint64_t)tok * nsb + q * 16 + j),
+                                                 (__attribute__((address_space(3))) void *)(sb + j * kPfMT), 4, 0, 0);
+        };
+        Item nx{};
+        if (next < n_items) nx = describe(next);
+        // the item for NB token blocks (a compile-time count: the MFMA
+        // accumulators stay in place)
+        auto run = [&](auto NBC) {
+        constexpr int NB = decltype(NBC)::value;
+        stage(0, 0);
+        f32x4 gA[NB], uA[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) { gA[b] = (f32x4){0.f, 0.f, 0.f, 0.f}; uA[b] = gA[b]; }
+        for (int q = 0; q < NQ; q++) {
+            const int b = dbl ? (q & 1) : 0;
+            // this wave's staging of step q has landed: it was issued before the
+            // step's weights when double-buffered (those may still fly), after
+            // them otherwise and at the first step
+            if (dbl && q > 0) __builtin_amdgcn_s_waitcnt(vmcnt_le(kWsPieces));
+            else __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();                                   // everyone's staging of step q; buffer b ^ 1 free
+            if (dbl && q + 1 < NQ) stage(q + 1, b ^ 1);
+            // this step's weights into the wave's area (one wave's LDS
+            // operations run in order: the previous step's reads are done)
+#pragma unroll
+            for (int i = 0; i < kWsPieces; i++) *(uint4 *)(wb + i * 1024 + lane * 16) = v[i];
+            if (q + 1 < NQ) issue_w(cur, q + 1);
+            else if (next < n_items) issue_w(nx, 0);
+            const uint16_t *ab = abase + (dbl ? b * (kWsA / 4) : 0);
+            const float *sb = sbase + b * (kWsS / 4);
+#pragma unroll
+            for (int sbk = 0; sbk < 2; sbk++) {
+                // one matrix (gate or up) of super-block sbk for all token blocks
+                auto pass = [&](const uint8_t *rw, f32x4 (&acc)[NB]) {
+                    const uint4 hw = *(const uint4 *)rw;
+                    // min-term operand: -dmin * m of sub-block 4h + kg of row col
+                    float bm[2];
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        uint32_t sc, mn;
+                        q4_scale_min(hw, 4 * h + kg, sc, mn);
+                        bm[h] = -h2f(hw.x >> 16) * (float)mn;
+                    }
+                    f32x4 dd[NB];
+#pragma unroll
+                    for (int tb = 0; tb < NB; tb++) dd[tb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const uint2 qw = *(const uint2 *)(rw + 16 + 32 * c + 8 * kg);
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            const int j = 2 * c + h;
+                            uint32_t sc, mn;
+                            q4_scale_min(hw, j, sc, mn);
+                            // sc as an fp16 pair: bits 0x6400 | sc = 1024 + sc, minus 1024
+                            const f16x2 sp = __builtin_bit_cast(f16x2, (sc * 0x10001u) | 0x64006400u) + m1024;
+                            const f16x8 bw = q4_codes_f16(qw, 4 * h, sp, sp * m1024);
+                            const int chunk = 32 * sbk + 4 * j + kg;
+#pragma unroll
+                            for (int tb = 0; tb < NB; tb++) {
+                                const int m = 16 * tb + col;
+                                const f16x8 av = *(const f16x8 *)(ab + m * kWsKC + 8 * (chunk ^ (m & 15)));
+                                dd[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bw, dd[tb], 0, 0, 0);
+                            }
+                        }
+                        // keep the scheduler from hoisting every sub-block's operands
+                        // (the live ranges would exceed the register budget)
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    const float d = h2f(hw.x);
+#pragma unroll
+                    for (int tb = 0; tb < NB; tb++) {
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[tb][i] = fmaf(d, dd[tb][i], acc[tb][i]);
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {   // A: S of token 16 tb + col, sub-block 8 sbk + 4 h + kg
+                            const float sa = sb[(8 * sbk + 4 * h + kg) * kPfMT + 16 * tb + col];
+                            acc[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, bm[h], acc[tb], 0, 0, 0);
+                        }
+                    }
+                };
+                pass(wb + col * 288 + sbk * 144, gA);
+                pass(wb + 4608 + col * 288 + sbk * 144, uA);
+            }
+            if (!dbl && q + 1 < NQ) {
+                __syncthreads();                               // everyone is done with buffer 0
+                stage(q + 1, 0);
+            }
+        }
+        // SwiGLU: lane holds tokens 16 tb + 4 kg + i of row 16 w + col
+        const int row = cur.fg * kWsRows + 16 * w + col;
+#pragma unroll
+        for (int tb = 0; tb < NB; tb++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * tb + 4 * kg + i;
+                if (m < n) {
+                    const int sx = s_exp[m];
+                    const float g = ldexpf(gA[tb][i], sx), u = ldexpf(uA[tb][i], sx);
+                    const float val = (g / (1.0f + expf(-g))) * u;
+                    const __bf16 hi = (__bf16)val;
+                    const __bf16 lo = (__bf16)(val - (float)hi);
+                    const uint64_t o = (uint64_t)(p0 + m) * a.F + row;
+                    a.act_hi[o] = __builtin_bit_cast(uint16_t, hi);
+                    a.act_lo[o] = __builtin_bit_cast(uint16_t, lo);
+                }
+            }
+        }
+        };
+        switch (nb) {
+            case 1: run(std::integral_constant<int, 1>{}); break;
+            case 2: run(std::integral_constant<int, 2>{}); break;
+            case 3: run(std::integral_constant<int, 3>{}); break;
+            default: run(std::integral_constant<int, 4>{}); break;
+        }
+        if (next >= n_items) break;
+        __syncthreads();                                       // s_item, s_exp and the buffers are free
+        if (tid == 0) s_item[0] = atomicAdd(a.n_tiles + 2, 1);
+        __syncthreads();
+        item = next;
+        next = s_item[0];
+        cur = nx;
+    }
+}
+
 constexpr int kPfDownWaves = 8;                   // 8 waves x 32 rows = 256 weight rows per work-group
 
 template <int DT>
@@ -742,7 +1017,8 @@ static hipError_t launch_gateup_t(const PrefillArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
+hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
+    PrefillArgs a = a_;
     const bool okt = (a.gate_type == GGML_TYPE_Q4_K || a.gate_type == GGML_TYPE_Q6_K) &&
                      (a.up_type == GGML_TYPE_Q4_K || a.up_type == GGML_TYPE_Q6_K) &&
                      (a.down_type == GGML_TYPE_Q4_K || a.down_type == GGML_TYPE_Q6_K);
@@ -765,8 +1041,22 @@ hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s) {
     if (err != hipSuccess) return err;
     if (a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K) {   // scale-after path
         const int64_t n = (int64_t)a.T * (a.H / 32);
-        k_pf_xsum<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(a);
-        k_pf_gateup_q4<<<pf_grid(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
+        if (a.F % kWsRows == 0 && a.H % kWsKC == 0) {   // fp16-exact weight-streaming kernel
+            k_pf_xprep<<<a.T, 256, 0, s>>>(a);
+            static bool ws_attr = false;   // above the 64 KiB default of dynamic LDS
+            if (!ws_attr) {
+                hipError_t e = hipFuncSetAttribute((const void *)k_pf_gateup_f16,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWsLds);
+                if (e != hipSuccess) return e;
+                ws_attr = true;
+            }
+            int dev = 0, n_cu = 256;
+            if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+            k_pf_gateup_f16<<<n_cu, 64 * kWsWaves, kWsLds, s>>>(a);
+        } else {
+            k_pf_xsum<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(a);
+            k_pf_gateup_q4<<<pf_grid(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
+        }
         err = hipGetLastError();
     }
 #define FO_GU(G, U) if (a.gate_type == G && a.up_type == U) err = launch_gateup_t<G, U>(a, s);

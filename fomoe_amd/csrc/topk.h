@@ -8,16 +8,25 @@
 
 namespace fo {
 
-// Top-k of E logits (<= 1024) with ties to the lowest index — the order of
-// reference src/tensor.c:226-252 applied to softmax(logits), which is
-// monotone — and the renormalised weights exp(l_i - l_max) / sum over the
-// selection (= softmax then renormalise, reference src/inference.c:488-502).
+// Top-k of E logits (<= 1024) as the reference selects them: over the fp32
+// probabilities p_i = expf(l_i - l_max) * (1 / sum) (reference
+// src/tensor.c:186-200), largest first, ties to the lowest index
+// (src/tensor.c:226-252), with the selected p renormalised
+// (src/inference.c:496-502). p is monotone in l, so the selection runs on the
+// logits and the weights are exp(l_i - l_1) / sum over the selection (the
+// same quantity), unless the last selected logit lies more than kSatGap below
+// the first: then p of the selection or of its rivals can underflow, distinct
+// logits can share p = 0 and the reference's ties apply, so the selection
+// runs again on p itself and the weights renormalise p as the reference does.
 // One wave: k rounds of "largest (value, lowest index)" over its lanes; the
 // results go to LDS s_ids[k], s_w[k] (visible after the caller's barrier).
 // Each round costs ~500 cycles of dependent VALU/SGPR latency, so the whole
 // selection is ~2 us of single-wave latency; splitting it over four waves
 // measured slower (the merge round-trip through LDS costs more than it saves).
 constexpr int kMaxE = 1024, kMaxK = 16;
+// exp(-80) / 1024 is still a normal float: above this gap p of every
+// selected expert is positive and normal and no unselected one can tie with it
+constexpr float kSatGap = 80.f;
 
 // One round of "take the largest (value, lowest index)" over the wave: lb/li
 // are this lane's best; returns the winner's value and index (uniform).
@@ -57,8 +66,49 @@ FO_DEV void wave_logits(const float *__restrict__ logits, int E, float (&v)[NV])
     }
 }
 
-template <int NV>  // logits per lane: E <= 64*NV; v from wave_logits (consumed)
-FO_DEV void wave_topk_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w) {
+// Logits (from wave_logits) to softmax probabilities in place, -1 past E
+// (below every probability); NaN logits drop out of the max.
+template <int NV>
+FO_DEV void wave_probs(float (&v)[NV], int E) {
+    const int lane = threadIdx.x & 63;
+    float mx = -FLT_MAX;
+#pragma unroll
+    for (int j = 0; j < NV; j++) mx = fmaxf(mx, v[j]);
+    mx = wave_max(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        v[j] = 64 * j + lane < E ? expf(v[j] - mx) : 0.f;
+        sum += v[j];
+    }
+    const float inv = 1.0f / group_sum<kWave>(sum);
+#pragma unroll
+    for (int j = 0; j < NV; j++) v[j] = 64 * j + lane < E ? v[j] * inv : -1.f;
+}
+
+// Weight of the selection held by lanes 0..k-1 (value v). Probabilities:
+// v * (1 / their sum in rank order) when the sum is positive, else v.
+// Logits: exp(v - v_0) / the sum of those.
+FO_DEV float select_weight(float v, int k, bool prob) {
+    if (prob) {
+        float s = 0.f;
+        for (int r = 0; r < k; r++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
+        return s > 0.f ? v * (1.0f / s) : v;
+    }
+    const int lane = threadIdx.x & 63;
+    const float m0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+    const float e = lane < k ? expf(v - m0) : 0.f;
+    return e * (1.0f / group_sum<kWave>(e));
+}
+
+// Whether a logit selection from `first` down to `last` needs no rerun on p
+// (false for non-finite values as well).
+FO_DEV bool logit_selection_exact(float first, float last) { return last - first > -kSatGap; }
+
+// Selection of k over v (logits, or probabilities when prob; E <= 64*NV;
+// consumed); returns false when a logit selection must rerun on p.
+template <int NV>
+FO_DEV bool wave_topk_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w, bool prob) {
     const int lane = threadIdx.x & 63;
     float my_v = -FLT_MAX;   // lane kk keeps selection kk (no indexed private arrays:
     int my_i = 0;            // those would put the kernel on scratch, which throttles residency)
@@ -79,17 +129,22 @@ FO_DEV void wave_topk_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w) {
                 if (j == (idx >> 6)) v[j] = -FLT_MAX;
         }
     }
-    const float m0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(my_v)));
-    const float e = lane < k ? expf(my_v - m0) : 0.f;
-    const float inv = 1.0f / group_sum<kWave>(e);
-    if (lane < k) { s_ids[lane] = my_i; if (s_w) s_w[lane] = e * inv; }
+    const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
+    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), k - 1));
+    if (!prob && !logit_selection_exact(first, last)) return false;
+    const float wv = s_w ? select_weight(my_v, k, prob) : 0.f;
+    if (lane < k) { s_ids[lane] = my_i; if (s_w) s_w[lane] = wv; }
+    return true;
 }
 
 template <int NV>
 FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *s_ids, float *s_w) {
     float v[NV];
     wave_logits<NV>(logits, E, v);
-    wave_topk_v<NV>(v, E, k, s_ids, s_w);
+    if (wave_topk_v<NV>(v, E, k, s_ids, s_w, false)) return;
+    wave_logits<NV>(logits, E, v);
+    wave_probs<NV>(v, E);
+    wave_topk_v<NV>(v, E, k, s_ids, s_w, true);
 }
 
 // Same selection through a threshold: the 64 lane maxima are sorted across
@@ -110,8 +165,8 @@ template <int CTRL>
 FO_DEV int dpp_keep_i(int v) { return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false); }
 
 template <int NV>
-FO_DEV void wave_topk_thr_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w, float2 *s_cand,
-                            float *s_val) {
+FO_DEV bool wave_topk_thr_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w, float2 *s_cand,
+                            float *s_val, bool prob) {
     const int lane = threadIdx.x & 63, r = lane & 15;
     float mx = -FLT_MAX;
 #pragma unroll
@@ -152,10 +207,7 @@ FO_DEV void wave_topk_thr_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w
             }
         }
     }
-    if (!ok) {
-        wave_topk_v<NV>(v, E, k, s_ids, s_w);
-        return;
-    }
+    if (!ok) return wave_topk_v<NV>(v, E, k, s_ids, s_w, prob);
     // lane l < n ranks candidate l against entries l+1 .. l+n-1 of the doubled list
     const float2 c = lane < 2 * n ? s_cand[lane] : make_float2(-FLT_MAX, __int_as_float(0x7FFFFFFF));
     const int ci = __float_as_int(c.y);
@@ -170,13 +222,12 @@ FO_DEV void wave_topk_thr_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w
         s_ids[rank] = (ci >= 0 && ci < E) ? ci : 0;
         s_val[rank] = c.x;
     }
+    if (!prob && !logit_selection_exact(s_val[0], s_val[k - 1])) return false;
     if (s_w) {
-        const float my_v = lane < k ? s_val[lane] : -FLT_MAX;
-        const float m0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(my_v)));
-        const float e = lane < k ? expf(my_v - m0) : 0.f;
-        const float inv = 1.0f / group_sum<kWave>(e);
-        if (lane < k) s_w[lane] = e * inv;
+        const float wv = select_weight(lane < k ? s_val[lane] : 0.f, k, prob);
+        if (lane < k) s_w[lane] = wv;
     }
+    return true;
 }
 
 template <int NV>
@@ -184,7 +235,10 @@ FO_DEV void wave_topk_thr(const float *__restrict__ logits, int E, int k, int *s
                           float2 *s_cand, float *s_val) {
     float v[NV];
     wave_logits<NV>(logits, E, v);
-    wave_topk_thr_v<NV>(v, E, k, s_ids, s_w, s_cand, s_val);
+    if (wave_topk_thr_v<NV>(v, E, k, s_ids, s_w, s_cand, s_val, false)) return;
+    wave_logits<NV>(logits, E, v);
+    wave_probs<NV>(v, E);
+    wave_topk_thr_v<NV>(v, E, k, s_ids, s_w, s_cand, s_val, true);
 }
 
 }  // namespace fo

@@ -302,16 +302,18 @@ def test_moe_layer_norm_residual_gate(gpu):
     assert np.array_equal(got, (x + ffn).astype(np.float32))
 
 
-@pytest.mark.parametrize("case", ["ties", "ties40", "E300_k15", "k3"])
+@pytest.mark.parametrize("case", ["ties", "ties40", "E300_k15", "k3", "saturated", "saturated_k3"])
 def test_moe_layer_topk_ties_and_fallback(gpu, case):
     """Expert selection inside the layer (one or two arg-max rounds per
     work-group, the threshold ranking beyond that, its fallback when more than
     32 values tie at the threshold) against the reference order: equal logits
     (duplicated router rows give bit-identical logits) resolve to the lowest
-    index (reference src/tensor.c:226-252)."""
+    index (reference src/tensor.c:226-252). Saturated: logits hundreds apart,
+    so softmax underflows the tail to p = 0 and distinct logits tie in p,
+    resolved by the lowest index as the reference's top_k over p does."""
     from fomoe_amd import synthetic as S
     from test_oracle import moe_desc
-    E, k = (300, 15) if case == "E300_k15" else (512, 3 if case == "k3" else 10)
+    E, k = (300, 15) if case == "E300_k15" else (512, 3 if case.endswith("k3") else 10)
     H, F = 512, 512
     say(f"layer top-k {case}: E={E} k={k}")
     shape = S.LayerShape(n_embd=H, inter=F, n_experts=E, k=k, shared=True)
@@ -321,6 +323,8 @@ def test_moe_layer_topk_ties_and_fallback(gpu, case):
     order = np.argsort(-O.mat_vec(O.F32, router.reshape(-1), x, E, H), kind="stable")
     if case == "ties40":     # 40 equal top logits: more ties at the threshold than lanes allow
         router[100:140] = 3 * router[order[0]]
+    elif case.startswith("saturated"):   # logits ~ N(0, 450): p = 0 beyond the first few
+        router *= 1000.0
     else:                    # groups of equal logits around the top and the selection boundary
         for rank, dup in ((0, (1, 200)), (2, (3, 250, 299)), (k - 1, (0, 41, 42, 43))):
             src = router[order[rank]].copy()
@@ -344,7 +348,11 @@ def test_moe_layer_topk_ties_and_fallback(gpu, case):
     d.expert_stride = shape.stride
     want, oid, ow = O.moe_layer(d, x, 0)
     assert np.array_equal(oid, sel)
-    assert len(set(logits[oid].tolist())) < k    # ties are in play
+    if case.startswith("saturated"):   # ties in p between distinct logits
+        probs = O.softmax(logits)
+        assert len(set(probs[oid].tolist())) < k and len(set(logits[oid].tolist())) == k
+    else:
+        assert len(set(logits[oid].tolist())) < k    # ties are in play
     assert np.array_equal(ids, oid), (ids, oid)
     assert inf_rel(w, ow) < 1e-6
     say(f"  inf_rel {inf_rel(got, want):.3e}")
@@ -602,15 +610,20 @@ def pf_bf16_mask(shape):
     return (0 if q4 else 3) | 4
 
 
-@pytest.mark.parametrize("T,shared,gate_vec,resid", [(200, True, True, True), (1, True, False, False),
-                                                      (33, False, False, True)])
-def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid):
+@pytest.mark.parametrize("T,shared,gate_vec,resid,H", [(200, True, True, True, 512), (1, True, False, False, 512),
+                                                        (33, False, False, True, 512),
+                                                        (40, True, False, False, 2048),
+                                                        (300, True, True, True, 1024),
+                                                        # H not a multiple of 512: the bf16 scale-after
+                                                        # gate/up kernel instead of the fp16 one
+                                                        (50, True, True, False, 768)])
+def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid, H):
     """Grouped bf16-MFMA prefill against the oracle's per-token composition
     (bf16-rounded weights and activations): every token, every output; with
     the residual flag the output is exactly x + ffn."""
     from fomoe_amd import synthetic as S
-    say(f"prefill small T={T} shared={shared} gate_vec={gate_vec} resid={resid}")
-    shape = S.LayerShape(n_embd=512, inter=256, n_experts=16, k=4, shared=shared)
+    say(f"prefill small T={T} shared={shared} gate_vec={gate_vec} resid={resid} H={H}")
+    shape = S.LayerShape(n_embd=H, inter=256, n_experts=16, k=4, shared=shared)
     L = S.build_layer(gpu, shape, 0, seed=21, zipf_s=1.1, norm=False)
     gv = O.synth_f32(22, 0, 0.05, shape.n_embd) if gate_vec else None
     if gate_vec:
@@ -636,6 +649,36 @@ def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid):
     e = max(parity_err(got[t], want[t]) for t in range(T))
     say(f"  parity_err {e:.3e} inf_rel {inf_rel(got, want):.3e}")
     assert e < PF_PARITY and inf_rel(got, want) < PF_INF
+
+
+def test_prefill_token_scales(gpu):
+    """Tokens whose magnitudes span 2^-40 .. 2^30 (one power of two per token,
+    some rows zero): the fp16 gate/up path scales each token row by its own
+    power of two, so every token keeps the oracle's relative accuracy."""
+    from fomoe_amd import synthetic as S
+    T = 36
+    say(f"prefill token scales T={T}")
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=16, k=4, shared=True)
+    L = S.build_layer(gpu, shape, 0, seed=21, zipf_s=1.1, norm=False)
+    H = shape.n_embd
+    base = O.synth_f32(31, 0, 1.0, T * H).reshape(T, H)
+    ex = np.linspace(-40, 30, T).round().astype(np.int32)
+    xf = (base * np.exp2(ex.astype(np.float64))[:, None]).astype(np.float32)
+    xf[5] = 0.0
+    x = O.to_bf16(xf.ravel()).reshape(T, H)
+    dx = gpu.upload(x)
+    dout = gpu.alloc(4 * T * H)
+    gpu.moe_prefill(L.desc, dx, T, dout, 0)
+    got = gpu.download(dout, np.float32, T * H).reshape(T, H)
+    ids, w = gpu.prefill_routing(T, shape.k)
+    d, keep = _prefill_host_layer(shape, 0, 21, True)
+    want, oids, ow = O.moe_prefill(d, x, 0, T, 0, bf16_mask=pf_bf16_mask(shape))
+    assert np.array_equal(ids, oids)
+    assert np.isfinite(got).all()
+    assert not got[5].any() and not want[5].any()
+    errs = [parity_err(got[t], want[t]) for t in range(T) if t != 5]
+    say(f"  worst parity_err {max(errs):.3e} (token scales 2^{ex.min()}..2^{ex.max()})")
+    assert max(errs) < PF_PARITY
 
 
 def test_prefill_config5_sampled(gpu):
