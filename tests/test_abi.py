@@ -65,6 +65,49 @@ def test_reference_gpu_h_list_is_complete_and_signatures_agree(tmp_path):
     assert r.returncode == 0, r.stderr
 
 
+@pytest.mark.skipif(not os.path.exists(REF_GPU_H), reason="reference sources absent")
+def test_reference_translation_unit_links_and_runs(tmp_path):
+    """A C program written against the reference's own include/gpu.h (as
+    model.c / inference.c / main.c are) links against libfomoe_gfx950.so with
+    every reference function referenced, and its NULL-context calls return the
+    reference's "not available" results — host-only, no device is touched."""
+    calls = "\n".join(f"    (void)(void *)&{n};" for n in REFERENCE_GPU_H)
+    unit = tmp_path / "ref_unit.c"
+    unit.write_text(f"""#include <stdio.h>
+#include "{REF_GPU_H}"
+int main(void) {{
+{calls}
+    float h[8] = {{0}}, out[8];
+    int fails = 0;
+    fails += gpu_upload_model(NULL, NULL) != -1;
+    fails += gpu_forward(NULL, NULL, 0, 0) != NULL;
+    fails += gpu_seed_vram_cache(NULL, NULL, "x") != -1;
+    fails += gpu_get_expert_freq(NULL) != NULL;
+    fails += gpu_expert_ffn(NULL, h, NULL, NULL, 1, 8, 8, 0, 0, 0, 12, 12, 14, out) != -1;
+    int nl = 7, ne = 7;
+    gpu_get_expert_dims(NULL, &nl, &ne);
+    fails += nl != 0 || ne != 0;
+    gpu_register_buffers(NULL, NULL, 0, 0);
+    gpu_unregister_buffers(NULL, NULL, 0);
+    gpu_set_ram_cache_mb(NULL, 1);
+    gpu_set_vram_cache_mb(NULL, 1);
+    gpu_reset_state(NULL);
+    gpu_enable_expert_freq(NULL);
+    gpu_free(NULL);
+    printf("fails %d\\n", fails);
+    return fails;
+}}
+""")
+    libdir = os.path.dirname(fomoe_amd.LIB_PATH)
+    exe = tmp_path / "ref_unit"
+    r = subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", str(unit), "-o", str(exe), f"-L{libdir}",
+                        "-lfomoe_gfx950", f"-Wl,-rpath,{libdir}", "-Wl,-rpath-link,/opt/rocm/lib"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 def test_reference_lifecycle_stubs_report_not_available():
     """Host-only: the whole-model entry points give the reference's fallback
     answers (no device needed for a NULL context)."""
