@@ -595,9 +595,9 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
     HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * P * F));
     HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
-    // xsum [T x H/32] fp32, then x16 [T x H] fp16, then xexp [T] int32
+    // xsum [T x H/32] fp32, then x16 [T x H] fp16, then xexp [T] int32, then pexp [P] int32
     const size_t xs_bytes = sizeof(float) * (size_t)T * (H / 32), x16_bytes = 2 * (size_t)T * H;
-    HIPC(ensure(ctx->pf_xsum, ctx->pf_xsum_cap, xs_bytes + x16_bytes + sizeof(int32_t) * (size_t)T));
+    HIPC(ensure(ctx->pf_xsum, ctx->pf_xsum_cap, xs_bytes + x16_bytes + sizeof(int32_t) * ((size_t)T + P)));
     fo::PrefillArgs a{};
     a.E = E; a.k = k; a.H = H; a.F = F;
     a.gate_type = L->gate_type; a.up_type = L->up_type; a.down_type = L->down_type;
@@ -613,6 +613,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.xsum = ctx->pf_xsum;
     a.x16 = (uint16_t *)((uint8_t *)ctx->pf_xsum + xs_bytes);
     a.xexp = (int32_t *)((uint8_t *)ctx->pf_xsum + xs_bytes + x16_bytes);
+    a.pexp = a.xexp + T;
     HIPC(fo::launch_prefill(a, ctx->stream));
     ctx->pf_T = T;
     ctx->pf_k = k;

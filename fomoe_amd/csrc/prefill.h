@@ -1,7 +1,8 @@
 // prefill.h — argument block and launchers of the multi-token (prefill) MoE
 // path: fp32 router GEMM, per-token top-k, deterministic grouping of
-// (token, expert) pairs by expert, grouped gate/up and down GEMMs on bf16
-// MFMA with the weights dequantized in registers, and the per-token combine.
+// (token, expert) pairs by expert, grouped gate/up and down GEMMs on fp16 /
+// bf16 MFMA with the weight operands built in registers, and the per-token
+// combine.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -37,11 +38,13 @@ struct PrefillArgs {
     int32_t *tiles;              // [max_tiles x 4] {expert (E = shared), first pair, n, 0}
     int32_t *n_tiles;            // [3]: tiles, -, work counter of the gate/up kernel
     int max_tiles;
-    uint16_t *act_hi, *act_lo;   // [P x F] SwiGLU activation as bf16 hi + lo terms
+    uint16_t *act_hi, *act_lo;   // [P x F] SwiGLU activation as bf16 hi + lo terms (a Q6_K
+                                 // down projection rewrites act_hi as fp16 rows, scale in pexp)
     float *xsum;                 // [T x H/32] sums of x over 32-value sub-blocks (Q4_K gate/up path)
     uint16_t *x16;               // [T x H] fp16(x * 2^-xexp[t]) (Q4_K gate/up path)
     int32_t *xexp;               // [T] per-token power-of-two scale of x16
     float *outp;                 // [P x H] fp32, per-pair down output
+    int32_t *pexp;               // [P] power-of-two scale of the fp16 activation rows (Q6_K down)
 };
 
 // Number of pair slots and an upper bound on the GEMM tiles for T tokens.

@@ -955,6 +955,145 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
             }
         }
 }
+
+// ------------------------------------------------------------ Q6_K down on fp16 operands
+// Activation prep, one work-group per pair row: v = hi + lo (the fp32 SwiGLU
+// value as the gate/up kernels store it, exactly), s = the power of two that
+// brings max|v| into [2^14, 2^15), and the row is rewritten in place (over the
+// hi plane) as fp16(v * 2^-s); s goes to pexp.
+__global__ __launch_bounds__(256) void k_pf_actprep(PrefillArgs a) {
+    __shared__ float red[4];
+    const int p = blockIdx.x, tid = threadIdx.x, F = a.F;
+    uint16_t *hi = a.act_hi + (uint64_t)p * F;
+    const uint16_t *lo = a.act_lo + (uint64_t)p * F;
+    constexpr int kMaxPer = 16;                            // F <= 4096
+    float v[kMaxPer];
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxPer; i++) {
+        const int j = tid + 256 * i;
+        v[i] = j < F ? bf2f(hi[j]) + bf2f(lo[j]) : 0.f;
+        m = fmaxf(m, fabsf(v[i]));
+    }
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();                                       // every read of the row is done
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int E = 0;
+    frexpf(m, &E);
+    const int sx = E - 15;
+#pragma unroll
+    for (int i = 0; i < kMaxPer; i++) {
+        const int j = tid + 256 * i;
+        if (j < F) hi[j] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(v[i], -sx));
+    }
+    if (tid == 0) a.pexp[p] = sx;
+}
+
+// The Q6_K down projection with B = fp16(q - 32) * fp16(d * sc) (one v_perm,
+// one v_pk_add_f16 and one v_pk_mul_f16 per two codes; both roundings are
+// nearest-even, 2^-11 relative at most) against the fp16 activation rows of
+// k_pf_actprep, one MFMA per operand; the epilogue applies the pair's 2^s.
+// One activation plane halves the LDS of k_pf_down (64 KiB for two buffers),
+// so two work-groups share a CU.
+__global__ __launch_bounds__(kPfDownWaves * 64, 4) void k_pf_down16(PrefillArgs a) {
+    using D = PfDec<GGML_TYPE_Q6_K>;
+    extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x tile
+    int tile, rbk;
+    pf_tile_of(a.H / (32 * kPfDownWaves), tile, rbk);
+    if (tile >= *a.n_tiles) return;
+    const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
+    const int e = tl.x, p0 = tl.y, n = tl.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
+    const bool shared = e == a.E;
+    const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
+    const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
+    const int row = rbk * (32 * kPfDownWaves) + 32 * wave + col;   // rows row, row + 16
+    const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
+    const uint8_t *drow = blob + down_off + (uint64_t)row * db, *drow1 = drow + 16 * db;
+    const int nb = (n + 15) >> 4, NK = a.F / 256;
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
+    auto stage = [&](int kb) {
+        uint16_t *buf = d16s + (kb & 1) * kPfTile;
+        for (int q = wave; q < nb * 8; q += kPfDownWaves) {
+            const int m = 2 * q + (lane >> 5), cs = lane & 31;
+            const int c = cs ^ (m & 15);
+            const uint16_t *src = a.act_hi + (uint64_t)(p0 + (m < n ? m : 0)) * a.F + kb * 256 + 8 * c;
+            __builtin_amdgcn_global_load_lds((const void *)src,
+                                             (__attribute__((address_space(3))) void *)(buf + q * 512), 16, 0, 0);
+        }
+    };
+    // fp16 operand of chunk ch (values 128n + 32t + 8kg .. +7, scale group
+    // 8n + 2t + kg/2) of one super-block
+    const f16x2 m1056 = {(_Float16)-1056.f, (_Float16)-1056.f};
+    auto dec = [&](const D::Sb &sb, int ch) {
+        const int nn = ch >> 2, t = ch & 3;
+        const uint2 l = sb.ql[2 * nn + (t & 1)];
+        const uint2 h = sb.qh[nn];
+        const int ls = 4 * (t >> 1), hs = 2 * t;
+        const uint32_t c0 = ((l.x >> ls) & 0x0F0F0F0Fu) | (((h.x >> hs) & 0x03030303u) << 4);
+        const uint32_t c1 = ((l.y >> ls) & 0x0F0F0F0Fu) | (((h.y >> hs) & 0x03030303u) << 4);
+        const int si = 8 * nn + 2 * t + (kg >> 1);
+        const uint32_t scw = si < 4 ? sb.sc.x : si < 8 ? sb.sc.y : si < 12 ? sb.sc.z : sb.sc.w;
+        const int scv = (int)(int8_t)((scw >> (8 * (si & 3))) & 0xFFu);
+        const _Float16 dsc = (_Float16)(h2f(sb.d) * (float)scv);   // exact product, one rounding
+        const f16x2 ds2 = {dsc, dsc};
+        const uint32_t pw[4] = {__builtin_amdgcn_perm(0x64646464u, c0, 0x04010400u),
+                                __builtin_amdgcn_perm(0x64646464u, c0, 0x04030402u),
+                                __builtin_amdgcn_perm(0x64646464u, c1, 0x04010400u),
+                                __builtin_amdgcn_perm(0x64646464u, c1, 0x04030402u)};
+        u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; i++)   // (1024 + q) - 1056 = q - 32 exactly, then one rounding
+            r[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, pw[i]) + m1056) * ds2);
+        return __builtin_bit_cast(f16x8, r);
+    };
+    stage(0);
+    auto s0_next = D::load(drow, kg);
+    auto s1_next = D::load(drow1, kg);
+    for (int kb = 0; kb < NK; kb++) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        const auto s0 = s0_next;
+        const auto s1 = s1_next;
+        if (kb + 1 < NK) {
+            stage(kb + 1);
+            s0_next = D::load(drow + (uint64_t)(kb + 1) * D::BLOCK, kg);
+            s1_next = D::load(drow1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
+        }
+        const uint16_t *xh = d16s + (kb & 1) * kPfTile;
+#pragma unroll
+        for (int ch = 0; ch < 8; ch++) {
+            const f16x8 b0 = dec(s0, ch), b1 = dec(s1, ch);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (b < nb) {
+                    const f16x8 av = *(const f16x8 *)(xh + pf_swz(16 * b + col, 4 * ch + kg));
+                    acc[0][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[0][b], 0, 0, 0);
+                    acc[1][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[1][b], 0, 0, 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (b >= nb) break;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * b + 4 * kg + i;
+            if (m < n) {
+                const int sx = a.pexp[p0 + m];
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+                    a.outp[(uint64_t)(p0 + m) * a.H + row + 16 * h] = ldexpf(acc[h][b][i], sx);
+            }
+        }
+    }
+}
 #pragma clang fp contract(on)
 
 // ============================================================ P6 combine
@@ -1077,7 +1216,18 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             if (e2 != hipSuccess) return e2;
             down_attr = true;
         }
-        if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
+        if (a.down_type == GGML_TYPE_Q6_K && a.F <= 4096) {   // fp16 operands, one activation plane
+            const size_t lds16 = 2 * (size_t)kPfTile * sizeof(uint16_t);   // 64 KiB
+            static bool d16_attr = false;
+            if (!d16_attr) {
+                hipError_t e = hipFuncSetAttribute((const void *)k_pf_down16,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds16);
+                if (e != hipSuccess) return e;
+                d16_attr = true;
+            }
+            k_pf_actprep<<<prefill_pairs(a.T, a.k, a.shared != nullptr), 256, 0, s>>>(a);
+            k_pf_down16<<<grid, kPfDownWaves * 64, lds16, s>>>(a);
+        } else if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
         else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
     }
     k_pf_combine<<<a.T, 256, 0, s>>>(a);

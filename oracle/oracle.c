@@ -540,19 +540,54 @@ void fo_fp32_to_bf16_n(const float *x, uint16_t *y, int64_t n) {
     for (int64_t i = 0; i < n; i++) y[i] = fo_fp32_to_bf16(x[i]);
 }
 
+static float f16_round(float v) { return fo_fp16_to_fp32(fo_fp32_to_fp16(v)); }
+
+/* A Q6_K row as the fp16 operands of the GPU prefill's down projection:
+ * fp16(q - 32) * fp16(d * sc) rounded to fp16 (both roundings nearest-even;
+ * d * sc and the product are exact in fp32 before rounding). Value order
+ * and scales as deq_q6_K. */
+static void deq_q6_K_f16ops(const block_q6_K *x, float *y, int64_t nb) {
+    for (int64_t i = 0; i < nb; i++, y += QK_K) {
+        const float d = fo_fp16_to_fp32(x[i].d);
+        for (int e = 0; e < QK_K; e++)
+            y[e] = f16_round((float)q6_code(&x[i], e) * f16_round(d * (float)x[i].scales[e >> 4]));
+    }
+}
+
 /* rows x cols matrix of `type` dequantized exactly, then rounded to bf16
- * when `round` is set */
+ * when `round` is 1; round 2 (Q6_K only): the fp16 operands above */
 static float *deq_bf16(const uint8_t *w, int type, int rows, int cols, int round) {
     float *m = (float *)malloc(sizeof(float) * (size_t)rows * cols);
     const uint64_t rb = fomoe_row_bytes(type, cols);
 #pragma omp parallel for if (rows > 64)
     for (int r = 0; r < rows; r++) {
         float *y = m + (size_t)r * cols;
+        if (round == 2 && type == GGML_TYPE_Q6_K) {
+            deq_q6_K_f16ops((const block_q6_K *)(w + (uint64_t)r * rb), y, cols / QK_K);
+            continue;
+        }
         fo_dequantize_row(type, w + (uint64_t)r * rb, y, cols);
         if (round)
             for (int c = 0; c < cols; c++) y[c] = fo_bf16_to_fp32(fo_fp32_to_bf16(y[c]));
     }
     return m;
+}
+
+/* The activation row as the fp16 down path carries it: v = hi + lo of its
+ * bf16 split, scaled by the power of two 2^-s that brings max|v| into
+ * [2^14, 2^15), rounded to fp16; returns s (values stay scaled). */
+static int act_f16(float *g, int n) {
+    float m = 0.0f;
+    for (int i = 0; i < n; i++) {
+        const float hi = fo_bf16_to_fp32(fo_fp32_to_bf16(g[i]));
+        g[i] = hi + fo_bf16_to_fp32(fo_fp32_to_bf16(g[i] - hi));
+        m = fmaxf(m, fabsf(g[i]));
+    }
+    int e = 0;
+    frexpf(m, &e);
+    const int s = e - 15;
+    for (int i = 0; i < n; i++) g[i] = f16_round(ldexpf(g[i], -s));
+    return s;
 }
 
 static void matvec_f64(float *out, const float *m, const float *v, int rows, int cols) {
@@ -565,20 +600,26 @@ static void matvec_f64(float *out, const float *m, const float *v, int rows, int
     }
 }
 
-/* bf16_mask: bit 0 gate, bit 1 up, bit 2 down weights rounded to bf16 */
+/* bf16_mask: bit 0 gate, bit 1 up, bit 2 down weights rounded to bf16;
+ * bit 3: a Q6_K down projection on fp16 operands (deq_q6_K_f16ops weights,
+ * act_f16 activation) instead */
 static void expert_ffn_bf16(const uint8_t *blob, const fo_moe_desc *L, uint64_t gs, uint64_t us,
                             const float *x, float *out, int bf16_mask) {
     const int H = L->n_embd, F = L->inter;
     float *g = (float *)malloc(sizeof(float) * (size_t)F * 2), *u = g + F;
-    float *wg = deq_bf16(blob, L->gate_type, F, H, bf16_mask & 1);
+    float *wg = deq_bf16(blob, L->gate_type, F, H, (bf16_mask & 1) ? 1 : 0);
     matvec_f64(g, wg, x, F, H);
     free(wg);
-    float *wu = deq_bf16(blob + gs, L->up_type, F, H, bf16_mask & 2);
+    float *wu = deq_bf16(blob + gs, L->up_type, F, H, (bf16_mask & 2) ? 1 : 0);
     matvec_f64(u, wu, x, F, H);
     free(wu);
     for (int i = 0; i < F; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
-    float *wd = deq_bf16(blob + gs + us, L->down_type, H, F, bf16_mask & 4);
+    const int f16 = (bf16_mask & 8) && L->down_type == GGML_TYPE_Q6_K;
+    const int s = f16 ? act_f16(g, F) : 0;
+    float *wd = deq_bf16(blob + gs + us, L->down_type, H, F, f16 ? 2 : (bf16_mask & 4) ? 1 : 0);
     matvec_f64(out, wd, g, H, F);
+    if (f16)
+        for (int r = 0; r < H; r++) out[r] = ldexpf(out[r], s);
     free(wd);
     free(g);
 }

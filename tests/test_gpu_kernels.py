@@ -581,18 +581,20 @@ def _prefill_host_layer(shape, layer, seed, zipf, gvec=None, experts_needed=None
     experts = np.zeros((E + 1) * shape.stride, np.uint8)
     need = range(E + 1) if experts_needed is None else experts_needed
     for e in need:
-        blob = np.concatenate([O.synth_quant(O.Q4_K, seed, S.stream(layer, e, S.GATE), 0.02, F, H),
-                               O.synth_quant(O.Q4_K, seed, S.stream(layer, e, S.UP), 0.02, F, H),
-                               O.synth_quant(O.Q6_K, seed, S.stream(layer, e, S.DOWN), 0.02, H, F)])
+        blob = np.concatenate([O.synth_quant(shape.gate_type, seed, S.stream(layer, e, S.GATE), 0.02, F, H),
+                               O.synth_quant(shape.gate_type, seed, S.stream(layer, e, S.UP), 0.02, F, H),
+                               O.synth_quant(shape.down_type, seed, S.stream(layer, e, S.DOWN), 0.02, H, F)])
         experts[e * shape.stride:e * shape.stride + blob.size] = blob
     bias = O.zipf_bias(seed, S.stream(layer, 0, S.ZIPF), E, 1.1) if zipf else None
     d = moe_desc(E, k, H, F, router, experts, shape.gate_size, shape.down_size,
                  shared_off=E * shape.stride if shape.shared else None, bias=bias, gvec=gvec)
+    d.gate_type, d.up_type, d.down_type = shape.gate_type, shape.gate_type, shape.down_type
     d.expert_stride = shape.stride
     return d, (router, experts, bias, gvec)
 
 
-# Prefill bar. Weights are bf16 on both sides (bit-identical); the GPU feeds
+# Prefill bar on the bf16 path (a Q4_K down projection; gate/up types other
+# than Q4_K). Weights are bf16 on both sides (bit-identical); the GPU feeds
 # the fp32 SwiGLU activation to the bf16 MFMA as hi + lo bf16 terms, which
 # carry it to within 2^-18 relative, so outputs differ from the oracle's
 # (fp32 activation, fp64 sums) by ~2^-18 of sum |w*a| per output: inf_rel
@@ -601,13 +603,47 @@ def _prefill_host_layer(shape, layer, seed, zipf, gvec=None, experts_needed=None
 # the oracle add ~1e-6 of their own). Bar: 2x the measured worst, parity_err
 # <= 6e-3, and inf_rel <= 1e-5 (the decode path keeps the 1e-3 parity bar).
 PF_PARITY, PF_INF = 6e-3, 1e-5
+# The Q6_K down projection runs on fp16 operands (weights fp16(q-32)*fp16(d*sc),
+# the activation as fp16 under its pair row's power of two). The oracle with
+# the same rounding (bf16_mask 8) agrees up to the rounding decisions of the
+# fp16 activation: the GPU's fp32 SwiGLU values differ from the oracle's by
+# ~1e-6, so a few values per row round to the neighbouring fp16 (2^-11 of one
+# term); measured worst token inf_rel 1.1e-4, bar 3e-4. Against the exact
+# computation (exact weights, fp32 activation) the design's own rounding is
+# 5.1-6.2e-4 per token on the oracle (the bf16 down weights it replaced:
+# 2.4-2.7e-3); bar 1.2e-3 per token.
+PF16_INF, PF16_EXACT = 3e-4, 1.2e-3
+
+
+def pf_check(got, d, x, t0, shape, flags=0, tokens=None):
+    """Prefill outputs got[i] of tokens t0 + i against the oracle with the
+    GPU's operand rounding (and, on the fp16 down path, against the exact
+    computation); returns (worst same-rounding error, worst exact error)."""
+    mask = pf_bf16_mask(shape)
+    nt = got.shape[0]
+    want, oids, ow = O.moe_prefill(d, x, t0, nt, flags, bf16_mask=mask)
+    rows = range(nt) if tokens is None else tokens
+    if mask & 8:
+        exact, _, _ = O.moe_prefill(d, x, t0, nt, flags, bf16_mask=mask & 3)
+        e1 = max(inf_rel(got[i], want[i]) for i in rows)
+        e2 = max(inf_rel(got[i], exact[i]) for i in rows)
+        say(f"  fp16 down: worst token inf_rel {e1:.3e} (same rounding), {e2:.3e} (exact)")
+        assert e1 <= PF16_INF and e2 <= PF16_EXACT, (e1, e2)
+    else:
+        e1 = max(parity_err(got[i], want[i]) for i in rows)
+        e2 = inf_rel(got[list(rows)], want[list(rows)])
+        say(f"  bf16 down: worst token parity_err {e1:.3e}, inf_rel {e2:.3e}")
+        assert e1 < PF_PARITY and e2 < PF_INF, (e1, e2)
+    return want, oids, ow
 
 
 def pf_bf16_mask(shape):
-    """Weight matrices the prefill path rounds to bf16: Q4_K gate/up run on the
-    scale-after MFMA path with exact weights, the rest are dequantized to bf16."""
+    """The prefill path's operand rounding, as the oracle's bf16_mask: Q4_K
+    gate/up run with exact weights, other gate/up types are dequantized to
+    bf16; a Q6_K down projection runs on fp16 operands (8), other down types
+    on bf16 weights (4)."""
     q4 = shape.gate_type == O.Q4_K
-    return (0 if q4 else 3) | 4
+    return (0 if q4 else 3) | (8 if shape.down_type == O.Q6_K else 4)
 
 
 @pytest.mark.parametrize("T,shared,gate_vec,resid,H", [(200, True, True, True, 512), (1, True, False, False, 512),
@@ -616,14 +652,18 @@ def pf_bf16_mask(shape):
                                                         (300, True, True, True, 1024),
                                                         # H not a multiple of 512: the bf16 scale-after
                                                         # gate/up kernel instead of the fp16 one
-                                                        (50, True, True, False, 768)])
+                                                        (50, True, True, False, 768),
+                                                        # a Q4_K down projection (bf16 weights)
+                                                        (70, True, False, True, -512)])
 def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid, H):
     """Grouped bf16-MFMA prefill against the oracle's per-token composition
     (bf16-rounded weights and activations): every token, every output; with
     the residual flag the output is exactly x + ffn."""
     from fomoe_amd import synthetic as S
-    say(f"prefill small T={T} shared={shared} gate_vec={gate_vec} resid={resid} H={H}")
-    shape = S.LayerShape(n_embd=H, inter=256, n_experts=16, k=4, shared=shared)
+    down = O.Q4_K if H < 0 else O.Q6_K
+    H = abs(H)
+    say(f"prefill small T={T} shared={shared} gate_vec={gate_vec} resid={resid} H={H} down={down}")
+    shape = S.LayerShape(n_embd=H, inter=256, n_experts=16, k=4, shared=shared, down_type=down)
     L = S.build_layer(gpu, shape, 0, seed=21, zipf_s=1.1, norm=False)
     gv = O.synth_f32(22, 0, 0.05, shape.n_embd) if gate_vec else None
     if gate_vec:
@@ -641,14 +681,11 @@ def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid, H):
         got_r = gpu.download(dout, np.float32, T * shape.n_embd).reshape(T, shape.n_embd)
         assert np.array_equal(got_r, O.bf16_to_f32(x).reshape(T, -1) + got)
     d, keep = _prefill_host_layer(shape, 0, 21, True, gv)
-    want, oids, ow = O.moe_prefill(d, x, 0, T, 0, bf16_mask=pf_bf16_mask(shape))
+    want, oids, ow = pf_check(got, d, x, 0, shape)
     assert np.array_equal(ids, oids)
     assert inf_rel(w[:, :shape.k], ow[:, :shape.k]) < 1e-5
     if shared:
         assert inf_rel(w[:, shape.k], ow[:, shape.k]) < 1e-5
-    e = max(parity_err(got[t], want[t]) for t in range(T))
-    say(f"  parity_err {e:.3e} inf_rel {inf_rel(got, want):.3e}")
-    assert e < PF_PARITY and inf_rel(got, want) < PF_INF
 
 
 def test_prefill_token_scales(gpu):
@@ -672,13 +709,11 @@ def test_prefill_token_scales(gpu):
     got = gpu.download(dout, np.float32, T * H).reshape(T, H)
     ids, w = gpu.prefill_routing(T, shape.k)
     d, keep = _prefill_host_layer(shape, 0, 21, True)
-    want, oids, ow = O.moe_prefill(d, x, 0, T, 0, bf16_mask=pf_bf16_mask(shape))
+    say(f"  token scales 2^{ex.min()}..2^{ex.max()}")
+    want, oids, ow = pf_check(got, d, x, 0, shape, tokens=[t for t in range(T) if t != 5])
     assert np.array_equal(ids, oids)
     assert np.isfinite(got).all()
     assert not got[5].any() and not want[5].any()
-    errs = [parity_err(got[t], want[t]) for t in range(T) if t != 5]
-    say(f"  worst parity_err {max(errs):.3e} (token scales 2^{ex.min()}..2^{ex.max()})")
-    assert max(errs) < PF_PARITY
 
 
 def test_prefill_config5_sampled(gpu):
@@ -686,7 +721,7 @@ def test_prefill_config5_sampled(gpu):
     Zipf(1.1) router bias): routing of every token against the oracle's fp32
     router, outputs of sampled tokens against the oracle, and every sampled
     token against the batch-1 decode layer on the same input (independent
-    GPU path, fp32 weights: agreement to the bf16 rounding scale)."""
+    GPU path, exact weights: agreement to the prefill's operand rounding)."""
     from fomoe_amd import synthetic as S
     say("prefill config5")
     shape = S.LayerShape()
@@ -713,13 +748,13 @@ def test_prefill_config5_sampled(gpu):
     dh = gpu.alloc(4 * H)
     dl = gpu.alloc(4 * H)
     for t in sample:
-        want, oids, _ = O.moe_prefill(d, x, t, 1, 0, bf16_mask=pf_bf16_mask(shape))
+        say(f"  token {t}:")
+        want, oids, _ = pf_check(got[t:t + 1], d, x, t, shape)
         assert np.array_equal(oids[0], ids[t])
-        e = parity_err(got[t], want[0])
         gpu.upload_to(dh, xf[t])
         gpu.moe_layer(L.desc, dh, dl, 0)
         dec = gpu.download(dl, np.float32, H)
-        say(f"  token {t}: parity_err {e:.3e} inf_rel {inf_rel(got[t], want[0]):.3e}  "
-            f"vs decode inf_rel {inf_rel(got[t], dec):.3e}")
-        assert e < PF_PARITY and inf_rel(got[t], want[0]) < PF_INF
-        assert inf_rel(got[t], dec) < 2e-2
+        say(f"  token {t}: vs decode inf_rel {inf_rel(got[t], dec):.3e}")
+        # the decode layer is within ~1e-6 of exact; the prefill's own operand
+        # rounding is <= 6.2e-4 per token (PF16_EXACT's measurement)
+        assert inf_rel(got[t], dec) < 1.5e-3
