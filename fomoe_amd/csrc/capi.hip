@@ -581,23 +581,25 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
                     (L->down_type == GGML_TYPE_Q4_K || L->down_type == GGML_TYPE_Q6_K);
     if (!pt) return fail(ctx, -1, "moe prefill: gate/up/down types must be Q4_K or Q6_K");
     const int T = n_tokens, E = L->n_experts, k = L->k, H = L->n_embd, F = L->inter;
-    if (E > 1023 || E * ((T + 31) / 32) > 16384)
-        return fail(ctx, -1, "moe prefill: n_experts %d x n_tokens %d exceeds the grouping table", E, T);
+    if (E > 1023) return fail(ctx, -1, "moe prefill: n_experts %d > 1023", E);
+    // the grouping table holds n_experts x ceil(tokens/32) words: larger
+    // batches run as consecutive chunks (the results per token are the same)
+    const int Tc = std::min(T, (16384 / E) * 32);
     const bool sh = L->shared != nullptr;
-    const size_t P = (size_t)fo::prefill_pairs(T, k, sh);
-    const int max_tiles = fo::prefill_max_tiles(T, k, E, sh);
-    HIPC(ensure(ctx->pf_logits, ctx->pf_logits_cap, sizeof(float) * (size_t)T * E));
+    const size_t P = (size_t)fo::prefill_pairs(Tc, k, sh);
+    const int max_tiles = fo::prefill_max_tiles(Tc, k, E, sh);
+    HIPC(ensure(ctx->pf_logits, ctx->pf_logits_cap, sizeof(float) * (size_t)Tc * E));
     HIPC(ensure(ctx->pf_ids, ctx->pf_ids_cap, sizeof(int32_t) * (size_t)T * k));
     HIPC(ensure(ctx->pf_w, ctx->pf_w_cap, sizeof(float) * (size_t)T * (k + 1)));
-    HIPC(ensure(ctx->pf_pairpos, ctx->pf_pairpos_cap, sizeof(int32_t) * (size_t)T * (k + 1)));
+    HIPC(ensure(ctx->pf_pairpos, ctx->pf_pairpos_cap, sizeof(int32_t) * (size_t)Tc * (k + 1)));
     HIPC(ensure(ctx->pf_pairtok, ctx->pf_pairtok_cap, sizeof(int32_t) * P));
     HIPC(ensure(ctx->pf_tiles, ctx->pf_tiles_cap, sizeof(int32_t) * 4 * (size_t)max_tiles));
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
     HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * P * F));
     HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
-    // xsum [T x H/32] fp32, then x16 [T x H] fp16, then xexp [T] int32, then pexp [P] int32
-    const size_t xs_bytes = sizeof(float) * (size_t)T * (H / 32), x16_bytes = 2 * (size_t)T * H;
-    HIPC(ensure(ctx->pf_xsum, ctx->pf_xsum_cap, xs_bytes + x16_bytes + sizeof(int32_t) * ((size_t)T + P)));
+    // xsum [Tc x H/32] fp32, then x16 [Tc x H] fp16, then xexp [Tc] int32, then pexp [P] int32
+    const size_t xs_bytes = sizeof(float) * (size_t)Tc * (H / 32), x16_bytes = 2 * (size_t)Tc * H;
+    HIPC(ensure(ctx->pf_xsum, ctx->pf_xsum_cap, xs_bytes + x16_bytes + sizeof(int32_t) * ((size_t)Tc + P)));
     fo::PrefillArgs a{};
     a.E = E; a.k = k; a.H = H; a.F = F;
     a.gate_type = L->gate_type; a.up_type = L->up_type; a.down_type = L->down_type;
@@ -606,15 +608,24 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.gate_size = L->gate_size; a.up_size = L->up_size;
     a.shared = (const uint8_t *)L->shared; a.sh_gate_size = L->shared_gate_size; a.sh_up_size = L->shared_up_size;
     a.shared_gate_vec = L->shared_gate_vec;
-    a.T = T; a.x = d_x; a.out = d_out; a.residual = (flags & GPU_MOE_RESIDUAL) ? 1 : 0;
-    a.logits = ctx->pf_logits; a.ids = ctx->pf_ids; a.w = ctx->pf_w; a.pairpos = ctx->pf_pairpos;
+    a.residual = (flags & GPU_MOE_RESIDUAL) ? 1 : 0;
+    a.logits = ctx->pf_logits; a.pairpos = ctx->pf_pairpos;
     a.pair_tok = ctx->pf_pairtok; a.tiles = ctx->pf_tiles; a.n_tiles = ctx->pf_ntiles;
-    a.max_tiles = max_tiles; a.act_hi = ctx->pf_act; a.act_lo = ctx->pf_act + P * F; a.outp = ctx->pf_outp;
+    a.act_hi = ctx->pf_act; a.act_lo = ctx->pf_act + P * F; a.outp = ctx->pf_outp;
     a.xsum = ctx->pf_xsum;
     a.x16 = (uint16_t *)((uint8_t *)ctx->pf_xsum + xs_bytes);
     a.xexp = (int32_t *)((uint8_t *)ctx->pf_xsum + xs_bytes + x16_bytes);
-    a.pexp = a.xexp + T;
-    HIPC(fo::launch_prefill(a, ctx->stream));
+    a.pexp = a.xexp + Tc;
+    for (int t0 = 0; t0 < T; t0 += Tc) {
+        const int n = std::min(Tc, T - t0);
+        a.T = n;
+        a.max_tiles = fo::prefill_max_tiles(n, k, E, sh);
+        a.x = d_x + (size_t)t0 * H;
+        a.out = d_out + (size_t)t0 * H;
+        a.ids = ctx->pf_ids + (size_t)t0 * k;
+        a.w = ctx->pf_w + (size_t)t0 * (k + 1);
+        HIPC(fo::launch_prefill(a, ctx->stream));
+    }
     ctx->pf_T = T;
     ctx->pf_k = k;
     return 0;

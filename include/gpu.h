@@ -281,12 +281,18 @@ void gpu_gguf_free_moe_layer(gpu_ctx_t *ctx, gpu_moe_layer_t *L);
  * n_embd] bf16, d_out [n_tokens x n_embd] fp32 (= x + ffn with
  * GPU_MOE_RESIDUAL). Per token the semantics of gpu_moe_layer without the
  * norm (fp32 router on the bf16 input, softmax, top-k, renormalise, shared
- * expert); the expert GEMMs are grouped by expert and run on bf16 MFMA with
- * the weights dequantized in registers (round to nearest even of the exact
- * fp32 value) and fp32 accumulation; the SwiGLU activation enters the down
- * projection as two bf16 terms (hi + lo, within 2^-18 of the fp32 value). gate/up/down types Q4_K or Q6_K; n_experts <=
- * 1023 and n_experts * ceil(n_tokens/32) <= 16384. No counterpart in the
- * reference, which decodes prompt tokens one at a time (gpu_forward). */
+ * expert); the expert GEMMs are grouped by expert and run on the matrix cores
+ * with fp32 accumulation. Operands: Q4_K gate/up weights exactly (fp16 sc*q,
+ * the tokens as fp16 under a per-token power of two); a Q6_K down projection
+ * as fp16(q - 32) * fp16(d * sc) against the SwiGLU activation as fp16 under
+ * a per-pair power of two (within ~6e-4 of the exact layer per token); other
+ * types dequantized to bf16 (round to nearest even), with the activation as
+ * two bf16 terms (hi + lo, within 2^-18). gate/up/down types Q4_K or Q6_K;
+ * n_experts <= 1023. A batch larger than the grouping table (n_experts *
+ * ceil(n_tokens/32) > 16384) runs as consecutive chunks of
+ * (16384 / n_experts) * 32 tokens with the same results per token. No
+ * counterpart in the reference, which decodes prompt tokens one at a time
+ * (gpu_forward). */
 int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *layer, const uint16_t *d_x, int n_tokens,
                     float *d_out, int flags);
 /* Routing of the last gpu_moe_prefill (sync): ids [n_tokens x k], weights

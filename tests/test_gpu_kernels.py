@@ -716,6 +716,42 @@ def test_prefill_token_scales(gpu):
     assert not got[5].any() and not want[5].any()
 
 
+def test_prefill_chunked_batch(gpu):
+    """A batch beyond the grouping table (512 experts x 1300 tokens) runs as
+    chunks of 1024 + 276 tokens: bit-identical to the two calls made
+    separately, routing of every token equal to the oracle's, and tokens on
+    both sides of the chunk boundary within the prefill bars."""
+    from fomoe_amd import synthetic as S
+    T, E = 1300, 512
+    say(f"prefill chunked T={T} E={E}")
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=E, k=4, shared=True)
+    H, k = shape.n_embd, shape.k
+    L = S.build_layer(gpu, shape, 0, seed=25, zipf_s=1.1, norm=False)
+    dx = S.tokens_bf16(gpu, T, H, seed=26)
+    dout = gpu.alloc(4 * T * H)
+    gpu.moe_prefill(L.desc, dx, T, dout, FA.MOE_RESIDUAL)
+    got = gpu.download(dout, np.float32, T * H).reshape(T, H)
+    ids, w = gpu.prefill_routing(T, k)
+    # the same tokens as two separate calls
+    d2 = gpu.alloc(4 * T * H)
+    gpu.moe_prefill(L.desc, dx, 1024, d2, FA.MOE_RESIDUAL)
+    gpu.moe_prefill(L.desc, dx.offset(2 * 1024 * H), T - 1024, d2.offset(4 * 1024 * H), FA.MOE_RESIDUAL)
+    sep = gpu.download(d2, np.float32, T * H).reshape(T, H)
+    assert np.array_equal(got.view(np.uint32), sep.view(np.uint32))
+    x = gpu.download(dx, np.uint16, T * H).reshape(T, H)
+    d, keep = _prefill_host_layer(shape, 0, 25, True)
+    router, bias = keep[0], keep[2]
+    xf = O.bf16_to_f32(x).reshape(T, H)
+    for t in range(T):
+        p = O.softmax(O.mat_vec(O.F32, router, xf[t], E, H) + bias)
+        oi, ov = O.top_k(p, k)
+        assert np.array_equal(ids[t], oi), t
+        assert inf_rel(w[t, :k], ov / ov.sum()) < 1e-5
+    for t in (0, 1023, 1024, 1299):
+        say(f"  token {t}:")
+        pf_check(got[t:t + 1], d, x, t, shape, flags=O.MOE_RESIDUAL)
+
+
 def test_prefill_config5_sampled(gpu):
     """Config 5 at full size (512 tokens, 512 experts, top-10, H 4096, F 1024,
     Zipf(1.1) router bias): routing of every token against the oracle's fp32
