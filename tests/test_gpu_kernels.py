@@ -643,7 +643,7 @@ def pf_bf16_mask(shape):
     bf16; a Q6_K down projection runs on fp16 operands (8), other down types
     on bf16 weights (4)."""
     q4 = shape.gate_type == O.Q4_K
-    return (0 if q4 else 3) | (8 if shape.down_type == O.Q6_K else 4)
+    return (0 if q4 else 3) | (8 if shape.down_type == O.Q6_K and shape.inter <= 4096 else 4)
 
 
 @pytest.mark.parametrize("T,shared,gate_vec,resid,H", [(200, True, True, True, 512), (1, True, False, False, 512),
