@@ -444,165 +444,6 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup(PrefillArgs 
     }
 }
 
-// ------------------------------------------------------------ Q4_K gate/up, scale after the MFMA
-// A Q4_K weight is d1*q - m1 with q in 0..15 and (d1, m1) constant over a
-// 32-value sub-block, which is exactly the k-range of one
-// v_mfma_f32_16x16x32_bf16. The codes enter the MFMA as the bf16 values
-// 128 + q (bit pattern 0x4300 | q, one v_perm per two codes, exact), so
-//   sum_k x_k (d1 q_k - m1) = d1 * D' - (128 d1 + m1) * S,
-//   D' = sum_k x_k (128 + q_k) (the MFMA),  S = sum_k x_k (k_pf_xsum),
-// applied per sub-block in fp32. The weights are used exactly (no bf16
-// rounding); the cost is the cancellation of 128 d1 S inside d1 D', a few
-// 2^-24 of 128 sum|x| per sub-block (about 1e-6 of the row's output), against
-// ~7 VALU instructions per weight for dequantizing to bf16 in registers.
-__global__ __launch_bounds__(256) void k_pf_xsum(PrefillArgs a) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // (token, sub-block)
-    const int nsb = a.H / 32;
-    if (i >= (int64_t)a.T * nsb) return;
-    const uint16_t *p = a.x + i * 32;    // token t = i / nsb, sub-block i % nsb: contiguous
-    float s = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint4 v = *(const uint4 *)(p + 8 * c);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) s = (s + bf2f(w[q] & 0xFFFFu)) + bf2f(w[q] >> 16);
-    }
-    a.xsum[i] = s;
-}
-
-// eight codes (two dwords of nibbles selected by sh) as bf16 128 + q
-FO_DEV u32x4 q4_codes_bf16(uint2 q, int sh) {
-    const uint32_t w0 = (q.x >> sh) & 0x0F0F0F0Fu, w1 = (q.y >> sh) & 0x0F0F0F0Fu;
-    u32x4 r;
-    r[0] = __builtin_amdgcn_perm(0x43434343u, w0, 0x04010400u);
-    r[1] = __builtin_amdgcn_perm(0x43434343u, w0, 0x04030402u);
-    r[2] = __builtin_amdgcn_perm(0x43434343u, w1, 0x04010400u);
-    r[3] = __builtin_amdgcn_perm(0x43434343u, w1, 0x04030402u);
-    return r;
-}
-
-// (d1, 128 d1 + m1) of sub-block j from a Q4_K header (reference src/quant.c:72-80)
-FO_DEV float2 q4_sub_scales(const uint4 &hdr, int j) {
-    const uint32_t sc4[3] = {hdr.y, hdr.z, hdr.w};
-    auto byte = [&](int i) -> uint32_t { return (sc4[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
-    uint32_t sc, mn;
-    if (j < 4) { sc = byte(j) & 63; mn = byte(j + 4) & 63; }
-    else {
-        sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
-        mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
-    }
-    const float d1 = h2f(hdr.x) * (float)sc, m1 = h2f(hdr.x >> 16) * (float)mn;
-    return make_float2(d1, fmaf(128.f, d1, m1));
-}
-
-// Same work-group shape and staging as k_pf_gateup; per super-block the
-// tile's S values (8 sub-blocks x 64 tokens) are staged next to the tokens.
-__global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2 * kPfTile];
-    __shared__ __attribute__((aligned(16))) float ss[2][8][kPfMT];
-    int tile, rbk;
-    pf_tile_of(a.F / kPfGateRows, tile, rbk);
-    if (tile >= *a.n_tiles) return;
-    const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
-    const int e = tl.x, p0 = tl.y, n = tl.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
-    const bool shared = e == a.E;
-    const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
-    constexpr int HW = kPfGateWaves / 2;
-    const bool is_up = wave >= HW;
-    const int rl = 32 * (wave % HW) + col;
-    const int row = rbk * kPfGateRows + rl;
-    const int nb = (n + 15) >> 4, NK = a.H / 256, nsb = a.H / 32;
-    const int32_t *toks = a.pair_tok + p0;
-    const int my_tok = toks[min(lane, n - 1)];
-    // S of super-block kb: waves 0..7 each load one sub-block's 64 token sums
-    const float *srow = a.xsum + (uint64_t)my_tok * nsb;
-    auto stage_s = [&](int kb) {
-        if (wave < 8)
-            __builtin_amdgcn_global_load_lds((const void *)(srow + kb * 8 + wave),
-                                             (__attribute__((address_space(3))) void *)&ss[kb & 1][wave][0], 4, 0, 0);
-    };
-    const uint64_t up_off = shared ? a.sh_gate_size : a.gate_size;
-    const uint64_t rb = (uint64_t)NK * 144;
-    const uint8_t *w0 = blob + (is_up ? up_off : 0) + (uint64_t)row * rb, *w1 = w0 + 16 * rb;
-    f32x4 acc[2][4];
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int b = 0; b < 4; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
-    using D = PfDec<GGML_TYPE_Q4_K>;
-    pf_stage_tokens(xs, n, 0, a.x, a.H, my_tok);
-    stage_s(0);
-    auto s0_next = D::load(w0, kg);
-    auto s1_next = D::load(w1, kg);
-    for (int kb = 0; kb < NK; kb++) {
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();                              // tile kb in LDS; buffers of kb-1 free
-        const auto s0 = s0_next;
-        const auto s1 = s1_next;
-        if (kb + 1 < NK) {
-            pf_stage_tokens(xs + ((kb + 1) & 1) * kPfTile, n, (kb + 1) * 256, a.x, a.H, my_tok);
-            stage_s(kb + 1);
-            s0_next = D::load(w0 + (uint64_t)(kb + 1) * D::BLOCK, kg);
-            s1_next = D::load(w1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
-        }
-        const uint16_t *xb = xs + (kb & 1) * kPfTile;
-#pragma unroll
-        for (int ch = 0; ch < 8; ch++) {
-            const bf16x8 b0 = as_bf16x8(q4_codes_bf16(s0.q[ch >> 1], 4 * (ch & 1)));
-            const bf16x8 b1 = as_bf16x8(q4_codes_bf16(s1.q[ch >> 1], 4 * (ch & 1)));
-            const float2 k0 = q4_sub_scales(s0.hdr, ch), k1 = q4_sub_scales(s1.hdr, ch);
-#pragma unroll
-            for (int b = 0; b < 4; b++)
-                if (b < nb) {
-                    const bf16x8 av = *(const bf16x8 *)(xb + pf_swz(16 * b + col, 4 * ch + kg));
-                    const f32x4 z = {0, 0, 0, 0};
-                    const f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b0, z, 0, 0, 0);
-                    const f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, z, 0, 0, 0);
-                    const f32x4 sv = *(const f32x4 *)&ss[kb & 1][ch][16 * b + 4 * kg];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        acc[0][b][i] = fmaf(-k0.y, sv[i], fmaf(k0.x, d0[i], acc[0][b][i]));
-                        acc[1][b][i] = fmaf(-k1.y, sv[i], fmaf(k1.x, d1[i], acc[1][b][i]));
-                    }
-                }
-        }
-    }
-    __syncthreads();                                      // all reads of xs done: reuse it
-    float *ub = (float *)xs;                              // [64 tokens][kPfGateRows] up sums
-    if (is_up) {
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int b = 0; b < 4; b++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) ub[(16 * b + 4 * kg + i) * kPfGateRows + rl + 16 * h] = acc[h][b][i];
-    }
-    __syncthreads();
-    if (!is_up) {
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                if (b >= nb) break;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int m = 16 * b + 4 * kg + i;
-                    if (m < n) {
-                        const float g = acc[h][b][i], u = ub[m * kPfGateRows + rl + 16 * h];
-                        const float v = (g / (1.0f + expf(-g))) * u;
-                        const __bf16 hi = (__bf16)v;
-                        const __bf16 lo = (__bf16)(v - (float)hi);
-                        const uint64_t o = (uint64_t)(p0 + m) * a.F + row + 16 * h;
-                        a.act_hi[o] = __builtin_bit_cast(uint16_t, hi);
-                        a.act_lo[o] = __builtin_bit_cast(uint16_t, lo);
-                    }
-                }
-            }
-    }
-}
-
 // ------------------------------------------------------------ Q4_K gate/up on exact fp16 MFMA operands
 // A Q4_K weight is d * sc_j * q - dmin * m_j (q 4-bit, sc_j / m_j 6-bit
 // per 32-value sub-block j, d / dmin fp16 per super-block). sc_j * q <= 945
@@ -619,25 +460,18 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup_q4(PrefillAr
 // by at most 2^-39 of it below), which the epilogue undoes.
 //
 // Work item = (tile, 128 rows of F); work-group = 8 waves, wave w owns the
-// 16 gate and 16 up rows 16w..16w+15 of the item. K runs in steps of 512
-// values (two super-blocks): per step a wave streams its rows' 288-byte
-// pieces (9 KiB, 1 KiB coalesced loads, the next step's in flight while this
-// one is multiplied) through a wave-private LDS area into MFMA layout, and
-// the whole work-group shares the step's token rows (<= 64 x 512 fp16,
-// swizzled) and sub-block sums, staged with direct global->LDS loads; tiles
-// of <= 32 tokens double-buffer them, larger ones stage after a barrier.
-// Work-groups take items from a counter (reset by k_pf_group) one item
-// ahead, so an item's first weights stream in during the previous one.
+// 16 gate and 16 up rows 16w..16w+15 of the item. K runs in steps of one
+// super-block: per step each wave's rows (2 x 16 x 144 bytes) go from HBM
+// straight into its own LDS area by direct global->LDS loads (1 KiB
+// coalesced pieces, no registers), and the work-group shares the step's token
+// rows (<= 64 x 256 fp16, swizzled) and sub-block sums, staged the same way.
+// 74 KiB of LDS and <= 128 VGPRs: two work-groups share a CU, and the loads
+// of one overlap the arithmetic of the other. Work-groups take items from a
+// counter (reset by k_pf_group).
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 constexpr int kWsWaves = 8;
 constexpr int kWsRows = 16 * kWsWaves;                // F rows per item
-constexpr int kWsKC = 512;                            // K values per step
-constexpr int kWsW = 2 * 16 * 288;                    // one wave's gate + up bytes per step
-constexpr int kWsPieces = kWsW / 1024;                // 9
-constexpr uint32_t kWsA = kPfMT * kWsKC * 2;          // token region: 64 KiB (two 32 KiB buffers or one)
-constexpr uint32_t kWsS = 16 * kPfMT * 4;             // sub-block sums of a step: [16][64] fp32
-constexpr uint32_t kWsLds = kWsA + 2 * kWsS + kWsWaves * kWsW;   // 64 + 8 + 72 KiB
 
 // Token prep for the fp16 path, one work-group per token: s = the power of
 // two that brings max|x| into [2^14, 2^15) (large and tiny rows alike),
@@ -692,102 +526,77 @@ FO_DEV f16x8 q4_codes_f16(uint2 q, int sh, f16x2 sc, f16x2 nsc) {
     return __builtin_bit_cast(f16x8, r);
 }
 
-__global__ __launch_bounds__(64 * kWsWaves, 1) void k_pf_gateup_f16(PrefillArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t ws_lds[];
-    __shared__ int s_item[2];
+constexpr int kGbKC = 256;                            // K values per step
+constexpr uint32_t kGbHalf = 16 * 144;                // a wave's 16 rows of one matrix per step
+constexpr uint32_t kGbW = 2 * kGbHalf;                // 4608 bytes: gate | up
+constexpr int kGbPieces = (kGbW + 1023) / 1024;       // 5 (the last one partial)
+constexpr uint32_t kGbArea = kGbPieces * 1024;        // a wave's LDS area (the partial piece lands whole)
+constexpr uint32_t kGbA = kPfMT * kGbKC * 2;          // 32 KiB token rows
+constexpr uint32_t kGbS = 8 * kPfMT * 4;              // 2 KiB sub-block sums
+constexpr uint32_t kGbLds = kGbA + kGbS + kWsWaves * kGbArea;   // 74 KiB
+
+__global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gb_lds[];
+    __shared__ int s_item;
     __shared__ int s_exp[kPfMT];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, col = lane & 15, kg = lane >> 4;
-    uint16_t *abase = (uint16_t *)ws_lds;
-    float *sbase = (float *)(ws_lds + kWsA);
-    uint8_t *wb = ws_lds + kWsA + 2 * kWsS + w * kWsW;    // [gate 16 x 288 | up 16 x 288]
-    const int H = a.H, nsb = H / 32, NQ = H / kWsKC, nfg = a.F / kWsRows;
+    uint16_t *ab = (uint16_t *)gb_lds;
+    float *sb = (float *)(gb_lds + kGbA);
+    uint8_t *wb = gb_lds + kGbA + kGbS + w * kGbArea;    // [gate 16 x 144 | up 16 x 144]
+    const int H = a.H, nsb = H / 32, NQ = H / kGbKC, nfg = a.F / kWsRows;
     const uint32_t rowb = (uint32_t)(H / 256) * 144;
     const int n_items = *a.n_tiles * nfg;
-    // per-lane byte offsets of the weight pieces of a step (piece i, lane l:
-    // byte o = 1024 i + 16 l of [gate | up] pieces, row (o mod 4608) / 288)
-    uint32_t woff[kWsPieces];
-#pragma unroll
-    for (int i = 0; i < kWsPieces; i++) {
-        const uint32_t o = i * 1024u + lane * 16u, oo = o < 4608u ? o : o - 4608u;
-        woff[i] = (oo / 288) * rowb + oo % 288;
-    }
-    struct Item { int p0, n, fg; const uint8_t *w0; uint32_t up_off; };
-    auto describe = [&](int it) {
-        const int tile = it / nfg, fg = it - tile * nfg;
+    const f16x2 m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+    for (;;) {
+        if (tid == 0) s_item = atomicAdd(a.n_tiles + 2, 1);
+        __syncthreads();
+        const int item = s_item;
+        if (item >= n_items) break;
+        const int tile = item / nfg, fg = item - tile * nfg;
         const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
         const bool shared = tl.x == a.E;
         const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)tl.x * a.stride;
-        return Item{tl.y, tl.z, fg, blob + (uint64_t)(fg * kWsRows + 16 * w) * rowb,
-                    (uint32_t)(shared ? a.sh_gate_size : a.gate_size)};
-    };
-    uint4 v[kWsPieces];
-    auto issue_w = [&](const Item &t, int q) {
-#pragma unroll
-        for (int i = 0; i < kWsPieces; i++) {   // pieces 0-3 are gate rows, 5-8 up rows, 4 both
-            const bool up = i > 4 || (i == 4 && lane >= 32);
-            v[i] = ld16(t.w0 + (woff[i] + (up ? t.up_off : 0u) + 288u * q));
-        }
-    };
-    if (tid == 0) { s_item[0] = atomicAdd(a.n_tiles + 2, 1); s_item[1] = atomicAdd(a.n_tiles + 2, 1); }
-    __syncthreads();
-    int item = s_item[0], next = s_item[1];
-    if (item >= n_items) return;
-    Item cur = describe(item);
-    issue_w(cur, 0);
-    const f16x2 m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
-    for (;;) {
-        const int p0 = cur.p0, n = cur.n, nb = (n + 15) >> 4;
-        const bool dbl = nb <= 2;
+        const uint8_t *w0 = blob + (uint64_t)(fg * kWsRows + 16 * w) * rowb;
+        const uint32_t up_off = (uint32_t)(shared ? a.sh_gate_size : a.gate_size);
+        const int p0 = tl.y, n = tl.z, nb = (n + 15) >> 4;
         const int tok = a.pair_tok[p0 + min(lane, n - 1)];    // token of tile row lane
         if (w == 0) s_exp[lane] = a.xexp[tok];
-        // stage the token rows and sub-block sums of step q into buffer b
-        auto stage = [&](int q, int b) {
-            uint16_t *ab = abase + (dbl ? b * (kWsA / 4) : 0);   // 32 KiB buffers (kWsA / 4 elements)
-            float *sb = sbase + b * (kWsS / 4);
-            for (int m = w; m < 16 * nb; m += kWsWaves) {        // one token row per wave instruction
-                const int c = lane ^ (m & 15);
-                const uint16_t *src = a.x16 + (uint64_t)__builtin_amdgcn_readlane(tok, m) * H + q * kWsKC + 8 * c;
-                __builtin_amdgcn_global_load_lds((const void *)src,
-                                                 (__attribute__((address_space(3))) void *)(ab + m * kWsKC), 16, 0, 0);
+        // step q: this wave's weights, then the token rows and their sub-block sums
+        auto issue_w = [&](int q) {
+#pragma unroll
+            for (int i = 0; i < kGbPieces; i++) {   // piece i, lane l: byte o = 1024 i + 16 l of [gate | up],
+                // row (o mod 2304) / 144; lanes past the step's bytes re-read its last 16
+                const uint32_t o = min(i * 1024u + lane * 16u, kGbW - 16);
+                const uint32_t oo = o < kGbHalf ? o : o - kGbHalf;
+                const uint32_t off = (oo / 144) * rowb + oo % 144 + (o >= kGbHalf ? up_off : 0u) + 144u * q;
+                __builtin_amdgcn_global_load_lds((const void *)(w0 + off),
+                                                 (__attribute__((address_space(3))) void *)(wb + i * 1024), 16, 0, 0);
             }
-            for (int j = w; j < 16; j += kWsWaves)               // one sub-block's token sums per instruction
-                __builtin_amdgcn_global_load_lds((const void *)(a.xsum + (uint64_t)tok * nsb + q * 16 + j),
-                                                 (__attribute__((address_space(3))) void *)(sb + j * kPfMT), 4, 0, 0);
         };
-        Item nx{};
-        if (next < n_items) nx = describe(next);
-        // the item for NB token blocks (a compile-time count: the MFMA
-        // accumulators stay in place)
+        auto issue_x = [&](int q) {
+            for (int q2 = w; q2 < 8 * nb; q2 += kWsWaves) {      // two token rows per wave instruction
+                const int m = 2 * q2 + (lane >> 5), c = (lane & 31) ^ (m & 15);
+                const uint16_t *src = a.x16 + (uint64_t)__builtin_amdgcn_ds_bpermute(4 * m, tok) * H + q * kGbKC + 8 * c;
+                __builtin_amdgcn_global_load_lds((const void *)src,
+                                                 (__attribute__((address_space(3))) void *)(ab + 2 * q2 * kGbKC), 16, 0, 0);
+            }
+            if (w < 8)                                           // one sub-block's token sums per instruction
+                __builtin_amdgcn_global_load_lds((const void *)(a.xsum + (uint64_t)tok * nsb + q * 8 + w),
+                                                 (__attribute__((address_space(3))) void *)(sb + w * kPfMT), 4, 0, 0);
+        };
         auto run = [&](auto NBC) {
-        constexpr int NB = decltype(NBC)::value;
-        stage(0, 0);
-        f32x4 gA[NB], uA[NB];
+            constexpr int NB = decltype(NBC)::value;
+            f32x4 gA[NB], uA[NB];
 #pragma unroll
-        for (int b = 0; b < NB; b++) { gA[b] = (f32x4){0.f, 0.f, 0.f, 0.f}; uA[b] = gA[b]; }
-        for (int q = 0; q < NQ; q++) {
-            const int b = dbl ? (q & 1) : 0;
-            // this wave's staging of step q has landed: it was issued before the
-            // step's weights when double-buffered (those may still fly), after
-            // them otherwise and at the first step
-            if (dbl && q > 0) __builtin_amdgcn_s_waitcnt(vmcnt_le(kWsPieces));
-            else __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();                                   // everyone's staging of step q; buffer b ^ 1 free
-            if (dbl && q + 1 < NQ) stage(q + 1, b ^ 1);
-            // this step's weights into the wave's area (one wave's LDS
-            // operations run in order: the previous step's reads are done)
-#pragma unroll
-            for (int i = 0; i < kWsPieces; i++) *(uint4 *)(wb + i * 1024 + lane * 16) = v[i];
-            if (q + 1 < NQ) issue_w(cur, q + 1);
-            else if (next < n_items) issue_w(nx, 0);
-            const uint16_t *ab = abase + (dbl ? b * (kWsA / 4) : 0);
-            const float *sb = sbase + b * (kWsS / 4);
-#pragma unroll
-            for (int sbk = 0; sbk < 2; sbk++) {
-                // one matrix (gate or up) of super-block sbk for all token blocks
+            for (int b = 0; b < NB; b++) { gA[b] = (f32x4){0.f, 0.f, 0.f, 0.f}; uA[b] = gA[b]; }
+            for (int q = 0; q < NQ; q++) {
+                issue_w(q);
+                issue_x(q);
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();                               // everyone's loads of step q have landed
                 auto pass = [&](const uint8_t *rw, f32x4 (&acc)[NB]) {
                     const uint4 hw = *(const uint4 *)rw;
-                    // min-term operand: -dmin * m of sub-block 4h + kg of row col
-                    float bm[2];
+                    float bm[2];                               // -dmin * m of sub-block 4h + kg of row col
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
                         uint32_t sc, mn;
@@ -805,19 +614,16 @@ __global__ __launch_bounds__(64 * kWsWaves, 1) void k_pf_gateup_f16(PrefillArgs 
                             const int j = 2 * c + h;
                             uint32_t sc, mn;
                             q4_scale_min(hw, j, sc, mn);
-                            // sc as an fp16 pair: bits 0x6400 | sc = 1024 + sc, minus 1024
                             const f16x2 sp = __builtin_bit_cast(f16x2, (sc * 0x10001u) | 0x64006400u) + m1024;
                             const f16x8 bw = q4_codes_f16(qw, 4 * h, sp, sp * m1024);
-                            const int chunk = 32 * sbk + 4 * j + kg;
+                            const int chunk = 4 * j + kg;
 #pragma unroll
                             for (int tb = 0; tb < NB; tb++) {
                                 const int m = 16 * tb + col;
-                                const f16x8 av = *(const f16x8 *)(ab + m * kWsKC + 8 * (chunk ^ (m & 15)));
+                                const f16x8 av = *(const f16x8 *)(ab + m * kGbKC + 8 * (chunk ^ (m & 15)));
                                 dd[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bw, dd[tb], 0, 0, 0);
                             }
                         }
-                        // keep the scheduler from hoisting every sub-block's operands
-                        // (the live ranges would exceed the register budget)
                         __builtin_amdgcn_sched_barrier(0);
                     }
                     const float d = h2f(hw.x);
@@ -826,39 +632,34 @@ __global__ __launch_bounds__(64 * kWsWaves, 1) void k_pf_gateup_f16(PrefillArgs 
 #pragma unroll
                         for (int i = 0; i < 4; i++) acc[tb][i] = fmaf(d, dd[tb][i], acc[tb][i]);
 #pragma unroll
-                        for (int h = 0; h < 2; h++) {   // A: S of token 16 tb + col, sub-block 8 sbk + 4 h + kg
-                            const float sa = sb[(8 * sbk + 4 * h + kg) * kPfMT + 16 * tb + col];
+                        for (int h = 0; h < 2; h++) {
+                            const float sa = sb[(4 * h + kg) * kPfMT + 16 * tb + col];
                             acc[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, bm[h], acc[tb], 0, 0, 0);
                         }
                     }
                 };
-                pass(wb + col * 288 + sbk * 144, gA);
-                pass(wb + 4608 + col * 288 + sbk * 144, uA);
+                pass(wb + col * 144, gA);
+                pass(wb + kGbHalf + col * 144, uA);
+                __syncthreads();                               // the step's LDS is free for the next one
             }
-            if (!dbl && q + 1 < NQ) {
-                __syncthreads();                               // everyone is done with buffer 0
-                stage(q + 1, 0);
-            }
-        }
-        // SwiGLU: lane holds tokens 16 tb + 4 kg + i of row 16 w + col
-        const int row = cur.fg * kWsRows + 16 * w + col;
+            const int row = fg * kWsRows + 16 * w + col;
 #pragma unroll
-        for (int tb = 0; tb < NB; tb++) {
+            for (int tb = 0; tb < NB; tb++) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 16 * tb + 4 * kg + i;
-                if (m < n) {
-                    const int sx = s_exp[m];
-                    const float g = ldexpf(gA[tb][i], sx), u = ldexpf(uA[tb][i], sx);
-                    const float val = (g / (1.0f + expf(-g))) * u;
-                    const __bf16 hi = (__bf16)val;
-                    const __bf16 lo = (__bf16)(val - (float)hi);
-                    const uint64_t o = (uint64_t)(p0 + m) * a.F + row;
-                    a.act_hi[o] = __builtin_bit_cast(uint16_t, hi);
-                    a.act_lo[o] = __builtin_bit_cast(uint16_t, lo);
+                for (int i = 0; i < 4; i++) {
+                    const int m = 16 * tb + 4 * kg + i;
+                    if (m < n) {
+                        const int sx = s_exp[m];
+                        const float g = ldexpf(gA[tb][i], sx), u = ldexpf(uA[tb][i], sx);
+                        const float val = (g / (1.0f + expf(-g))) * u;
+                        const __bf16 hi = (__bf16)val;
+                        const __bf16 lo = (__bf16)(val - (float)hi);
+                        const uint64_t o = (uint64_t)(p0 + m) * a.F + row;
+                        a.act_hi[o] = __builtin_bit_cast(uint16_t, hi);
+                        a.act_lo[o] = __builtin_bit_cast(uint16_t, lo);
+                    }
                 }
             }
-        }
         };
         switch (nb) {
             case 1: run(std::integral_constant<int, 1>{}); break;
@@ -866,13 +667,7 @@ __global__ __launch_bounds__(64 * kWsWaves, 1) void k_pf_gateup_f16(PrefillArgs 
             case 3: run(std::integral_constant<int, 3>{}); break;
             default: run(std::integral_constant<int, 4>{}); break;
         }
-        if (next >= n_items) break;
-        __syncthreads();                                       // s_item, s_exp and the buffers are free
-        if (tid == 0) s_item[0] = atomicAdd(a.n_tiles + 2, 1);
-        __syncthreads();
-        item = next;
-        next = s_item[0];
-        cur = nx;
+        __syncthreads();                                       // s_item and s_exp are free
     }
 }
 
@@ -1178,24 +973,18 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
     k_pf_group<<<1, 1024, 2 * (size_t)a.E * W * sizeof(uint32_t), s>>>(a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    if (a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K) {   // scale-after path
-        const int64_t n = (int64_t)a.T * (a.H / 32);
-        if (a.F % kWsRows == 0 && a.H % kWsKC == 0) {   // fp16-exact weight-streaming kernel
-            k_pf_xprep<<<a.T, 256, 0, s>>>(a);
-            static bool ws_attr = false;   // above the 64 KiB default of dynamic LDS
-            if (!ws_attr) {
-                hipError_t e = hipFuncSetAttribute((const void *)k_pf_gateup_f16,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWsLds);
-                if (e != hipSuccess) return e;
-                ws_attr = true;
-            }
-            int dev = 0, n_cu = 256;
-            if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-            k_pf_gateup_f16<<<n_cu, 64 * kWsWaves, kWsLds, s>>>(a);
-        } else {
-            k_pf_xsum<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(a);
-            k_pf_gateup_q4<<<pf_grid(a.F / kPfGateRows, a.max_tiles), kPfGateWaves * 64, 0, s>>>(a);
+    if (a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K) {   // exact fp16 operands
+        k_pf_xprep<<<a.T, 256, 0, s>>>(a);
+        static bool gb_attr = false;   // above the 64 KiB default of dynamic LDS
+        if (!gb_attr) {
+            hipError_t e = hipFuncSetAttribute((const void *)k_pf_gateup_f16,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGbLds);
+            if (e != hipSuccess) return e;
+            gb_attr = true;
         }
+        int dev = 0, n_cu = 256;
+        if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+        k_pf_gateup_f16<<<2 * n_cu, 64 * kWsWaves, kGbLds, s>>>(a);
         err = hipGetLastError();
     }
 #define FO_GU(G, U) if (a.gate_type == G && a.up_type == U) err = launch_gateup_t<G, U>(a, s);

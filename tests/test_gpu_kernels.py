@@ -650,8 +650,7 @@ def pf_bf16_mask(shape):
                                                         (33, False, False, True, 512),
                                                         (40, True, False, False, 2048),
                                                         (300, True, True, True, 1024),
-                                                        # H not a multiple of 512: the bf16 scale-after
-                                                        # gate/up kernel instead of the fp16 one
+                                                        # an odd number of 256-value K steps
                                                         (50, True, True, False, 768),
                                                         # a Q4_K down projection (bf16 weights)
                                                         (70, True, False, True, -512)])
