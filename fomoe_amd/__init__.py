@@ -14,7 +14,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libfomoe_gfx950.so")
+# FOMOE_LIB: another build of the same library (the host-sanitizer build in
+# tests); the product library otherwise.
+LIB_PATH = os.environ.get("FOMOE_LIB") or os.path.join(HERE, "libfomoe_gfx950.so")
 
 F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16, MXFP4 = 0, 1, 8, 12, 13, 14, 30, 39
 BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34),
