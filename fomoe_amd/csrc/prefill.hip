@@ -54,60 +54,93 @@ FO_DEV uint32_t pack_bf16(float lo, float hi) {   // round to nearest even, lo i
 }
 
 // ============================================================ P1 router GEMM
-// 32 tokens x 32 experts per work-group (4 waves, one 16 x 16 block each) on
-// v_mfma_f32_16x16x4_f32: fp32 operands (x widened exactly from bf16), fp32
-// accumulate. K runs in chunks of 64 staged in LDS (double-buffered, rows
-// padded by 4 floats so the 16 rows an operand read touches fall on distinct
-// banks), the next chunk held in registers while the current one is multiplied.
-constexpr int kRT = 32, kRK = 64, kRKP = kRK + 4;
+// 32 tokens x 32 experts per work-group on v_mfma_f32_32x32x2_f32: fp32
+// operands (x widened exactly from bf16), fp32 accumulate. K runs in chunks
+// of 256 staged in LDS k-major (x as [k][token], router as [k][expert]:
+// every operand read is 64 consecutive floats), double-buffered, the next
+// chunk held in registers while the current one is multiplied; each of the
+// four waves accumulates the whole 32 x 32 tile over its quarter of every
+// chunk, and the quarters are summed in a fixed order at the end.
+constexpr int kRT = 32, kRK = 256;
+constexpr uint32_t kRLds = 2u * 2u * kRK * kRT * 4u;    // 128 KiB
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __global__ __launch_bounds__(256) void k_pf_router(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) float xs[2][kRT][kRKP];
-    __shared__ __attribute__((aligned(16))) float rs[2][kRT][kRKP];
+    extern __shared__ __attribute__((aligned(16))) float rl_lds[];   // [2][2][kRK][kRT]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.y * kRT, e0 = blockIdx.x * kRT;
-    const int lr = tid >> 3, lk = (tid & 7) * 8;          // loader: row lr, 8 values at lk
-    const uint16_t *xp = a.x + (uint64_t)min(t0 + lr, a.T - 1) * a.H + lk;
-    const float *rp = a.router + (uint64_t)min(e0 + lr, a.E - 1) * a.H + lk;
-    uint4 xv;
-    float4 r0, r1;
+    // loader: row lr (token / expert) of the tile, values 32 c .. 32 c + 31 of the chunk
+    const int lr = tid & 31, c = tid >> 5;
+    const uint16_t *xp = a.x + (uint64_t)min(t0 + lr, a.T - 1) * a.H + 32 * c;
+    const float *rp = a.router + (uint64_t)min(e0 + lr, a.E - 1) * a.H + 32 * c;
+    uint4 xv[4];
+    float4 rv[8];
     auto fetch = [&](int k0) {
-        xv = *(const uint4 *)(xp + k0);
-        r0 = *(const float4 *)(rp + k0);
-        r1 = *(const float4 *)(rp + k0 + 4);
+#pragma unroll
+        for (int q = 0; q < 4; q++) xv[q] = *(const uint4 *)(xp + k0 + 8 * q);
+#pragma unroll
+        for (int q = 0; q < 8; q++) rv[q] = *(const float4 *)(rp + k0 + 4 * q);
     };
     auto put = [&](int b) {
-        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-        float4 x0 = make_float4(bf2f(xw[0] & 0xFFFFu), bf2f(xw[0] >> 16), bf2f(xw[1] & 0xFFFFu), bf2f(xw[1] >> 16));
-        float4 x1 = make_float4(bf2f(xw[2] & 0xFFFFu), bf2f(xw[2] >> 16), bf2f(xw[3] & 0xFFFFu), bf2f(xw[3] >> 16));
-        *(float4 *)&xs[b][lr][lk] = x0;
-        *(float4 *)&xs[b][lr][lk + 4] = x1;
-        *(float4 *)&rs[b][lr][lk] = r0;
-        *(float4 *)&rs[b][lr][lk + 4] = r1;
+        float *xs = rl_lds + b * (2 * kRK * kRT), *rs = xs + kRK * kRT;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t w[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const int k = 32 * c + 8 * q + 2 * h;
+                xs[k * kRT + lr] = bf2f(w[h] & 0xFFFFu);
+                xs[(k + 1) * kRT + lr] = bf2f(w[h] >> 16);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int k = 32 * c + 4 * q;
+            rs[k * kRT + lr] = rv[q].x;
+            rs[(k + 1) * kRT + lr] = rv[q].y;
+            rs[(k + 2) * kRT + lr] = rv[q].z;
+            rs[(k + 3) * kRT + lr] = rv[q].w;
+        }
     };
-    const int tb = wv >> 1, eb = wv & 1, row = lane & 15, kq = lane >> 4;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0.f;
     fetch(0);
     put(0);
     __syncthreads();
     const int NKC = a.H / kRK;
+    // A operand: x[token lane % 32][k + lane / 32]; B: router[expert lane % 32][k + lane / 32]
+    const int m = lane & 31, kh = lane >> 5;
     for (int kc = 0; kc < NKC; kc++) {
         const int b = kc & 1;
         if (kc + 1 < NKC) fetch((kc + 1) * kRK);
+        const float *xs = rl_lds + b * (2 * kRK * kRT), *rs = xs + kRK * kRT;
 #pragma unroll
-        for (int kk = 0; kk < kRK; kk += 4) {
-            const float av = xs[b][16 * tb + row][kk + kq];
-            const float bv = rs[b][16 * eb + row][kk + kq];
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+        for (int kk = 64 * wv; kk < 64 * wv + 64; kk += 2) {
+            const float av = xs[(kk + kh) * kRT + m];
+            const float bv = rs[(kk + kh) * kRT + m];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
         }
         if (kc + 1 < NKC) put(b ^ 1);
         __syncthreads();
     }
-    // D layout: lane holds rows 4*(lane/16)+i (tokens) of column lane%16 (expert)
+    // D layout: lane holds rows 8 (i / 4) + 4 (lane / 32) + i % 4 (tokens) of
+    // column lane % 32 (expert); waves 1-3 hand their quarters to wave 0
+    float *red = rl_lds;                                   // [3][16][64]
+    if (wv > 0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int t = t0 + 16 * tb + 4 * kq + i, e = e0 + 16 * eb + row;
-        if (t < a.T && e < a.E) a.logits[(uint64_t)t * a.E + e] = acc[i] + (a.router_bias ? a.router_bias[e] : 0.f);
+        for (int i = 0; i < 16; i++) red[((wv - 1) * 16 + i) * 64 + lane] = acc[i];
+    }
+    __syncthreads();
+    if (wv == 0) {
+        const int e = e0 + m;
+        const float bias = (a.router_bias && e < a.E) ? a.router_bias[e] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float v = ((acc[i] + red[i * 64 + lane]) + red[(16 + i) * 64 + lane]) + red[(32 + i) * 64 + lane];
+            const int t = t0 + 8 * (i >> 2) + 4 * kh + (i & 3);
+            if (t < a.T && e < a.E) a.logits[(uint64_t)t * a.E + e] = v + bias;
+        }
     }
 }
 
@@ -961,7 +994,14 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         a.H <= 0 || a.H % 256 || a.H % (32 * kPfDownWaves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
         a.max_tiles < prefill_max_tiles(a.T, a.k, a.E, a.shared != nullptr))
         return hipErrorInvalidValue;
-    k_pf_router<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 256, 0, s>>>(a);
+    static bool router_attr = false;   // above the 64 KiB default of dynamic LDS
+    if (!router_attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_pf_router, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)kRLds);
+        if (e != hipSuccess) return e;
+        router_attr = true;
+    }
+    k_pf_router<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 256, kRLds, s>>>(a);
     k_pf_topk<<<(a.T + 3) / 4, 256, 0, s>>>(a);
     static bool lds_attr = false;   // the grouping tables may exceed the 64 KiB default
     if (!lds_attr) {
