@@ -582,6 +582,13 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     if (!pt) return fail(ctx, -1, "moe prefill: gate/up/down types must be Q4_K or Q6_K");
     const int T = n_tokens, E = L->n_experts, k = L->k, H = L->n_embd, F = L->inter;
     if (E > 1023) return fail(ctx, -1, "moe prefill: n_experts %d > 1023", E);
+    if (L->gate_type == GGML_TYPE_Q4_K) {   // its gate/up rows move by direct 16-byte global->LDS loads
+        auto a16 = [](uint64_t v) { return v % 16 == 0; };
+        if (!a16((uintptr_t)L->experts) || !a16(L->expert_stride) || !a16(L->gate_size) ||
+            (L->shared && (!a16((uintptr_t)L->shared) || !a16(L->shared_gate_size))))
+            return fail(ctx, -1, "moe prefill: Q4_K gate/up blobs must be 16-byte aligned "
+                                 "(experts, shared, expert_stride, gate sizes)");
+    }
     // the grouping table holds n_experts x ceil(tokens/32) words: larger
     // batches run as consecutive chunks (the results per token are the same)
     const int Tc = std::min(T, (16384 / E) * 32);

@@ -715,6 +715,25 @@ def test_prefill_token_scales(gpu):
     assert not got[5].any() and not want[5].any()
 
 
+def test_prefill_rejects_misaligned_q4k_blobs(gpu):
+    """The Q4_K gate/up rows are moved by 16-byte direct global->LDS loads: a
+    layer whose expert blobs are not 16-byte aligned is refused with an error
+    instead of being read wrongly."""
+    from fomoe_amd import synthetic as S
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=16, k=4, shared=True)
+    L = S.build_layer(gpu, shape, 0, seed=21, zipf_s=None, norm=False)
+    dx = S.tokens_bf16(gpu, 4, shape.n_embd, seed=23)
+    dout = gpu.alloc(4 * 4 * shape.n_embd)
+    gpu.moe_prefill(L.desc, dx, 4, dout, 0)   # aligned: runs
+    L.desc.experts += 8
+    with pytest.raises(FA.GpuError, match="16-byte aligned"):
+        gpu.moe_prefill(L.desc, dx, 4, dout, 0)
+    L.desc.experts -= 8
+    L.desc.expert_stride += 8
+    with pytest.raises(FA.GpuError, match="16-byte aligned"):
+        gpu.moe_prefill(L.desc, dx, 4, dout, 0)
+
+
 def test_prefill_chunked_batch(gpu):
     """A batch beyond the grouping table (512 experts x 1300 tokens) runs as
     chunks of 1024 + 276 tokens: bit-identical to the two calls made
