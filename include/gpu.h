@@ -288,7 +288,8 @@ void gpu_gguf_free_moe_layer(gpu_ctx_t *ctx, gpu_moe_layer_t *L);
  * a per-pair power of two (within ~6e-4 of the exact layer per token); other
  * types dequantized to bf16 (round to nearest even), with the activation as
  * two bf16 terms (hi + lo, within 2^-18). gate/up/down types Q4_K or Q6_K;
- * n_experts <= 1023. A batch larger than the grouping table (n_experts *
+ * n_experts <= 1023; with Q4_K gate/up, the experts and shared pointers,
+ * expert_stride and the gate sizes must be multiples of 16 bytes (-1 else). A batch larger than the grouping table (n_experts *
  * ceil(n_tokens/32) > 16384) runs as consecutive chunks of
  * (16384 / n_experts) * 32 tokens with the same results per token. No
  * counterpart in the reference, which decodes prompt tokens one at a time
