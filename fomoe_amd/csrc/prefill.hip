@@ -330,6 +330,17 @@ FO_DEV void pf_tile_of(int nrb, int &tile, int &rb) {
     rb = j >> 3;
 }
 inline unsigned pf_grid(int nrb, int max_tiles) { return (unsigned)(nrb * ((max_tiles + 7) & ~7)); }
+// The same grid with each XCD given a contiguous range of ceil(n_tiles / 8)
+// tiles (work-group i on XCD i % 8 takes the i / 8-th (tile, row block) of its
+// range): the tiles of one expert are consecutive, so an expert with several
+// tiles streams its weights through one XCD's L2, its tiles in flight
+// together. tile >= n_tiles: nothing to do.
+FO_DEV void pf_tile_of_xcd(int nrb, int n_tiles, int &tile, int &rb) {
+    const int i = blockIdx.x, x = i & 7, slot = i >> 3;
+    const int per = (n_tiles + 7) >> 3, tl = slot / nrb;
+    rb = slot - tl * nrb;
+    tile = tl < per ? x * per + tl : n_tiles;
+}
 // Work-group: 4 waves, tile of <= 64 pairs (token rows) x 64 weight rows; wave
 // w owns weight rows 16w..16w+15 (MFMA columns: lane % 16) for every token
 // block. The tile's activations for one 256-value super-block sit in LDS
@@ -578,8 +589,8 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
     uint8_t *wb = gb_lds + kGbA + kGbS + w * kGbArea;    // [gate 16 x 144 | up 16 x 144]
     const int H = a.H, nsb = H / 32, NQ = H / kGbKC, nfg = a.F / kWsRows;
     const uint32_t rowb = (uint32_t)(H / 256) * 144;
-    const int n_items = *a.n_tiles * nfg;
     const f16x2 m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+    const int n_items = *a.n_tiles * nfg;
     for (;;) {
         if (tid == 0) s_item = atomicAdd(a.n_tiles + 2, 1);
         __syncthreads();
@@ -828,7 +839,7 @@ __global__ __launch_bounds__(kPfDownWaves * 64, 4) void k_pf_down16(PrefillArgs 
     using D = PfDec<GGML_TYPE_Q6_K>;
     extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x tile
     int tile, rbk;
-    pf_tile_of(a.H / (32 * kPfDownWaves), tile, rbk);
+    pf_tile_of_xcd(a.H / (32 * kPfDownWaves), *a.n_tiles, tile, rbk);
     if (tile >= *a.n_tiles) return;
     const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
     const int e = tl.x, p0 = tl.y, n = tl.z;
