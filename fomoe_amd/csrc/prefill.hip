@@ -638,13 +638,22 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
                 issue_x(q);
                 __builtin_amdgcn_s_waitcnt(0);
                 __syncthreads();                               // everyone's loads of step q have landed
+                // Lane group kg owns sub-blocks 2 kg and 2 kg + 1 of the super-block
+                // (MFMA (c, h): lane group kg's 8 values are values 8c..8c+7 of
+                // sub-block 2 kg + h; the token operand is read in the same
+                // order), so each lane decodes two (scale, min) pairs instead of
+                // all eight.
                 auto pass = [&](const uint8_t *rw, f32x4 (&acc)[NB]) {
                     const uint4 hw = *(const uint4 *)rw;
-                    float bm[2];                               // -dmin * m of sub-block 4h + kg of row col
+                    f16x2 sp[2], nsp[2];
+                    float bm[2];                               // -dmin * m of sub-block 2 kg + h of row col
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
                         uint32_t sc, mn;
-                        q4_scale_min(hw, 4 * h + kg, sc, mn);
+                        q4_scale_min(hw, 2 * kg + h, sc, mn);
+                        // sc as an fp16 pair: bits 0x6400 | sc = 1024 + sc, minus 1024
+                        sp[h] = __builtin_bit_cast(f16x2, (sc * 0x10001u) | 0x64006400u) + m1024;
+                        nsp[h] = sp[h] * m1024;
                         bm[h] = -h2f(hw.x >> 16) * (float)mn;
                     }
                     f32x4 dd[NB];
@@ -652,15 +661,11 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
                     for (int tb = 0; tb < NB; tb++) dd[tb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        const uint2 qw = *(const uint2 *)(rw + 16 + 32 * c + 8 * kg);
+                        const uint2 qw = *(const uint2 *)(rw + 16 + 32 * kg + 8 * c);   // sub-blocks 2 kg, 2 kg + 1
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
-                            const int j = 2 * c + h;
-                            uint32_t sc, mn;
-                            q4_scale_min(hw, j, sc, mn);
-                            const f16x2 sp = __builtin_bit_cast(f16x2, (sc * 0x10001u) | 0x64006400u) + m1024;
-                            const f16x8 bw = q4_codes_f16(qw, 4 * h, sp, sp * m1024);
-                            const int chunk = 4 * j + kg;
+                            const f16x8 bw = q4_codes_f16(qw, 4 * h, sp[h], nsp[h]);
+                            const int chunk = 8 * kg + 4 * h + c;  // values 32 (2 kg + h) + 8 c
 #pragma unroll
                             for (int tb = 0; tb < NB; tb++) {
                                 const int m = 16 * tb + col;
@@ -676,8 +681,8 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
 #pragma unroll
                         for (int i = 0; i < 4; i++) acc[tb][i] = fmaf(d, dd[tb][i], acc[tb][i]);
 #pragma unroll
-                        for (int h = 0; h < 2; h++) {
-                            const float sa = sb[(4 * h + kg) * kPfMT + 16 * tb + col];
+                        for (int h = 0; h < 2; h++) {   // A: S of token 16 tb + col, sub-block 2 kg + h
+                            const float sa = sb[(2 * kg + h) * kPfMT + 16 * tb + col];
                             acc[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(sa, bm[h], acc[tb], 0, 0, 0);
                         }
                     }
