@@ -43,37 +43,49 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def rotation(gpu, t, M, K, wseed, xseed, n_mats, steps, warmup):
+class Rotation:
     """n_mats distinct [M x K] matrices of type t (matrix m from stream m of
-    wseed; matrix 0 is the BASELINE config's W) times one x, one launch per step."""
-    rb = FA.row_bytes(t, K) * M
-    stride = (rb + 4095) // 4096 * 4096
-    dW = gpu.alloc(stride * n_mats)
-    gpu.synth_quant(t, wseed, 0, 1, 0.02, M, K, n_mats, dW, stride)
-    dx = gpu.alloc(4 * K)
-    gpu.synth_f32(xseed, 0, 1.0, dx, K)
-    dy = gpu.alloc(4 * M * n_mats)
-    for _ in range(warmup):
-        gpu.matvec_batched(t, dW, stride, n_mats, dx, 0, dy, M, M, K)
-    gpu.sync()
-    gpu.timer_start()
-    for _ in range(steps):
-        gpu.matvec_batched(t, dW, stride, n_mats, dx, 0, dy, M, M, K)
-    ms = gpu.timer_stop() / steps
-    # per-launch spread, from >= 100 separately timed launches after the timed region
-    each = []
-    for _ in range(max(steps, 100)):
-        gpu.timer_start()
-        gpu.matvec_batched(t, dW, stride, n_mats, dx, 0, dy, M, M, K)
-        each.append(gpu.timer_stop())
-    p10, p50, p90 = np.percentile(each, [10, 50, 90])
-    bytes_per_mat = rb + 4 * K + 4 * M        # weights + x + y, each counted once per launch
-    total = bytes_per_mat * n_mats
-    res = {"ms_per_step": ms, "bytes_per_step": total, "GB/s": total / ms / 1e6,
-           "weight_bytes": rb * n_mats, "launch_ms_p10": p10, "launch_ms_p50": p50, "launch_ms_p90": p90}
-    res["frac_hbm"] = res["GB/s"] / HBM_PEAK_GBS
-    keep = (dW, dx, dy, stride)
-    return res, keep
+    wseed; matrix 0 is the BASELINE config's W) times one x, one launch per
+    step. setup() generates the weights in HBM, timed() runs W warmup and K
+    timed steps back to back, spread() times >= 100 launches one by one."""
+
+    def __init__(self, gpu, t, M, K, wseed, xseed, n_mats):
+        self.gpu, self.t, self.M, self.K, self.n = gpu, t, M, K, n_mats
+        self.rb = FA.row_bytes(t, K) * M
+        self.stride = (self.rb + 4095) // 4096 * 4096
+        self.dW = gpu.alloc(self.stride * n_mats)
+        gpu.synth_quant(t, wseed, 0, 1, 0.02, M, K, n_mats, self.dW, self.stride)
+        self.dx = gpu.alloc(4 * K)
+        gpu.synth_f32(xseed, 0, 1.0, self.dx, K)
+        self.dy = gpu.alloc(4 * M * n_mats)
+        self.res = {}
+
+    def launch(self):
+        self.gpu.matvec_batched(self.t, self.dW, self.stride, self.n, self.dx, 0, self.dy, self.M, self.M, self.K)
+
+    def timed(self, steps, warmup):
+        for _ in range(warmup):
+            self.launch()
+        self.gpu.sync()
+        self.gpu.timer_start()
+        for _ in range(steps):
+            self.launch()
+        ms = self.gpu.timer_stop() / steps
+        total = (self.rb + 4 * self.K + 4 * self.M) * self.n   # weights + x + y, each once per launch
+        self.res.update({"ms_per_step": ms, "bytes_per_step": total, "GB/s": total / ms / 1e6,
+                         "weight_bytes": self.rb * self.n, "frac_hbm": total / ms / 1e6 / HBM_PEAK_GBS})
+
+    def spread(self, steps):
+        each = []
+        for _ in range(max(steps, 100)):
+            self.gpu.timer_start()
+            self.launch()
+            each.append(self.gpu.timer_stop())
+        p10, p50, p90 = np.percentile(each, [10, 50, 90])
+        self.res.update({"launch_ms_p10": p10, "launch_ms_p50": p50, "launch_ms_p90": p90})
+
+    def report(self):
+        return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in self.res.items()}
 
 
 def cpu_env():
@@ -352,34 +364,44 @@ def main():
     log(f"device {gpu.arch}: {gpu.n_cu} CUs, {gpu.hbm / 1e9:.1f} GB")
     extra = {}
     keeps = {}
-    t_wall = time.perf_counter()
-    q6, keep6 = rotation(gpu, FA.Q6_K, 4096, 1024, 2, 3, 512, args.steps, args.warmup)
-    log(f"Q6_K rotation: {q6['GB/s']:.0f} GB/s ({q6['frac_hbm'] * 100:.1f}% of HBM)")
-    wall_steps = time.perf_counter() - t_wall
-    keeps["q6k"] = (keep6[0], keep6[3])
-    extra["config2_q6k"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q6.items()}
+    # All rotations' weights are generated first and their timed loops run
+    # back to back, the headline (Q6_K) last: a GPU fresh from idle needs
+    # ~30 ms of sustained load before its clocks settle (the same Q6_K launch
+    # takes ~380 us early and 278-280 us from about the 100th launch on, on
+    # any allocation), and idle gaps (weight generation, one-by-one timed
+    # launches) between legs let it fall back. The headline gets its own W
+    # warmup steps and exactly K timed steps; the per-launch spreads follow.
+    legs = []
     if "q4k" not in skip:
-        q4, keep = rotation(gpu, FA.Q4_K, 1024, 4096, 0, 1, 512, args.steps, args.warmup)
-        extra["config1_q4k"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q4.items()}
-        log(f"Q4_K rotation: {q4['GB/s']:.0f} GB/s")
-        keeps["q4k"] = (keep[0], keep[3])
+        legs.append(("config1_q4k", "q4k", Rotation(gpu, FA.Q4_K, 1024, 4096, 0, 1, 512)))
     if "q8_0" not in skip:
-        q8, keep = rotation(gpu, FA.Q8_0, 4096, 1024, 2, 3, 512, args.steps, args.warmup)
-        extra["config2_q8_0"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q8.items()}
-        log(f"Q8_0 rotation: {q8['GB/s']:.0f} GB/s")
-        keeps["q8_0"] = (keep[0], keep[3])
+        legs.append(("config2_q8_0", "q8_0", Rotation(gpu, FA.Q8_0, 4096, 1024, 2, 3, 512)))
     if "q5k" not in skip:   # the real model's down projections are partly Q5_K (same shape as config 2)
-        q5, keep = rotation(gpu, FA.Q5_K, 4096, 1024, 2, 3, 512, args.steps, args.warmup)
-        extra["config2_q5k"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in q5.items()}
-        log(f"Q5_K rotation: {q5['GB/s']:.0f} GB/s")
-        del keep
+        legs.append(("config2_q5k", None, Rotation(gpu, FA.Q5_K, 4096, 1024, 2, 3, 512)))
+    q6r = Rotation(gpu, FA.Q6_K, 4096, 1024, 2, 3, 512)
+    legs.append(("config2_q6k", "q6k", q6r))
+    gpu.sync()
+    for name, _, r in legs:
+        if r is q6r:
+            t_wall = time.perf_counter()
+        r.timed(args.steps, args.warmup)
+        if r is q6r:
+            wall_steps = time.perf_counter() - t_wall
+        log(f"{name}: {r.res['GB/s']:.0f} GB/s ({r.res['frac_hbm'] * 100:.1f}% of HBM)")
+    for name, kname, r in legs:
+        r.spread(args.steps)
+        extra[name] = r.report()
+        if kname:
+            keeps[kname] = (r.dW, r.stride)
+    q6 = q6r.res
+    keep6 = None
     cpu = None
     if "cpu" not in skip:
         cpu, cinfo = cpu_matvec_baselines(gpu, keeps, args.cpu_seconds, env)
         extra.update(cinfo)
         if cpu:
             log(f"CPU baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['kind']})")
-    del keeps, keep6
+    del keeps, keep6, legs, q6r
     if "stack" not in skip and args.stack_layers > 0:
         extra.update(moe_layer_and_stack(gpu, args.stack_layers, args.stack_steps, args.layer_calls,
                                          0 if "prefill" in skip else args.prefill_reps,
