@@ -75,6 +75,37 @@ FO_DEV void stage_lds_wait() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 }
+// LDS byte address of a pointer into this work-group's LDS.
+FO_DEV uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Direct global->LDS loads (lane l's 16 / 4 bytes land at lds_base + 16 l /
+// 4 l; lds_base wave-uniform) issued as inline assembly, so that the compiler
+// does not track them: once it knows of an outstanding direct-to-LDS load it
+// makes every later LDS read wait for all outstanding loads (vmcnt(0)), which
+// serialises a prefetch of the next step with the arithmetic on the current
+// one. The caller waits for them itself (s_waitcnt vmcnt, counting the loads
+// issued after them); the compiler's own waits for later loads stay correct
+// because these are older.
+FO_DEV void dma16_untracked(const void *g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
+}
+FO_DEV void dma16_untracked_nt(const void *g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
+}
+FO_DEV void dma4_untracked(const void *g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
+}
+
+// Work-group barrier that orders LDS only: outstanding global loads stay in
+// flight (the compiler's LDS fence also waits for them once a direct-to-LDS
+// load has been issued). The clobber keeps memory accesses on their side.
+FO_DEV void wg_sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __host__ __device__ constexpr uint32_t lds_round(uint64_t n) { return (uint32_t)((n + 1023) & ~(uint64_t)1023); }
 
 // fp16 bits -> fp32 (exact; hardware conversion handles subnormals, inf, NaN)

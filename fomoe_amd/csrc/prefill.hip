@@ -838,9 +838,13 @@ __global__ __launch_bounds__(256) void k_pf_actprep(PrefillArgs a) {
 // one v_pk_add_f16 and one v_pk_mul_f16 per two codes; both roundings are
 // nearest-even, 2^-11 relative at most) against the fp16 activation rows of
 // k_pf_actprep, one MFMA per operand; the epilogue applies the pair's 2^s.
-// One activation plane halves the LDS of k_pf_down (64 KiB for two buffers),
-// so two work-groups share a CU.
-__global__ __launch_bounds__(kPfDownWaves * 64, 4) void k_pf_down16(PrefillArgs a) {
+// One activation plane halves the LDS of k_pf_down (64 KiB for two buffers).
+// One work-group per CU (148 VGPRs, no spills): the next step's activation
+// rows and weights are requested before the current step is multiplied, and
+// with untracked direct-to-LDS loads and no spill reloads nothing in the step
+// waits for them (measured 341 us against 358 us for two work-groups per CU
+// at 128 VGPRs, whose spill reloads waited for every outstanding load).
+__global__ __launch_bounds__(kPfDownWaves * 64, 1) void k_pf_down16(PrefillArgs a) {
     using D = PfDec<GGML_TYPE_Q6_K>;
     extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x tile
     int tile, rbk;
@@ -848,7 +852,7 @@ __global__ __launch_bounds__(kPfDownWaves * 64, 4) void k_pf_down16(PrefillArgs 
     if (tile >= *a.n_tiles) return;
     const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
     const int e = tl.x, p0 = tl.y, n = tl.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), col = lane & 15, kg = lane >> 4;
     const bool shared = e == a.E;
     const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
     const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
@@ -856,19 +860,17 @@ __global__ __launch_bounds__(kPfDownWaves * 64, 4) void k_pf_down16(PrefillArgs 
     const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
     const uint8_t *drow = blob + down_off + (uint64_t)row * db, *drow1 = drow + 16 * db;
     const int nb = (n + 15) >> 4, NK = a.F / 256;
-    f32x4 acc[2][4];
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int b = 0; b < 4; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
+    // the next step's activation rows land while this step is multiplied: the
+    // direct-to-LDS loads are untracked by the compiler (a tracked one makes
+    // every LDS read of the current step wait for them); the wait at the top
+    // of each step covers them
     auto stage = [&](int kb) {
-        uint16_t *buf = d16s + (kb & 1) * kPfTile;
+        const uint32_t buf = lds_addr(d16s + (kb & 1) * kPfTile);
         for (int q = wave; q < nb * 8; q += kPfDownWaves) {
             const int m = 2 * q + (lane >> 5), cs = lane & 31;
             const int c = cs ^ (m & 15);
             const uint16_t *src = a.act_hi + (uint64_t)(p0 + (m < n ? m : 0)) * a.F + kb * 256 + 8 * c;
-            __builtin_amdgcn_global_load_lds((const void *)src,
-                                             (__attribute__((address_space(3))) void *)(buf + q * 512), 16, 0, 0);
+            dma16_untracked(src, buf + q * 1024);
         }
     };
     // fp16 operand of chunk ch (values 128n + 32t + 8kg .. +7, scale group
@@ -896,46 +898,60 @@ __global__ __launch_bounds__(kPfDownWaves * 64, 4) void k_pf_down16(PrefillArgs 
             r[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, pw[i]) + m1056) * ds2);
         return __builtin_bit_cast(f16x8, r);
     };
-    stage(0);
-    auto s0_next = D::load(drow, kg);
-    auto s1_next = D::load(drow1, kg);
-    for (int kb = 0; kb < NK; kb++) {
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        const auto s0 = s0_next;
-        const auto s1 = s1_next;
-        if (kb + 1 < NK) {
-            stage(kb + 1);
-            s0_next = D::load(drow + (uint64_t)(kb + 1) * D::BLOCK, kg);
-            s1_next = D::load(drow1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
-        }
-        const uint16_t *xh = d16s + (kb & 1) * kPfTile;
+    // the token-block count is a compile-time constant of the loop (fewer
+    // live registers for small tiles: no spill reloads, whose waits would
+    // also wait for the next step's loads)
+    auto run = [&](auto NBC) {
+        constexpr int NB = decltype(NBC)::value;
+        f32x4 acc[2][NB];
 #pragma unroll
-        for (int ch = 0; ch < 8; ch++) {
-            const f16x8 b0 = dec(s0, ch), b1 = dec(s1, ch);
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                if (b < nb) {
+            for (int b = 0; b < NB; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
+        stage(0);
+        auto s0_next = D::load(drow, kg);
+        auto s1_next = D::load(drow1, kg);
+        for (int kb = 0; kb < NK; kb++) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            const auto s0 = s0_next;
+            const auto s1 = s1_next;
+            if (kb + 1 < NK) {
+                stage(kb + 1);
+                s0_next = D::load(drow + (uint64_t)(kb + 1) * D::BLOCK, kg);
+                s1_next = D::load(drow1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
+            }
+            const uint16_t *xh = d16s + (kb & 1) * kPfTile;
+#pragma unroll
+            for (int ch = 0; ch < 8; ch++) {
+                const f16x8 b0 = dec(s0, ch), b1 = dec(s1, ch);
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
                     const f16x8 av = *(const f16x8 *)(xh + pf_swz(16 * b + col, 4 * ch + kg));
                     acc[0][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[0][b], 0, 0, 0);
                     acc[1][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[1][b], 0, 0, 0);
                 }
             }
         }
-    }
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        if (b >= nb) break;
+        for (int b = 0; b < NB; b++) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 16 * b + 4 * kg + i;
-            if (m < n) {
-                const int sx = a.pexp[p0 + m];
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * b + 4 * kg + i;
+                if (m < n) {
+                    const int sx = a.pexp[p0 + m];
 #pragma unroll
-                for (int h = 0; h < 2; h++)
-                    a.outp[(uint64_t)(p0 + m) * a.H + row + 16 * h] = ldexpf(acc[h][b][i], sx);
+                    for (int h = 0; h < 2; h++)
+                        a.outp[(uint64_t)(p0 + m) * a.H + row + 16 * h] = ldexpf(acc[h][b][i], sx);
+                }
             }
         }
+    };
+    switch (nb) {
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        case 3: run(std::integral_constant<int, 3>{}); break;
+        default: run(std::integral_constant<int, 4>{}); break;
     }
 }
 #pragma clang fp contract(on)
