@@ -552,22 +552,37 @@ __global__ __launch_bounds__(256) void k_pf_xprep(PrefillArgs a) {
 FO_DEV void q4_scale_min(const uint4 &hdr, int j, uint32_t &sc, uint32_t &mn) {
     const int jj = j & 3;
     const uint32_t b0 = (hdr.y >> (8 * jj)) & 0xFFu, b4 = (hdr.z >> (8 * jj)) & 0xFFu, b8 = (hdr.w >> (8 * jj)) & 0xFFu;
-    if (j < 4) { sc = b0 & 63; mn = b4 & 63; }
-    else { sc = (b8 & 0xF) | ((b0 >> 6) << 4); mn = (b8 >> 4) | ((b4 >> 6) << 4); }
+    const bool lo = j < 4;
+    sc = lo ? (b0 & 63) : ((b8 & 0xF) | ((b0 >> 2) & 0x30));
+    mn = lo ? (b4 & 63) : ((b8 >> 4) | ((b4 >> 2) & 0x30));
 }
 
-// eight codes (bytes of q selected by nibble sh) times sc as exact fp16
-FO_DEV f16x8 q4_codes_f16(uint2 q, int sh, f16x2 sc, f16x2 nsc) {
-    const uint32_t w0 = (q.x >> sh) & 0x0F0F0F0Fu, w1 = (q.y >> sh) & 0x0F0F0F0Fu;
+// Eight codes of nibble h (0: low, 1: high) of q times the sub-block scale as
+// exact fp16. A byte b = code (h = 0) or 16 code (h = 1, the nibble masked in
+// place, no shift) becomes the fp16 1024 + b through byte permutes with 0x64;
+// with (sc, nsc) = q4_scale_f16(scale, h) one fma per pair gives code * scale:
+// (1024 + b) s - 1024 s with s = scale / 16^h, exact with one rounding
+// (|code * scale| <= 945).
+FO_DEV f16x8 q4_codes_f16(uint2 q, int h, f16x2 sc, f16x2 nsc) {
+    const uint32_t m = h ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    const uint32_t w0 = q.x & m, w1 = q.y & m;
     const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u),
                            __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
                            __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u),
                            __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u)};
     u32x4 r;
 #pragma unroll
-    for (int i = 0; i < 4; i++)   // (1024 + q) sc - 1024 sc, one rounding: exact
+    for (int i = 0; i < 4; i++)
         r[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p[i]), sc, nsc));
     return __builtin_bit_cast(f16x8, r);
+}
+// (scale / 16^h, -1024 scale / 16^h) as fp16 pairs, exact: the bits 0x6400 |
+// scale are 1024 + scale, 0x5400 | scale are 64 + scale / 16
+FO_DEV void q4_scale_f16(uint32_t scale, int h, f16x2 &sc, f16x2 &nsc) {
+    const f16x2 m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
+    const f16x2 off = h ? (f16x2){(_Float16)-64.f, (_Float16)-64.f} : m1024;
+    sc = __builtin_bit_cast(f16x2, (scale * 0x10001u) | (h ? 0x54005400u : 0x64006400u)) + off;
+    nsc = sc * m1024;
 }
 
 constexpr int kGbKC = 256;                            // K values per step
@@ -589,7 +604,6 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
     uint8_t *wb = gb_lds + kGbA + kGbS + w * kGbArea;    // [gate 16 x 144 | up 16 x 144]
     const int H = a.H, nsb = H / 32, NQ = H / kGbKC, nfg = a.F / kWsRows;
     const uint32_t rowb = (uint32_t)(H / 256) * 144;
-    const f16x2 m1024 = {(_Float16)-1024.f, (_Float16)-1024.f};
     const int n_items = *a.n_tiles * nfg;
     for (;;) {
         if (tid == 0) s_item = atomicAdd(a.n_tiles + 2, 1);
@@ -652,8 +666,7 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
                         uint32_t sc, mn;
                         q4_scale_min(hw, 2 * kg + h, sc, mn);
                         // sc as an fp16 pair: bits 0x6400 | sc = 1024 + sc, minus 1024
-                        sp[h] = __builtin_bit_cast(f16x2, (sc * 0x10001u) | 0x64006400u) + m1024;
-                        nsp[h] = sp[h] * m1024;
+                        q4_scale_f16(sc, h, sp[h], nsp[h]);
                         bm[h] = -h2f(hw.x >> 16) * (float)mn;
                     }
                     f32x4 dd[NB];
@@ -664,7 +677,7 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
                         const uint2 qw = *(const uint2 *)(rw + 16 + 32 * kg + 8 * c);   // sub-blocks 2 kg, 2 kg + 1
 #pragma unroll
                         for (int h = 0; h < 2; h++) {
-                            const f16x8 bw = q4_codes_f16(qw, 4 * h, sp[h], nsp[h]);
+                            const f16x8 bw = q4_codes_f16(qw, h, sp[h], nsp[h]);
                             const int chunk = 8 * kg + 4 * h + c;  // values 32 (2 kg + h) + 8 c
 #pragma unroll
                             for (int tb = 0; tb < NB; tb++) {
