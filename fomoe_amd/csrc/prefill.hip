@@ -330,17 +330,6 @@ FO_DEV void pf_tile_of(int nrb, int &tile, int &rb) {
     rb = j >> 3;
 }
 inline unsigned pf_grid(int nrb, int max_tiles) { return (unsigned)(nrb * ((max_tiles + 7) & ~7)); }
-// The same grid with each XCD given a contiguous range of ceil(n_tiles / 8)
-// tiles (work-group i on XCD i % 8 takes the i / 8-th (tile, row block) of its
-// range): the tiles of one expert are consecutive, so an expert with several
-// tiles streams its weights through one XCD's L2, its tiles in flight
-// together. tile >= n_tiles: nothing to do.
-FO_DEV void pf_tile_of_xcd(int nrb, int n_tiles, int &tile, int &rb) {
-    const int i = blockIdx.x, x = i & 7, slot = i >> 3;
-    const int per = (n_tiles + 7) >> 3, tl = slot / nrb;
-    rb = slot - tl * nrb;
-    tile = tl < per ? x * per + tl : n_tiles;
-}
 // Work-group: 4 waves, tile of <= 64 pairs (token rows) x 64 weight rows; wave
 // w owns weight rows 16w..16w+15 (MFMA columns: lane % 16) for every token
 // block. The tile's activations for one 256-value super-block sit in LDS
@@ -852,37 +841,51 @@ __global__ __launch_bounds__(256) void k_pf_actprep(PrefillArgs a) {
 // nearest-even, 2^-11 relative at most) against the fp16 activation rows of
 // k_pf_actprep, one MFMA per operand; the epilogue applies the pair's 2^s.
 // One activation plane halves the LDS of k_pf_down (64 KiB for two buffers).
-// One work-group per CU (148 VGPRs, no spills): the next step's activation
-// rows and weights are requested before the current step is multiplied, and
-// with untracked direct-to-LDS loads and no spill reloads nothing in the step
-// waits for them (measured 341 us against 358 us for two work-groups per CU
-// at 128 VGPRs, whose spill reloads waited for every outstanding load).
+// One persistent work-group per CU (205 VGPRs, no spills) loops over the
+// items (tile, 256 rows) of its XCD: the next step's activation rows and
+// weights are requested before the current step is multiplied — the last
+// step of an item requests the next item's first, so no item starts on an
+// empty pipeline — and with untracked direct-to-LDS loads and no spill
+// reloads nothing in the step waits for them (config 5: 0.807 ms per
+// prefill against 0.817 ms for one work-group per item; that kernel, 341 µs,
+// against 358 µs for two work-groups per CU at 128 VGPRs, whose spill
+// reloads waited for every outstanding load).
 __global__ __launch_bounds__(kPfDownWaves * 64, 1) void k_pf_down16(PrefillArgs a) {
     using D = PfDec<GGML_TYPE_Q6_K>;
     extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x tile
-    int tile, rbk;
-    pf_tile_of_xcd(a.H / (32 * kPfDownWaves), *a.n_tiles, tile, rbk);
-    if (tile >= *a.n_tiles) return;
-    const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
-    const int e = tl.x, p0 = tl.y, n = tl.z;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), col = lane & 15, kg = lane >> 4;
-    const bool shared = e == a.E;
-    const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
-    const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
-    const int row = rbk * (32 * kPfDownWaves) + 32 * wave + col;   // rows row, row + 16
+    // items (tile, block of 256 rows) of this work-group's XCD (work-group i
+    // runs on XCD i % 8; the XCD's contiguous range of ceil(n_tiles / 8)
+    // tiles, so an expert's tiles share one L2): u = i / 8, + G8, ...
+    const int nt = *a.n_tiles, nrb = a.H / (32 * kPfDownWaves);
+    const int x = blockIdx.x & 7, G8 = gridDim.x >> 3, per = (nt + 7) >> 3, n_u = per * nrb;
     const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
-    const uint8_t *drow = blob + down_off + (uint64_t)row * db, *drow1 = drow + 16 * db;
-    const int nb = (n + 15) >> 4, NK = a.F / 256;
-    // the next step's activation rows land while this step is multiplied: the
-    // direct-to-LDS loads are untracked by the compiler (a tracked one makes
-    // every LDS read of the current step wait for them); the wait at the top
-    // of each step covers them
-    auto stage = [&](int kb) {
-        const uint32_t buf = lds_addr(d16s + (kb & 1) * kPfTile);
+    const int NK = a.F / 256;
+    struct Item { int p0, n, row; const uint8_t *drow; bool ok; };
+    auto item_at = [&](int u) {
+        Item it;
+        const int tl = u / nrb, tile = x * per + tl;
+        it.ok = u < n_u && tile < nt;
+        const int4 t4 = *(const int4 *)(a.tiles + 4 * (it.ok ? tile : 0));
+        const bool shared = t4.x == a.E;
+        const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)t4.x * a.stride;
+        const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
+        it.p0 = t4.y; it.n = t4.z;
+        it.row = (u - tl * nrb) * (32 * kPfDownWaves) + 32 * wave + col;   // rows row, row + 16
+        it.drow = blob + down_off + (uint64_t)it.row * db;
+        return it;
+    };
+    // a step's activation rows land while the previous step is multiplied:
+    // the direct-to-LDS loads are untracked by the compiler (a tracked one
+    // makes every LDS read of the current step wait for them); the wait at
+    // the top of each step covers them
+    auto stage = [&](const Item &it, int kb, int buf_i) {
+        const uint32_t buf = lds_addr(d16s + buf_i * kPfTile);
+        const int nb = (it.n + 15) >> 4;
         for (int q = wave; q < nb * 8; q += kPfDownWaves) {
             const int m = 2 * q + (lane >> 5), cs = lane & 31;
             const int c = cs ^ (m & 15);
-            const uint16_t *src = a.act_hi + (uint64_t)(p0 + (m < n ? m : 0)) * a.F + kb * 256 + 8 * c;
+            const uint16_t *src = a.act_hi + (uint64_t)(it.p0 + (m < it.n ? m : 0)) * a.F + kb * 256 + 8 * c;
             dma16_untracked(src, buf + q * 1024);
         }
     };
@@ -911,30 +914,38 @@ __global__ __launch_bounds__(kPfDownWaves * 64, 1) void k_pf_down16(PrefillArgs 
             r[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, pw[i]) + m1056) * ds2);
         return __builtin_bit_cast(f16x8, r);
     };
-    // the token-block count is a compile-time constant of the loop (fewer
-    // live registers for small tiles: no spill reloads, whose waits would
-    // also wait for the next step's loads)
-    auto run = [&](auto NBC) {
+    int u = blockIdx.x >> 3;
+    Item cur = item_at(u);
+    if (!cur.ok) return;
+    int gs = 0;                                       // steps done: LDS buffer gs & 1
+    stage(cur, 0, 0);
+    D::Sb s0_next = D::load(cur.drow, kg), s1_next = D::load(cur.drow + 16 * db, kg);
+    // the token-block count is a compile-time constant of an item's steps
+    // (fewer live registers for small tiles: no spill reloads, whose waits
+    // would also wait for the next step's loads); the last step requests the
+    // next item's first
+    auto run = [&](auto NBC, const Item &nxt) {
         constexpr int NB = decltype(NBC)::value;
         f32x4 acc[2][NB];
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int b = 0; b < NB; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
-        stage(0);
-        auto s0_next = D::load(drow, kg);
-        auto s1_next = D::load(drow1, kg);
         for (int kb = 0; kb < NK; kb++) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             const auto s0 = s0_next;
             const auto s1 = s1_next;
             if (kb + 1 < NK) {
-                stage(kb + 1);
-                s0_next = D::load(drow + (uint64_t)(kb + 1) * D::BLOCK, kg);
-                s1_next = D::load(drow1 + (uint64_t)(kb + 1) * D::BLOCK, kg);
+                stage(cur, kb + 1, (gs + 1) & 1);
+                s0_next = D::load(cur.drow + (uint64_t)(kb + 1) * D::BLOCK, kg);
+                s1_next = D::load(cur.drow + 16 * db + (uint64_t)(kb + 1) * D::BLOCK, kg);
+            } else if (nxt.ok) {
+                stage(nxt, 0, (gs + 1) & 1);
+                s0_next = D::load(nxt.drow, kg);
+                s1_next = D::load(nxt.drow + 16 * db, kg);
             }
-            const uint16_t *xh = d16s + (kb & 1) * kPfTile;
+            const uint16_t *xh = d16s + (gs & 1) * kPfTile;
 #pragma unroll
             for (int ch = 0; ch < 8; ch++) {
                 const f16x8 b0 = dec(s0, ch), b1 = dec(s1, ch);
@@ -945,26 +956,33 @@ __global__ __launch_bounds__(kPfDownWaves * 64, 1) void k_pf_down16(PrefillArgs 
                     acc[1][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[1][b], 0, 0, 0);
                 }
             }
+            gs++;
         }
 #pragma unroll
         for (int b = 0; b < NB; b++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = 16 * b + 4 * kg + i;
-                if (m < n) {
-                    const int sx = a.pexp[p0 + m];
+                if (m < cur.n) {
+                    const int sx = a.pexp[cur.p0 + m];
 #pragma unroll
                     for (int h = 0; h < 2; h++)
-                        a.outp[(uint64_t)(p0 + m) * a.H + row + 16 * h] = ldexpf(acc[h][b][i], sx);
+                        a.outp[(uint64_t)(cur.p0 + m) * a.H + cur.row + 16 * h] = ldexpf(acc[h][b][i], sx);
                 }
             }
         }
     };
-    switch (nb) {
-        case 1: run(std::integral_constant<int, 1>{}); break;
-        case 2: run(std::integral_constant<int, 2>{}); break;
-        case 3: run(std::integral_constant<int, 3>{}); break;
-        default: run(std::integral_constant<int, 4>{}); break;
+    for (;;) {
+        u += G8;
+        const Item nxt = item_at(u);
+        switch ((cur.n + 15) >> 4) {
+            case 1: run(std::integral_constant<int, 1>{}, nxt); break;
+            case 2: run(std::integral_constant<int, 2>{}, nxt); break;
+            case 3: run(std::integral_constant<int, 3>{}, nxt); break;
+            default: run(std::integral_constant<int, 4>{}, nxt); break;
+        }
+        if (!nxt.ok) break;
+        cur = nxt;
     }
 }
 #pragma clang fp contract(on)
@@ -1100,7 +1118,9 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
                 d16_attr = true;
             }
             k_pf_actprep<<<prefill_pairs(a.T, a.k, a.shared != nullptr), 256, 0, s>>>(a);
-            k_pf_down16<<<grid, kPfDownWaves * 64, lds16, s>>>(a);
+            int dev = 0, n_cu = 256;
+            if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+            k_pf_down16<<<(n_cu + 7) & ~7, kPfDownWaves * 64, lds16, s>>>(a);   // persistent, one per CU
         } else if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
         else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
     }
