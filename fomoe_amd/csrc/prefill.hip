@@ -850,14 +850,15 @@ __global__ __launch_bounds__(256) void k_pf_actprep(PrefillArgs a) {
 // prefill against 0.817 ms for one work-group per item; that kernel, 341 µs,
 // against 358 µs for two work-groups per CU at 128 VGPRs, whose spill
 // reloads waited for every outstanding load).
-__global__ __launch_bounds__(kPfDownWaves * 64, 1) void k_pf_down16(PrefillArgs a) {
+constexpr int kPfD16Waves = 8, kPfD16PerCU = 1;   // waves per work-group (32 rows each), work-groups per CU
+__global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) void k_pf_down16(PrefillArgs a) {
     using D = PfDec<GGML_TYPE_Q6_K>;
     extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x tile
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), col = lane & 15, kg = lane >> 4;
     // items (tile, block of 256 rows) of this work-group's XCD (work-group i
     // runs on XCD i % 8; the XCD's contiguous range of ceil(n_tiles / 8)
     // tiles, so an expert's tiles share one L2): u = i / 8, + G8, ...
-    const int nt = *a.n_tiles, nrb = a.H / (32 * kPfDownWaves);
+    const int nt = *a.n_tiles, nrb = a.H / (32 * kPfD16Waves);
     const int x = blockIdx.x & 7, G8 = gridDim.x >> 3, per = (nt + 7) >> 3, n_u = per * nrb;
     const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
     const int NK = a.F / 256;
@@ -871,7 +872,7 @@ __global__ __launch_bounds__(kPfDownWaves * 64, 1) void k_pf_down16(PrefillArgs 
         const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)t4.x * a.stride;
         const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
         it.p0 = t4.y; it.n = t4.z;
-        it.row = (u - tl * nrb) * (32 * kPfDownWaves) + 32 * wave + col;   // rows row, row + 16
+        it.row = (u - tl * nrb) * (32 * kPfD16Waves) + 32 * wave + col;   // rows row, row + 16
         it.drow = blob + down_off + (uint64_t)it.row * db;
         return it;
     };
@@ -882,7 +883,7 @@ __global__ __launch_bounds__(kPfDownWaves * 64, 1) void k_pf_down16(PrefillArgs 
     auto stage = [&](const Item &it, int kb, int buf_i) {
         const uint32_t buf = lds_addr(d16s + buf_i * kPfTile);
         const int nb = (it.n + 15) >> 4;
-        for (int q = wave; q < nb * 8; q += kPfDownWaves) {
+        for (int q = wave; q < nb * 8; q += kPfD16Waves) {
             const int m = 2 * q + (lane >> 5), cs = lane & 31;
             const int c = cs ^ (m & 15);
             const uint16_t *src = a.act_hi + (uint64_t)(it.p0 + (m < it.n ? m : 0)) * a.F + kb * 256 + 8 * c;
@@ -1054,7 +1055,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
                      (a.down_type == GGML_TYPE_Q4_K || a.down_type == GGML_TYPE_Q6_K);
     const int W = (a.T + 31) / 32;
     if (!okt || a.T <= 0 || a.E <= 0 || a.E > 1023 || a.k <= 0 || a.k > a.E || a.k > kMaxK ||
-        a.H <= 0 || a.H % 256 || a.H % (32 * kPfDownWaves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
+        a.H <= 0 || a.H % 256 || a.H % (32 * kPfDownWaves) || a.H % (32 * kPfD16Waves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
         a.max_tiles < prefill_max_tiles(a.T, a.k, a.E, a.shared != nullptr))
         return hipErrorInvalidValue;
     static bool router_attr = false;   // above the 64 KiB default of dynamic LDS
@@ -1120,7 +1121,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             k_pf_actprep<<<prefill_pairs(a.T, a.k, a.shared != nullptr), 256, 0, s>>>(a);
             int dev = 0, n_cu = 256;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-            k_pf_down16<<<(n_cu + 7) & ~7, kPfDownWaves * 64, lds16, s>>>(a);   // persistent, one per CU
+            k_pf_down16<<<(kPfD16PerCU * n_cu + 7) & ~7, kPfD16Waves * 64, lds16, s>>>(a);   // persistent
         } else if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
         else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
     }
