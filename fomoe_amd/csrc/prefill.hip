@@ -207,10 +207,26 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     const int off = block_exclusive_scan(cnt, scan_buf);   // pair offset of expert tid
     const int nt = (cnt + kPfMT - 1) / kPfMT;
     const int toff = block_exclusive_scan(nt, scan_buf);   // first tile of expert tid
+    // The GEMMs take tiles in decreasing cost: entry i's fourth word is the
+    // i-th tile by token-block count (4, 3, 2, 1; expert order within a
+    // count), so the last work handed out is the cheapest. Per expert: its
+    // full tiles (count 4) and its last, partial tile (count cb).
+    const int nfull = cnt / kPfMT, rem = cnt - kPfMT * nfull, cb = (rem + 15) >> 4;   // cb = 0: no partial tile
+    const int c4 = nfull + (cb == 4), c3 = cb == 3, c2 = cb == 2, c1 = cb == 1;
+    const int o43 = block_exclusive_scan(c4 | (c3 << 16), scan_buf);
+    const int o21 = block_exclusive_scan(c2 | (c1 << 16), scan_buf);
+    __shared__ int s_tot[2];
+    if (tid == 1023) { s_tot[0] = o43 + (c4 | (c3 << 16)); s_tot[1] = o21 + (c2 | (c1 << 16)); }
+    __syncthreads();
+    const int T4 = s_tot[0] & 0xFFFF, T3 = s_tot[0] >> 16, T2 = s_tot[1] & 0xFFFF;
+    const int b4 = o43 & 0xFFFF;                                 // this expert's first rank per count
+    const int bpart = cb == 4 ? b4 + nfull : cb == 3 ? T4 + (o43 >> 16)
+                    : cb == 2 ? T4 + T3 + (o21 & 0xFFFF) : T4 + T3 + T2 + (o21 >> 16);
     if (tid <= E) {
         for (int i = 0; i < nt; i++) {
             int32_t *tp = a.tiles + 4 * (toff + i);
-            tp[0] = tid; tp[1] = off + kPfMT * i; tp[2] = min(kPfMT, cnt - kPfMT * i); tp[3] = 0;
+            tp[0] = tid; tp[1] = off + kPfMT * i; tp[2] = min(kPfMT, cnt - kPfMT * i);
+            a.tiles[4 * (i < nfull ? b4 + i : bpart) + 3] = toff + i;
         }
     }
     if (tid == 1023) { a.n_tiles[0] = toff + nt; a.n_tiles[2] = 0; }   // [2]: k_pf_gateup_f16 work counter
@@ -599,7 +615,8 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
         __syncthreads();
         const int item = s_item;
         if (item >= n_items) break;
-        const int tile = item / nfg, fg = item - tile * nfg;
+        const int ti = item / nfg, fg = item - ti * nfg;
+        const int tile = a.tiles[4 * ti + 3];                    // tiles in decreasing cost
         const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
         const bool shared = tl.x == a.E;
         const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)tl.x * a.stride;
@@ -856,18 +873,20 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x tile
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), col = lane & 15, kg = lane >> 4;
     // items (tile, block of 256 rows) of this work-group's XCD (work-group i
-    // runs on XCD i % 8; the XCD's contiguous range of ceil(n_tiles / 8)
-    // tiles, so an expert's tiles share one L2): u = i / 8, + G8, ...
+    // runs on XCD i % 8): the XCD takes every eighth tile in decreasing cost
+    // (the order k_pf_group records), so the XCDs get like work; its
+    // work-groups take its items u = i / 8, + G8, ..., the costliest first
     const int nt = *a.n_tiles, nrb = a.H / (32 * kPfD16Waves);
-    const int x = blockIdx.x & 7, G8 = gridDim.x >> 3, per = (nt + 7) >> 3, n_u = per * nrb;
+    const int x = blockIdx.x & 7, G8 = gridDim.x >> 3, per = (nt - x + 7) >> 3, n_u = per * nrb;
     const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
     const int NK = a.F / 256;
     struct Item { int p0, n, row; const uint8_t *drow; bool ok; };
     auto item_at = [&](int u) {
         Item it;
-        const int tl = u / nrb, tile = x * per + tl;
-        it.ok = u < n_u && tile < nt;
-        const int4 t4 = *(const int4 *)(a.tiles + 4 * (it.ok ? tile : 0));
+        const int tl = u / nrb;
+        it.ok = u < n_u;
+        const int tile = a.tiles[4 * (it.ok ? x + 8 * tl : 0) + 3];
+        const int4 t4 = *(const int4 *)(a.tiles + 4 * tile);
         const bool shared = t4.x == a.E;
         const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)t4.x * a.stride;
         const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
