@@ -812,3 +812,57 @@ def test_prefill_config5_sampled(gpu):
         # the decode layer is within ~1e-6 of exact; the prefill's own operand
         # rounding is <= 6.2e-4 per token (PF16_EXACT's measurement)
         assert inf_rel(got[t], dec) < 1.5e-3
+
+
+def test_stack_decode_norm_and_shared_gate(gpu):
+    """Stack decode with random RMSNorm weights and a shared-expert sigmoid
+    gate on every layer: four layers with F = 1024 (the LDS-staged down
+    kernel), three graph-replayed steps, bit-identical to the same layer calls
+    issued one by one and within TOL of the oracle's chained layers."""
+    from fomoe_amd import synthetic as S
+    from test_oracle import moe_desc
+    say("stack norm + shared gate")
+    shape = S.LayerShape(n_embd=1024, inter=1024, n_experts=40, k=5)
+    E, H, F, k = shape.n_experts, shape.n_embd, shape.inter, shape.k
+    n_layers, n_steps = 4, 3
+    layers = [S.build_layer(gpu, shape, l, seed=21, zipf_s=1.1) for l in range(n_layers)]
+    host = []
+    try:
+        for l, L in enumerate(layers):
+            norm_w = (0.5 + O.synth_f32(21, S.stream(l, 0, 9), 0.25, H) ** 2).astype(np.float32)
+            gvec = O.synth_f32(21, S.stream(l, 0, 10), 0.05, H)
+            dn, dg = gpu.upload(norm_w), gpu.upload(gvec)
+            L.buffers += [dn, dg]
+            L.desc.norm_w, L.desc.shared_gate_vec = dn.ptr, dg.ptr
+            router = O.synth_f32(21, S.stream(l, 0, S.ROUTER), 0.02, E * H)
+            experts = gpu.download(L.desc.experts, np.uint8, (E + 1) * shape.stride)
+            bias = O.zipf_bias(21, S.stream(l, 0, S.ZIPF), E, 1.1)
+            d = moe_desc(E, k, H, F, router, experts, shape.gate_size, shape.down_size,
+                         shared_off=E * shape.stride, bias=bias, norm_w=norm_w, gvec=gvec)
+            d.expert_stride = shape.stride
+            host.append((d, router, experts, bias, norm_w, gvec))   # d points into the arrays
+        descs = [L.desc for L in layers]
+        x0 = O.synth_f32(22, 0, 1.0, H)
+        dx = gpu.upload(x0)
+        gpu.stack_decode(descs, dx, n_steps)
+        gpu.sync()
+        got = gpu.download(dx, np.float32, H)
+        dy = gpu.upload(x0)
+        for _ in range(n_steps):
+            for l in range(n_layers):
+                gpu.moe_layer(descs[l], dy, dy, O.MOE_NORM | O.MOE_RESIDUAL)
+        calls = gpu.download(dy, np.float32, H)
+        dx.free()
+        dy.free()
+        assert np.array_equal(got.view(np.uint32), calls.view(np.uint32))
+        x = x0.copy()
+        for _ in range(n_steps):
+            for l in range(n_layers):
+                x, _, _ = O.moe_layer(host[l][0], x, O.MOE_NORM | O.MOE_RESIDUAL)
+        e = parity_err(got, x)
+        say(f"  parity_err {e:.3e}")
+        assert e <= TOL
+    finally:
+        for L in layers:
+            for b in L.buffers:
+                b.free()
