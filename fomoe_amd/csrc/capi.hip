@@ -90,7 +90,7 @@ void gpu_free(gpu_ctx_t *c) {
     void *bufs[] = {c->logits, c->counter, c->ids, c->weights, c->xq_h, c->xq_act, c->act,
                     c->act2, c->vec_in, c->vec_out, c->staging, c->pf_logits, c->pf_ids,
                     c->pf_w, c->pf_pairpos, c->pf_pairtok, c->pf_tiles, c->pf_ntiles,
-                    c->pf_act, c->pf_outp, c->pf_xsum};
+                    c->pf_act, c->pf_outp, c->pf_xsum, c->pf_rsplit};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     for (int b = 0; b < 2; b++) {
@@ -604,6 +604,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
     HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * P * F));
     HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
+    HIPC(ensure(ctx->pf_rsplit, ctx->pf_rsplit_cap, sizeof(uint16_t) * fo::prefill_router_ws_elems(E, Tc, H)));
     // xsum [Tc x H/32] fp32, then x16 [Tc x H] fp16, then xexp [Tc] int32, then pexp [P] int32
     const size_t xs_bytes = sizeof(float) * (size_t)Tc * (H / 32), x16_bytes = 2 * (size_t)Tc * H;
     HIPC(ensure(ctx->pf_xsum, ctx->pf_xsum_cap, xs_bytes + x16_bytes + sizeof(int32_t) * ((size_t)Tc + P)));
@@ -623,6 +624,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.x16 = (uint16_t *)((uint8_t *)ctx->pf_xsum + xs_bytes);
     a.xexp = (int32_t *)((uint8_t *)ctx->pf_xsum + xs_bytes + x16_bytes);
     a.pexp = a.xexp + Tc;
+    a.rsplit = ctx->pf_rsplit;
     for (int t0 = 0; t0 < T; t0 += Tc) {
         const int n = std::min(Tc, T - t0);
         a.T = n;

@@ -48,6 +48,7 @@ struct gpu_ctx {
     uint16_t *pf_act = nullptr;    size_t pf_act_cap = 0;   // hi plane then lo plane
     float *pf_outp = nullptr;      size_t pf_outp_cap = 0;
     float *pf_xsum = nullptr;      size_t pf_xsum_cap = 0;
+    uint16_t *pf_rsplit = nullptr; size_t pf_rsplit_cap = 0;   // bf16 router GEMM operands
     int pf_T = 0, pf_k = 0;
 
     // pinned staging for host->device uploads of expert stores

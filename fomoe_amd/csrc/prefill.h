@@ -45,12 +45,19 @@ struct PrefillArgs {
     int32_t *xexp;               // [T] per-token power-of-two scale of x16
     float *outp;                 // [P x H] fp32, per-pair down output
     int32_t *pexp;               // [P] power-of-two scale of the fp16 activation rows (Q6_K down)
+    uint16_t *rsplit;            // bf16 router GEMM operands (prefill_router_ws_elems)
 };
 
 // Number of pair slots and an upper bound on the GEMM tiles for T tokens.
 inline int prefill_pairs(int T, int k, bool shared) { return T * (k + (shared ? 1 : 0)); }
 inline int prefill_max_tiles(int T, int k, int E, bool shared) {
     return (prefill_pairs(T, k, shared) + kPfMT - 1) / kPfMT + E + (shared ? 1 : 0);
+}
+
+// Workspace of the bf16 router GEMM (rsplit, uint16 elements): the router's
+// three bf16 terms and the token rows, in 32-row x 64-value chunks.
+inline uint64_t prefill_router_ws_elems(int E, int T, int H) {
+    return ((uint64_t)3 * ((E + 31) / 32) + (uint64_t)((T + 31) / 32)) * 32 * H;
 }
 
 hipError_t launch_prefill(const PrefillArgs &a, hipStream_t s);

@@ -35,6 +35,7 @@
 // (oracle/oracle.c fo_moe_prefill: bf16 weights, fp32 activation).
 #include <float.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -144,6 +145,141 @@ __global__ __launch_bounds__(256) void k_pf_router(PrefillArgs a) {
     }
 }
 
+// The router GEMM on bf16 MFMA (H % 512 == 0). The tokens are bf16 already;
+// each fp32 router weight w is written as three bf16 terms hi = bf16(w),
+// mid = bf16(w - hi), lo = bf16(w - hi - mid) (each subtraction exact; hi +
+// mid + lo = w to within 2^-24 |w|), so every product x * term is exact in
+// fp32 and v_mfma_f32_32x32x16_bf16 accumulates the three partial GEMMs in
+// fp32 — fp32-level products at the bf16 matrix rate.
+//
+// Operand layout (k_pf_rtile, once per call): a 32-row x 64-value block of x
+// or of one router term is a 4 KiB chunk ordered [q][lane][8 values], lane
+// (r = lane % 32, h = lane / 32) holding values 32h + 8q .. +7 of row r, so
+// every load instruction of the GEMM reads 1 KiB contiguous (per-lane 16-byte
+// pieces of 32 different rows touch 32-64 cache lines per instruction and
+// left the router GEMM bound by the address unit: 30-36 us). MFMA q of a
+// block takes the lane's piece q on both operands (the same K permutation on
+// A and B leaves the sum unchanged). Chunks: x [T/32][H/64], router
+// [E/32][H/64][3 terms]; rows past T or E are zero.
+//
+// k_pf_router3: 32 tokens x 32 experts per work-group, eight waves, each over
+// an eighth of the K blocks, two blocks in flight ahead of the one
+// multiplied; the eight partial tiles are summed in wave order at the end.
+constexpr int kR3Waves = 8, kR3Ahead = 2;
+
+// One thread per 16-byte piece of the chunks: consecutive threads write
+// consecutive pieces, each reading its 8 values (32 bytes of router, 16 of
+// x) from its row. (Row-contiguous reads with scattered 16-byte writes, or a
+// per-tile transpose through LDS, measured slower: 25 and 15 us against 9.)
+__global__ void k_pf_rtile(PrefillArgs a) {
+    const int NB = a.H / 64, ET = (a.E + 31) / 32, TT = (a.T + 31) / 32;
+    const uint64_t nr = (uint64_t)ET * NB * 256, nx = (uint64_t)TT * NB * 256;   // 16-byte pieces
+    uint4 *xt = (uint4 *)(a.rsplit + (uint64_t)3 * ET * 32 * a.H);
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nr + nx; i += (uint64_t)gridDim.x * blockDim.x) {
+        const bool isx = i >= nr;
+        const uint64_t pi = isx ? i - nr : i;
+        const uint64_t chunk = pi >> 8;                  // (row tile, K block)
+        const int q = (int)((pi >> 6) & 3), lane = (int)(pi & 63);
+        const int kb = (int)(chunk % NB), tile = (int)(chunk / NB);
+        const int row = 32 * tile + (lane & 31), k = 64 * kb + 32 * (lane >> 5) + 8 * q;
+        if (isx) {
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (row < a.T) v = *(const uint4 *)(a.x + (uint64_t)row * a.H + k);
+            xt[pi] = v;
+        } else {
+            float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (row < a.E) {
+                const float4 v0 = *(const float4 *)(a.router + (uint64_t)row * a.H + k);
+                const float4 v1 = *(const float4 *)(a.router + (uint64_t)row * a.H + k + 4);
+                f[0] = v0.x; f[1] = v0.y; f[2] = v0.z; f[3] = v0.w;
+                f[4] = v1.x; f[5] = v1.y; f[6] = v1.z; f[7] = v1.w;
+            }
+            uint32_t t[3][4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                uint32_t hw[3] = {0, 0, 0};
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const float fv = f[2 * p + e];
+                    const __bf16 th = (__bf16)fv;
+                    const float r1 = fv - (float)th;
+                    const __bf16 tm = (__bf16)r1;
+                    const __bf16 tl = (__bf16)(r1 - (float)tm);
+                    hw[0] |= (uint32_t)__builtin_bit_cast(uint16_t, th) << (16 * e);
+                    hw[1] |= (uint32_t)__builtin_bit_cast(uint16_t, tm) << (16 * e);
+                    hw[2] |= (uint32_t)__builtin_bit_cast(uint16_t, tl) << (16 * e);
+                }
+#pragma unroll
+                for (int j = 0; j < 3; j++) t[j][p] = hw[j];
+            }
+            uint4 *rt = (uint4 *)a.rsplit + (chunk * 3) * 256 + (pi & 255);
+#pragma unroll
+            for (int j = 0; j < 3; j++) rt[j * 256] = make_uint4(t[j][0], t[j][1], t[j][2], t[j][3]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(64 * kR3Waves) void k_pf_router3(PrefillArgs a) {
+    __shared__ float red[kR3Waves - 1][16][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int NB = a.H / 64, ET = (a.E + 31) / 32;
+    const int t0 = blockIdx.y * kRT, e0 = blockIdx.x * kRT;
+    const int r = lane & 31, h = lane >> 5;
+    const int nb = NB / kR3Waves, kb0 = wv * nb;
+    const uint4 *xc = (const uint4 *)(a.rsplit + (uint64_t)3 * ET * 32 * a.H) + ((uint64_t)blockIdx.y * NB + kb0) * 256 + lane;
+    const uint4 *wc = (const uint4 *)a.rsplit + ((uint64_t)blockIdx.x * NB + kb0) * 768 + lane;
+    struct Blk { uint4 x[4], w[3][4]; };
+    auto fetch = [&](Blk &b, int i) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) b.x[q] = xc[i * 256 + 64 * q];
+#pragma unroll
+        for (int j = 0; j < 3; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) b.w[j][q] = wc[i * 768 + j * 256 + 64 * q];
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0.f;
+    Blk ring[kR3Ahead + 1];
+#pragma unroll
+    for (int i = 0; i < kR3Ahead; i++)
+        if (i < nb) fetch(ring[i], i);
+    for (int i0 = 0; i0 < nb; i0 += kR3Ahead + 1) {
+#pragma unroll
+        for (int u = 0; u <= kR3Ahead; u++) {   // ring slot u: block i0 + u
+            const int i = i0 + u;
+            if (i >= nb) break;
+            if (i + kR3Ahead < nb) fetch(ring[(u + kR3Ahead) % (kR3Ahead + 1)], i + kR3Ahead);
+            const Blk &b = ring[u];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const bf16x8 xa = __builtin_bit_cast(bf16x8, b.x[q]);
+#pragma unroll
+                for (int j = 2; j >= 0; j--)   // lo, mid, hi
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, __builtin_bit_cast(bf16x8, b.w[j][q]), acc, 0, 0, 0);
+            }
+        }
+    }
+    // D layout: lane holds rows 8 (i / 4) + 4 (lane / 32) + i % 4 (tokens) of column lane % 32
+    if (wv > 0) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) red[wv - 1][i][lane] = acc[i];
+    }
+    __syncthreads();
+    if (wv == 0) {
+        const int e = e0 + r;
+        const float bias = (a.router_bias && e < a.E) ? a.router_bias[e] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float v = acc[i];
+#pragma unroll
+            for (int w = 0; w < kR3Waves - 1; w++) v += red[w][i][lane];
+            const int t = t0 + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (t < a.T && e < a.E) a.logits[(uint64_t)t * a.E + e] = v + bias;
+        }
+    }
+}
+
 // ============================================================ P2 top-k
 __global__ __launch_bounds__(256) void k_pf_topk(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
@@ -170,18 +306,21 @@ __global__ __launch_bounds__(256) void k_pf_topk(PrefillArgs a) {
 constexpr int kPfGroupLds = 16384;     // E*W words of each table
 
 FO_DEV int block_exclusive_scan(int v, int *buf) {   // 1024 threads, returns exclusive prefix
-    const int tid = threadIdx.x;
-    buf[tid] = v;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int add = tid >= o ? buf[tid - o] : 0;
-        __syncthreads();
-        buf[tid] += add;
-        __syncthreads();
+    // inclusive scan within each wave by shuffles, then the 16 wave totals
+    // (buf[0..15]) scanned by every thread: two barriers per scan
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
     }
-    const int incl = buf[tid];
+    if (lane == 63) buf[wv] = x;
     __syncthreads();
-    return incl - v;
+    int base = 0;
+    for (int w = 0; w < wv; w++) base += buf[w];
+    __syncthreads();                                 // buf is free for the next scan
+    return base + x - v;
 }
 
 __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
@@ -1008,18 +1147,21 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
 #pragma clang fp contract(on)
 
 // ============================================================ P6 combine
-// One work-group per token; each thread owns float4 columns and requests all
+// One work-group per (token, kCombCols columns); each thread owns float4 columns and requests all
 // of the token's pair rows for a column before summing them in rank order.
+constexpr int kCombCols = 1024;   // columns of one token per work-group
+
 __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
     __shared__ int s_pp[kMaxK + 1];
     __shared__ float s_w[kMaxK + 1];
     const int t = blockIdx.x, K1 = a.k + 1, n = a.k + (a.shared ? 1 : 0);
+    const int c0 = blockIdx.y * kCombCols / 4, c1 = min(a.H / 4, c0 + kCombCols / 4);   // float4 columns
     if ((int)threadIdx.x < K1) {
         s_pp[threadIdx.x] = a.pairpos[(uint64_t)t * K1 + threadIdx.x];
         s_w[threadIdx.x] = a.w[(uint64_t)t * K1 + threadIdx.x];
     }
     __syncthreads();
-    for (int i4 = threadIdx.x; i4 < a.H / 4; i4 += 256) {
+    for (int i4 = c0 + threadIdx.x; i4 < c1; i4 += 256) {
         float4 o[kMaxK + 1];
 #pragma unroll
         for (int r = 0; r <= kMaxK; r++)
@@ -1077,14 +1219,20 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         a.H <= 0 || a.H % 256 || a.H % (32 * kPfDownWaves) || a.H % (32 * kPfD16Waves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
         a.max_tiles < prefill_max_tiles(a.T, a.k, a.E, a.shared != nullptr))
         return hipErrorInvalidValue;
-    static bool router_attr = false;   // above the 64 KiB default of dynamic LDS
-    if (!router_attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_pf_router, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)kRLds);
-        if (e != hipSuccess) return e;
-        router_attr = true;
+    if (a.H % (64 * kR3Waves) == 0 && a.rsplit) {
+        const uint64_t pieces = prefill_router_ws_elems(a.E, a.T, a.H) / 8;   // upper bound
+        k_pf_rtile<<<(unsigned)std::min<uint64_t>((pieces + 255) / 256, 8192), 256, 0, s>>>(a);
+        k_pf_router3<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 64 * kR3Waves, 0, s>>>(a);
+    } else {
+        static bool router_attr = false;   // above the 64 KiB default of dynamic LDS
+        if (!router_attr) {
+            hipError_t e = hipFuncSetAttribute((const void *)k_pf_router, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)kRLds);
+            if (e != hipSuccess) return e;
+            router_attr = true;
+        }
+        k_pf_router<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 256, kRLds, s>>>(a);
     }
-    k_pf_router<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 256, kRLds, s>>>(a);
     k_pf_topk<<<(a.T + 3) / 4, 256, 0, s>>>(a);
     static bool lds_attr = false;   // the grouping tables may exceed the 64 KiB default
     if (!lds_attr) {
@@ -1144,7 +1292,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         } else if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
         else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
     }
-    k_pf_combine<<<a.T, 256, 0, s>>>(a);
+    k_pf_combine<<<dim3(a.T, (a.H + kCombCols - 1) / kCombCols), 256, 0, s>>>(a);
     return hipGetLastError();
 }
 
