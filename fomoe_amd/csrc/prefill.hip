@@ -691,6 +691,53 @@ __global__ __launch_bounds__(256) void k_pf_xprep(PrefillArgs a) {
     if (tid == 0) a.xexp[t] = sx;
 }
 
+// k_pf_xprep with one wave per token (H % 2048 == 0): lane l owns values
+// V l .. V l + V - 1 (V = H / 64, whole 32-value sub-blocks), so the same
+// maximum, scale and sequential sub-block sums as k_pf_xprep come out of
+// shuffles and registers instead of barriers and 2-byte loads; the row is
+// read twice (the second time from the caches).
+constexpr int kXpWaves = 4;
+
+__global__ __launch_bounds__(64 * kXpWaves) void k_pf_xprep_w(PrefillArgs a) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * kXpWaves + (threadIdx.x >> 6);
+    if (t >= a.T) return;
+    const int H = a.H, V = H / 64, nc = V / 8;          // 16-byte chunks per lane
+    const uint16_t *xr = a.x + (uint64_t)t * H + (uint64_t)lane * V;
+    float m = 0.f;
+    for (int c = 0; c < nc; c++) {
+        const uint4 w = *(const uint4 *)(xr + 8 * c);
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) m = fmaxf(m, fmaxf(fabsf(bf2f(u[i] & 0xFFFFu)), fabsf(bf2f(u[i] >> 16))));
+    }
+    m = wave_max(m);
+    int E = 0;
+    frexpf(m, &E);                                         // 2^(E-1) <= m < 2^E (m finite, nonzero)
+    const int sx = E - 15;
+    uint16_t *x16 = a.x16 + (uint64_t)t * H + (uint64_t)lane * V;
+    float *xs = a.xsum + (uint64_t)t * (H / 32) + lane * (V / 32);
+    float sum = 0.f;
+    for (int c = 0; c < nc; c++) {
+        const uint4 w = *(const uint4 *)(xr + 8 * c);
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float f0 = bf2f(u[i] & 0xFFFFu), f1 = bf2f(u[i] >> 16);
+            sum = sum + f0;
+            sum = sum + f1;
+            o[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)ldexpf(f0, -sx)) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)ldexpf(f1, -sx)) << 16);
+        }
+        *(uint4 *)(x16 + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+        if ((c & 3) == 3) {
+            xs[c >> 2] = ldexpf(sum, -sx);
+            sum = 0.f;
+        }
+    }
+    if (lane == 0) a.xexp[t] = sx;
+}
+
 // 6-bit (scale, min) of sub-block j from the 12 scale bytes (words y, z, w
 // of a Q4_K header; reference src/quant.c:72-80)
 FO_DEV void q4_scale_min(const uint4 &hdr, int j, uint32_t &sc, uint32_t &mn) {
@@ -959,37 +1006,49 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
 }
 
 // ------------------------------------------------------------ Q6_K down on fp16 operands
-// Activation prep, one work-group per pair row: v = hi + lo (the fp32 SwiGLU
-// value as the gate/up kernels store it, exactly), s = the power of two that
-// brings max|v| into [2^14, 2^15), and the row is rewritten in place (over the
-// hi plane) as fp16(v * 2^-s); s goes to pexp.
-__global__ __launch_bounds__(256) void k_pf_actprep(PrefillArgs a) {
-    __shared__ float red[4];
-    const int p = blockIdx.x, tid = threadIdx.x, F = a.F;
-    uint16_t *hi = a.act_hi + (uint64_t)p * F;
-    const uint16_t *lo = a.act_lo + (uint64_t)p * F;
-    constexpr int kMaxPer = 16;                            // F <= 4096
-    float v[kMaxPer];
+// Activation prep, one wave per pair row: v = hi + lo (the fp32 SwiGLU value
+// as the gate/up kernels store it, exactly), s = the power of two that brings
+// max|v| into [2^14, 2^15), and the row is rewritten in place (over the hi
+// plane) as fp16(v * 2^-s); s goes to pexp. Lane l owns values V l .. V l + V
+// - 1 (V = F / 64 <= 64), held in registers between the maximum (shuffles) and
+// the rewrite (was one 256-thread work-group per row: 14.6 against ~8 us).
+constexpr int kApWaves = 4;
+
+__global__ __launch_bounds__(64 * kApWaves) void k_pf_actprep_w(PrefillArgs a, int n_pairs) {
+    const int lane = threadIdx.x & 63, p = blockIdx.x * kApWaves + (threadIdx.x >> 6);
+    if (p >= n_pairs) return;
+    const int F = a.F, nc = F / 256;                       // 4-value chunks per lane
+    uint16_t *hi = a.act_hi + (uint64_t)p * F + (uint64_t)lane * 4 * nc;
+    const uint16_t *lo = a.act_lo + (uint64_t)p * F + (uint64_t)lane * 4 * nc;
+    constexpr int kMaxC = 16;                              // F <= 4096
+    float v[kMaxC][4];
     float m = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMaxPer; i++) {
-        const int j = tid + 256 * i;
-        v[i] = j < F ? bf2f(hi[j]) + bf2f(lo[j]) : 0.f;
-        m = fmaxf(m, fabsf(v[i]));
+    for (int c = 0; c < kMaxC; c++) {
+        if (c < nc) {
+            const uint2 h2 = *(const uint2 *)(hi + 4 * c), l2 = *(const uint2 *)(lo + 4 * c);
+            v[c][0] = bf2f(h2.x & 0xFFFFu) + bf2f(l2.x & 0xFFFFu);
+            v[c][1] = bf2f(h2.x >> 16) + bf2f(l2.x >> 16);
+            v[c][2] = bf2f(h2.y & 0xFFFFu) + bf2f(l2.y & 0xFFFFu);
+            v[c][3] = bf2f(h2.y >> 16) + bf2f(l2.y >> 16);
+#pragma unroll
+            for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(v[c][i]));
+        }
     }
     m = wave_max(m);
-    if ((tid & 63) == 0) red[tid >> 6] = m;
-    __syncthreads();                                       // every read of the row is done
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     int E = 0;
     frexpf(m, &E);
     const int sx = E - 15;
 #pragma unroll
-    for (int i = 0; i < kMaxPer; i++) {
-        const int j = tid + 256 * i;
-        if (j < F) hi[j] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(v[i], -sx));
+    for (int c = 0; c < kMaxC; c++) {
+        if (c < nc) {
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(v[c][i], -sx));
+            *(uint2 *)(hi + 4 * c) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+        }
     }
-    if (tid == 0) a.pexp[p] = sx;
+    if (lane == 0) a.pexp[p] = sx;
 }
 
 // The Q6_K down projection with B = fp16(q - 32) * fp16(d * sc) (one v_perm,
@@ -1245,7 +1304,8 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K) {   // exact fp16 operands
-        k_pf_xprep<<<a.T, 256, 0, s>>>(a);
+        if (a.H % 2048 == 0) k_pf_xprep_w<<<(a.T + kXpWaves - 1) / kXpWaves, 64 * kXpWaves, 0, s>>>(a);
+        else k_pf_xprep<<<a.T, 256, 0, s>>>(a);
         static bool gb_attr = false;   // above the 64 KiB default of dynamic LDS
         if (!gb_attr) {
             hipError_t e = hipFuncSetAttribute((const void *)k_pf_gateup_f16,
@@ -1285,7 +1345,8 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
                 if (e != hipSuccess) return e;
                 d16_attr = true;
             }
-            k_pf_actprep<<<prefill_pairs(a.T, a.k, a.shared != nullptr), 256, 0, s>>>(a);
+            const int np = prefill_pairs(a.T, a.k, a.shared != nullptr);
+            k_pf_actprep_w<<<(np + kApWaves - 1) / kApWaves, 64 * kApWaves, 0, s>>>(a, np);
             int dev = 0, n_cu = 256;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
             k_pf_down16<<<(kPfD16PerCU * n_cu + 7) & ~7, kPfD16Waves * 64, lds16, s>>>(a);   // persistent
