@@ -1,8 +1,10 @@
 // prefill.hip — the multi-token MoE path (512 tokens,
 // top-10 of 512 experts, Q4_K gate/up and Q6_K down).
 //
-//   P1 k_pf_router   logits[T x E] = x . W_r^T (+ bias), fp32 (x is bf16,
-//                    converted exactly), LDS-tiled 32 x 32 outputs per WG.
+//   P1 k_pf_router3  logits[T x E] = x . W_r^T (+ bias): bf16 MFMA on x (bf16)
+//                    and the fp32 router as three exact bf16 terms, operands
+//                    laid out by k_pf_rtile (k_pf_router, fp32 MFMA with LDS
+//                    staging, for H not a multiple of 512).
 //   P2 k_pf_topk     one wave per token: top-k with lowest-index ties and the
 //                    renormalised weights (topk.h), the shared-expert weight
 //                    sigmoid(x . v) or 1.
