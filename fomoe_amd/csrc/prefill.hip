@@ -173,11 +173,11 @@ constexpr int kR3Waves = 8, kR3Ahead = 2;
 // consecutive pieces, each reading its 8 values (32 bytes of router, 16 of
 // x) from its row. (Row-contiguous reads with scattered 16-byte writes, or a
 // per-tile transpose through LDS, measured slower: 25 and 15 us against 9.)
-__global__ void k_pf_rtile(PrefillArgs a) {
+FO_DEV void pf_rtile_body(const PrefillArgs &a, uint32_t blk, uint32_t nblk) {
     const int NB = a.H / 64, ET = (a.E + 31) / 32, TT = (a.T + 31) / 32;
     const uint64_t nr = (uint64_t)ET * NB * 256, nx = (uint64_t)TT * NB * 256;   // 16-byte pieces
     uint4 *xt = (uint4 *)(a.rsplit + (uint64_t)3 * ET * 32 * a.H);
-    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nr + nx; i += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t i = blk * (uint64_t)blockDim.x + threadIdx.x; i < nr + nx; i += (uint64_t)nblk * blockDim.x) {
         const bool isx = i >= nr;
         const uint64_t pi = isx ? i - nr : i;
         const uint64_t chunk = pi >> 8;                  // (row tile, K block)
@@ -220,6 +220,8 @@ __global__ void k_pf_rtile(PrefillArgs a) {
         }
     }
 }
+
+__global__ __launch_bounds__(256) void k_pf_rtile(PrefillArgs a) { pf_rtile_body(a, blockIdx.x, gridDim.x); }
 
 __global__ __launch_bounds__(64 * kR3Waves) void k_pf_router3(PrefillArgs a) {
     __shared__ float red[kR3Waves - 1][16][64];
@@ -700,8 +702,8 @@ __global__ __launch_bounds__(256) void k_pf_xprep(PrefillArgs a) {
 // read twice (the second time from the caches).
 constexpr int kXpWaves = 4;
 
-__global__ __launch_bounds__(64 * kXpWaves) void k_pf_xprep_w(PrefillArgs a) {
-    const int lane = threadIdx.x & 63, t = blockIdx.x * kXpWaves + (threadIdx.x >> 6);
+FO_DEV void pf_xprep_body(const PrefillArgs &a, uint32_t blk) {
+    const int lane = threadIdx.x & 63, t = blk * kXpWaves + (threadIdx.x >> 6);
     if (t >= a.T) return;
     const int H = a.H, V = H / 64, nc = V / 8;          // 16-byte chunks per lane
     const uint16_t *xr = a.x + (uint64_t)t * H + (uint64_t)lane * V;
@@ -738,6 +740,16 @@ __global__ __launch_bounds__(64 * kXpWaves) void k_pf_xprep_w(PrefillArgs a) {
         }
     }
     if (lane == 0) a.xexp[t] = sx;
+}
+
+__global__ __launch_bounds__(64 * kXpWaves) void k_pf_xprep_w(PrefillArgs a) { pf_xprep_body(a, blockIdx.x); }
+
+// The router operand layout and the token prep in one launch (neither reads
+// what the other writes): work-groups [0, n_rt) lay out the router GEMM's
+// operands, the rest prepare the tokens for the fp16 gate/up kernel.
+__global__ __launch_bounds__(256) void k_pf_prep(PrefillArgs a, uint32_t n_rt) {
+    if (blockIdx.x < n_rt) pf_rtile_body(a, blockIdx.x, n_rt);
+    else pf_xprep_body(a, blockIdx.x - n_rt);
 }
 
 // 6-bit (scale, min) of sub-block j from the 12 scale bytes (words y, z, w
@@ -1011,30 +1023,33 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
 // Activation prep, one wave per pair row: v = hi + lo (the fp32 SwiGLU value
 // as the gate/up kernels store it, exactly), s = the power of two that brings
 // max|v| into [2^14, 2^15), and the row is rewritten in place (over the hi
-// plane) as fp16(v * 2^-s); s goes to pexp. Lane l owns values V l .. V l + V
-// - 1 (V = F / 64 <= 64), held in registers between the maximum (shuffles) and
-// the rewrite (was one 256-thread work-group per row: 14.6 against ~8 us).
+// plane) as fp16(v * 2^-s); s goes to pexp. Lane l owns the 8-value chunks l,
+// l + 64, ... (every load and store instruction covers 1 KiB contiguous),
+// held in registers between the maximum (shuffles) and the rewrite.
 constexpr int kApWaves = 4;
 
 __global__ __launch_bounds__(64 * kApWaves) void k_pf_actprep_w(PrefillArgs a, int n_pairs) {
     const int lane = threadIdx.x & 63, p = blockIdx.x * kApWaves + (threadIdx.x >> 6);
     if (p >= n_pairs) return;
-    const int F = a.F, nc = F / 256;                       // 4-value chunks per lane
-    uint16_t *hi = a.act_hi + (uint64_t)p * F + (uint64_t)lane * 4 * nc;
-    const uint16_t *lo = a.act_lo + (uint64_t)p * F + (uint64_t)lane * 4 * nc;
-    constexpr int kMaxC = 16;                              // F <= 4096
-    float v[kMaxC][4];
+    const int F = a.F, nc = F / 8;                         // 8-value chunks; lane takes lane + 64 i
+    uint16_t *hi = a.act_hi + (uint64_t)p * F;
+    const uint16_t *lo = a.act_lo + (uint64_t)p * F;
+    constexpr int kMaxI = 8;                               // F <= 4096
+    float v[kMaxI][8];
     float m = 0.f;
 #pragma unroll
-    for (int c = 0; c < kMaxC; c++) {
+    for (int i = 0; i < kMaxI; i++) {
+        const int c = lane + 64 * i;
         if (c < nc) {
-            const uint2 h2 = *(const uint2 *)(hi + 4 * c), l2 = *(const uint2 *)(lo + 4 * c);
-            v[c][0] = bf2f(h2.x & 0xFFFFu) + bf2f(l2.x & 0xFFFFu);
-            v[c][1] = bf2f(h2.x >> 16) + bf2f(l2.x >> 16);
-            v[c][2] = bf2f(h2.y & 0xFFFFu) + bf2f(l2.y & 0xFFFFu);
-            v[c][3] = bf2f(h2.y >> 16) + bf2f(l2.y >> 16);
+            const uint4 h4 = *(const uint4 *)(hi + 8 * c), l4 = *(const uint4 *)(lo + 8 * c);
+            const uint32_t hw[4] = {h4.x, h4.y, h4.z, h4.w}, lw[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
-            for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(v[c][i]));
+            for (int q = 0; q < 4; q++) {
+                v[i][2 * q] = bf2f(hw[q] & 0xFFFFu) + bf2f(lw[q] & 0xFFFFu);
+                v[i][2 * q + 1] = bf2f(hw[q] >> 16) + bf2f(lw[q] >> 16);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) m = fmaxf(m, fabsf(v[i][e]));
         }
     }
     m = wave_max(m);
@@ -1042,12 +1057,15 @@ __global__ __launch_bounds__(64 * kApWaves) void k_pf_actprep_w(PrefillArgs a, i
     frexpf(m, &E);
     const int sx = E - 15;
 #pragma unroll
-    for (int c = 0; c < kMaxC; c++) {
+    for (int i = 0; i < kMaxI; i++) {
+        const int c = lane + 64 * i;
         if (c < nc) {
             uint32_t o[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = __builtin_bit_cast(uint16_t, (_Float16)ldexpf(v[c][i], -sx));
-            *(uint2 *)(hi + 4 * c) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+            for (int q = 0; q < 4; q++)
+                o[q] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)ldexpf(v[i][2 * q], -sx)) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)ldexpf(v[i][2 * q + 1], -sx)) << 16);
+            *(uint4 *)(hi + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
         }
     }
     if (lane == 0) a.pexp[p] = sx;
@@ -1280,9 +1298,17 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         a.H <= 0 || a.H % 256 || a.H % (32 * kPfDownWaves) || a.H % (32 * kPfD16Waves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
         a.max_tiles < prefill_max_tiles(a.T, a.k, a.E, a.shared != nullptr))
         return hipErrorInvalidValue;
+    const bool fp16_gateup = a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K;
+    bool xprep_done = false;
     if (a.H % (64 * kR3Waves) == 0 && a.rsplit) {
         const uint64_t pieces = prefill_router_ws_elems(a.E, a.T, a.H) / 8;   // upper bound
-        k_pf_rtile<<<(unsigned)std::min<uint64_t>((pieces + 255) / 256, 8192), 256, 0, s>>>(a);
+        const unsigned n_rt = (unsigned)std::min<uint64_t>((pieces + 255) / 256, 8192);
+        if (fp16_gateup && a.H % 2048 == 0) {
+            k_pf_prep<<<n_rt + (a.T + kXpWaves - 1) / kXpWaves, 256, 0, s>>>(a, n_rt);
+            xprep_done = true;
+        } else {
+            k_pf_rtile<<<n_rt, 256, 0, s>>>(a);
+        }
         k_pf_router3<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 64 * kR3Waves, 0, s>>>(a);
     } else {
         static bool router_attr = false;   // above the 64 KiB default of dynamic LDS
@@ -1305,9 +1331,13 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
     k_pf_group<<<1, 1024, 2 * (size_t)a.E * W * sizeof(uint32_t), s>>>(a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    if (a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K) {   // exact fp16 operands
-        if (a.H % 2048 == 0) k_pf_xprep_w<<<(a.T + kXpWaves - 1) / kXpWaves, 64 * kXpWaves, 0, s>>>(a);
-        else k_pf_xprep<<<a.T, 256, 0, s>>>(a);
+    if (fp16_gateup) {   // exact fp16 operands
+        if (xprep_done) {
+        } else if (a.H % 2048 == 0) {
+            k_pf_xprep_w<<<(a.T + kXpWaves - 1) / kXpWaves, 64 * kXpWaves, 0, s>>>(a);
+        } else {
+            k_pf_xprep<<<a.T, 256, 0, s>>>(a);
+        }
         static bool gb_attr = false;   // above the 64 KiB default of dynamic LDS
         if (!gb_attr) {
             hipError_t e = hipFuncSetAttribute((const void *)k_pf_gateup_f16,
