@@ -280,8 +280,9 @@ void gpu_gguf_free_moe_layer(gpu_ctx_t *ctx, gpu_moe_layer_t *L);
  * n_tokens tokens through one MoE layer at once (async): d_x [n_tokens x
  * n_embd] bf16, d_out [n_tokens x n_embd] fp32 (= x + ffn with
  * GPU_MOE_RESIDUAL). Per token the semantics of gpu_moe_layer without the
- * norm (fp32 router on the bf16 input, softmax, top-k, renormalise, shared
- * expert); the expert GEMMs are grouped by expert and run on the matrix cores
+ * norm (fp32-level router on the bf16 input — bf16 matrix cores with each
+ * router weight as three exact bf16 terms when n_embd % 512 == 0, fp32 matrix
+ * cores otherwise —, softmax, top-k, renormalise, shared expert); the expert GEMMs are grouped by expert and run on the matrix cores
  * with fp32 accumulation. Operands: Q4_K gate/up weights exactly (fp16 sc*q,
  * the tokens as fp16 under a per-token power of two); a Q6_K down projection
  * as fp16(q - 32) * fp16(d * sc) against the SwiGLU activation as fp16 under
