@@ -331,9 +331,11 @@ __global__ __launch_bounds__(64) void k_matvec_q6k_tile(MatvecArgs a) {
     }
 }
 
-template <int NSB>
+// TPW = 4 tiles per wave: per-launch p50 0.7-2.2 % below TPW = 8 in same-box
+// alternating runs on two boxes (TPW = 2, 3 slower; 6 between)
+template <int NSB, int TPW = 4>
 static hipError_t matvec_q6k_tile(const MatvecArgs &a, hipStream_t s) {
-    constexpr int TPW = 8, K = NSB * 256;
+    constexpr int K = NSB * 256;
     const int ntiles = (a.M + kT6Rows - 1) / kT6Rows;
     const uint32_t lds = ((xq_bytes(K, 16) + 15) & ~15u) + kT6Zero +
                          ((kT6Rows * NSB * 210 + 15) & ~15u) + TPW * kT6Rows * 4;
