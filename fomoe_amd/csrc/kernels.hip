@@ -426,13 +426,17 @@ __global__ __launch_bounds__(64) void k_matvec_q80_mfma(MatvecArgs a) {
     }
 }
 
-static hipError_t matvec_q80_mfma(const MatvecArgs &a, hipStream_t s) {
-    constexpr int TPW = 8;
+// 4 tiles per wave (as the Q6_K tile kernel): per-launch p50 3 % (Q8_0) and 4 %
+// (Q5_K) below 8 tiles per wave in alternating same-box runs
+template <int TPW>
+static hipError_t matvec_q80_mfma_t(const MatvecArgs &a, hipStream_t s) {
     const int ntiles = (a.M + 15) / 16;
     const uint32_t lds = kQ8X + kQ8Zero + 16 * kQ8Row + TPW * 16 * 4;
     k_matvec_q80_mfma<TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
     return hipGetLastError();
 }
+
+static hipError_t matvec_q80_mfma(const MatvecArgs &a, hipStream_t s) { return matvec_q80_mfma_t<4>(a, s); }
 
 // ============================================================ Q5_K matvec, tile-staged MFMA (K = 1024)
 // The Q8_0 MFMA kernel's stream (one wave per work-group, 16-row tiles =
@@ -500,13 +504,16 @@ __global__ __launch_bounds__(64) void k_matvec_q5k_mfma(MatvecArgs a) {
     }
 }
 
-static hipError_t matvec_q5k_mfma(const MatvecArgs &a, hipStream_t s) {
-    constexpr int TPW = 8;
+// 4 tiles per wave: see matvec_q80_mfma_t
+template <int TPW>
+static hipError_t matvec_q5k_mfma_t(const MatvecArgs &a, hipStream_t s) {
     const int ntiles = (a.M + 15) / 16;
     const uint32_t lds = kQ5X + kQ5Zero + 16 * kQ5Row + TPW * 16 * 4;
     k_matvec_q5k_mfma<TPW><<<dim3((ntiles + TPW - 1) / TPW, a.n_mats), 64, lds, s>>>(a);
     return hipGetLastError();
 }
+
+static hipError_t matvec_q5k_mfma(const MatvecArgs &a, hipStream_t s) { return matvec_q5k_mfma_t<4>(a, s); }
 
 // ============================================================ Q4_K matvec, tile-staged MFMA
 // For Q4_K rows of K = 4096 (the expert gate/up shape). Four-wave work-groups
