@@ -43,6 +43,9 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+LEG_WARMUP = 50   # warmup steps of the rotation legs timed before the headline
+
+
 class Rotation:
     """n_mats distinct [M x K] matrices of type t (matrix m from stream m of
     wseed; matrix 0 is the BASELINE config's W) times one x, one launch per
@@ -72,8 +75,9 @@ class Rotation:
             self.launch()
         ms = self.gpu.timer_stop() / steps
         total = (self.rb + 4 * self.K + 4 * self.M) * self.n   # weights + x + y, each once per launch
-        self.res.update({"ms_per_step": ms, "bytes_per_step": total, "GB/s": total / ms / 1e6,
-                         "weight_bytes": self.rb * self.n, "frac_hbm": total / ms / 1e6 / HBM_PEAK_GBS})
+        self.res.update({"ms_per_step": ms, "steps": steps, "warmup": warmup, "bytes_per_step": total,
+                         "GB/s": total / ms / 1e6, "weight_bytes": self.rb * self.n,
+                         "frac_hbm": total / ms / 1e6 / HBM_PEAK_GBS})
 
     def spread(self, steps):
         each = []
@@ -371,6 +375,11 @@ def main():
     # any allocation), and idle gaps (weight generation, one-by-one timed
     # launches) between legs let it fall back. The headline gets its own W
     # warmup steps and exactly K timed steps; the per-launch spreads follow.
+    # The legs before it take at least LEG_WARMUP warmup steps (recorded in
+    # their own extra.* entries), so that ~55 ms of sustained load precede
+    # the headline's timed loop whatever W the caller passes (with W = 5 the
+    # three legs before it gave ~17 ms, and its 20 timed steps still ran on
+    # rising clocks: step mean 1-3 % above the per-launch median).
     legs = []
     if "q4k" not in skip:
         legs.append(("config1_q4k", "q4k", Rotation(gpu, FA.Q4_K, 1024, 4096, 0, 1, 512)))
@@ -384,7 +393,7 @@ def main():
     for name, _, r in legs:
         if r is q6r:
             t_wall = time.perf_counter()
-        r.timed(args.steps, args.warmup)
+        r.timed(args.steps, args.warmup if r is q6r else max(args.warmup, LEG_WARMUP))
         if r is q6r:
             wall_steps = time.perf_counter() - t_wall
         log(f"{name}: {r.res['GB/s']:.0f} GB/s ({r.res['frac_hbm'] * 100:.1f}% of HBM)")
