@@ -86,15 +86,8 @@ FO_DEV void group_scale_sum(float M, float chk, int e, int isum, float &scale, f
 // k_xprep uses one thread per group, the tile kernels one lane per group,
 // bit-identically.
 template <int GSZ>
-FO_DEV void prep_group_regs(const float *__restrict__ xp, int (&limb)[kLimbs][GSZ / 4], float &scale,
-                            float &sum) {
-    float vals[GSZ];
+FO_DEV void prep_group_vals(const float (&vals)[GSZ], int (&limb)[kLimbs][GSZ / 4], float &scale, float &sum) {
     float M = 0.f, chk = 0.f;
-#pragma unroll
-    for (int i = 0; i < GSZ; i += 4) {
-        float4 t = *(const float4 *)(xp + i);
-        vals[i] = t.x; vals[i + 1] = t.y; vals[i + 2] = t.z; vals[i + 3] = t.w;
-    }
 #pragma unroll
     for (int i = 0; i < GSZ; i++) { M = fmaxf(M, fabsf(vals[i])); chk += vals[i] * 0.f; }
     int E = 0;
@@ -124,6 +117,18 @@ FO_DEV void prep_group_regs(const float *__restrict__ xp, int (&limb)[kLimbs][GS
     for (int L = 0; L < kLimbs; L++)
 #pragma unroll
         for (int k = 0; k < GSZ / 4; k++) limb[L][k] = (int)lb[L][k];
+}
+
+template <int GSZ>
+FO_DEV void prep_group_regs(const float *__restrict__ xp, int (&limb)[kLimbs][GSZ / 4], float &scale,
+                            float &sum) {
+    float vals[GSZ];
+#pragma unroll
+    for (int i = 0; i < GSZ; i += 4) {
+        float4 t = *(const float4 *)(xp + i);
+        vals[i] = t.x; vals[i + 1] = t.y; vals[i + 2] = t.z; vals[i + 3] = t.w;
+    }
+    prep_group_vals<GSZ>(vals, limb, scale, sum);
 }
 
 // Load the groups gi[0..NG) of a prepared vector into registers.

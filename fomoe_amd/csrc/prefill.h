@@ -11,6 +11,7 @@
 namespace fo {
 
 constexpr int kPfMT = 64;        // tokens per GEMM tile (4 MFMA row blocks of 16)
+constexpr int kPfThin = 4;       // pairs of a thin tile (integer-MFMA Q6_K down path)
 constexpr int kPfGateWaves = 8;                   // gate/up work-group: 4 gate + 4 up waves (two per CU)
 constexpr int kPfGateRows = 32 * kPfGateWaves / 2; // F rows per gate/up work-group (32 per wave)
 
@@ -36,7 +37,7 @@ struct PrefillArgs {
     int32_t *pairpos;            // [T x (k+1)]: pair slot of (token, rank); rank k = shared
     int32_t *pair_tok;           // [P] token of each pair slot, grouped by expert
     int32_t *tiles;              // [max_tiles x 4] {expert (E = shared), first pair, n, 0}
-    int32_t *n_tiles;            // [3]: tiles, -, work counter of the gate/up kernel
+    int32_t *n_tiles;            // [3]: tiles, tiles before the thin ones, work counter of the gate/up kernel
     int max_tiles;
     uint16_t *act_hi, *act_lo;   // [P x F] SwiGLU activation as bf16 hi + lo terms (a Q6_K
                                  // down projection rewrites act_hi as fp16 rows, scale in pexp)
@@ -46,6 +47,7 @@ struct PrefillArgs {
     float *outp;                 // [P x H] fp32, per-pair down output
     int32_t *pexp;               // [P] power-of-two scale of the fp16 activation rows (Q6_K down)
     uint16_t *rsplit;            // bf16 router GEMM operands (prefill_router_ws_elems)
+    int thin_down;               // set by launch_prefill: thin tiles take k_pf_down_thin
 };
 
 // Number of pair slots and an upper bound on the GEMM tiles for T tokens.

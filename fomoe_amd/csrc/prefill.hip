@@ -42,6 +42,7 @@
 
 #include "common.h"
 #include "prefill.h"
+#include "q6k_mfma.h"
 #include "topk.h"
 
 namespace fo {
@@ -352,19 +353,24 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     const int toff = block_exclusive_scan(nt, scan_buf);   // first tile of expert tid
     // The GEMMs take tiles in decreasing cost: entry i's fourth word is the
     // i-th tile by token-block count (4, 3, 2, 1; expert order within a
-    // count), so the last work handed out is the cheapest. Per expert: its
-    // full tiles (count 4) and its last, partial tile (count cb).
+    // count), so the last work handed out is the cheapest; one-block tiles of
+    // at most kPfThin pairs come last of all (the thin tiles, which the Q6_K
+    // down projection runs on its integer path). Per expert: its full tiles
+    // (count 4) and its last, partial tile (count cb).
     const int nfull = cnt / kPfMT, rem = cnt - kPfMT * nfull, cb = (rem + 15) >> 4;   // cb = 0: no partial tile
-    const int c4 = nfull + (cb == 4), c3 = cb == 3, c2 = cb == 2, c1 = cb == 1;
+    const int thin = cb == 1 && rem <= kPfThin;
+    const int c4 = nfull + (cb == 4), c3 = cb == 3, c2 = cb == 2, c1 = cb == 1 && !thin;
     const int o43 = block_exclusive_scan(c4 | (c3 << 16), scan_buf);
     const int o21 = block_exclusive_scan(c2 | (c1 << 16), scan_buf);
-    __shared__ int s_tot[2];
-    if (tid == 1023) { s_tot[0] = o43 + (c4 | (c3 << 16)); s_tot[1] = o21 + (c2 | (c1 << 16)); }
+    const int o0 = block_exclusive_scan(thin, scan_buf);
+    __shared__ int s_tot[3];
+    if (tid == 1023) { s_tot[0] = o43 + (c4 | (c3 << 16)); s_tot[1] = o21 + (c2 | (c1 << 16)); s_tot[2] = o0 + thin; }
     __syncthreads();
-    const int T4 = s_tot[0] & 0xFFFF, T3 = s_tot[0] >> 16, T2 = s_tot[1] & 0xFFFF;
+    const int T4 = s_tot[0] & 0xFFFF, T3 = s_tot[0] >> 16, T2 = s_tot[1] & 0xFFFF, T1 = s_tot[1] >> 16;
     const int b4 = o43 & 0xFFFF;                                 // this expert's first rank per count
     const int bpart = cb == 4 ? b4 + nfull : cb == 3 ? T4 + (o43 >> 16)
-                    : cb == 2 ? T4 + T3 + (o21 & 0xFFFF) : T4 + T3 + T2 + (o21 >> 16);
+                    : cb == 2 ? T4 + T3 + (o21 & 0xFFFF) : thin ? T4 + T3 + T2 + T1 + o0
+                    : T4 + T3 + T2 + (o21 >> 16);
     if (tid <= E) {
         for (int i = 0; i < nt; i++) {
             int32_t *tp = a.tiles + 4 * (toff + i);
@@ -372,7 +378,8 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
             a.tiles[4 * (i < nfull ? b4 + i : bpart) + 3] = toff + i;
         }
     }
-    if (tid == 1023) { a.n_tiles[0] = toff + nt; a.n_tiles[2] = 0; }   // [2]: k_pf_gateup_f16 work counter
+    // [0]: tiles, [1]: tiles before the thin ones, [2]: k_pf_gateup_f16 work counter
+    if (tid == 1023) { a.n_tiles[0] = toff + nt; a.n_tiles[1] = toff + nt - s_tot[2]; a.n_tiles[2] = 0; }
     // pair offsets of each expert for the placement pass
     __shared__ int s_off[1025];
     if (tid <= E) s_off[tid] = off;
@@ -1094,7 +1101,7 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     // runs on XCD i % 8): the XCD takes every eighth tile in decreasing cost
     // (the order k_pf_group records), so the XCDs get like work; its
     // work-groups take its items u = i / 8, + G8, ..., the costliest first
-    const int nt = *a.n_tiles, nrb = a.H / (32 * kPfD16Waves);
+    const int nt = a.n_tiles[a.thin_down ? 1 : 0], nrb = a.H / (32 * kPfD16Waves);   // thin tiles: k_pf_down_thin
     const int x = blockIdx.x & 7, G8 = gridDim.x >> 3, per = (nt - x + 7) >> 3, n_u = per * nrb;
     const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
     const int NK = a.F / 256;
@@ -1224,6 +1231,100 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     }
 }
 #pragma clang fp contract(on)
+
+// ------------------------------------------------------------ Q6_K down of the thin tiles
+// Tiles of at most kPfThin pairs (k_pf_group orders them last) run the
+// decode matvec's integer path instead of k_pf_down16: a 16-row weight tile
+// streamed with 1 KiB loads into LDS (the next tile in flight) and, per pair,
+// the Q6_K super-block dot on v_mfma_i32_16x16x64_i8 against the pair's
+// activation as int8 limbs (q6k_mfma.h, as k_matvec_q6k_tile). The limbs are
+// prepared from the fp16 activation rows k_pf_actprep_w wrote (exactly: a
+// fp16 value needs 11 of the 22 fixed-point bits), and the pair's 2^s is
+// applied to the result. The code building is shared by the tile's pairs, so
+// a weight costs ~0.75 + 0.5 n VALU instructions per code against ~3.4 for
+// the fp16 operand decode of k_pf_down16, whose 16-token MFMA blocks a thin
+// tile leaves mostly empty. Work unit = (thin tile, kPfThinTPW * 16 rows),
+// one wave per work-group, units dealt round-robin; F == 1024.
+constexpr int kPfThinTPW = 8;
+constexpr uint32_t kPfThinX = 3 * 1024 + 64 * 8;                  // one pair's prepared activation
+constexpr uint32_t kPfThinZero = 304;                              // zero A operands (as kT6Zero)
+constexpr uint32_t kPfThinTile = 16 * 840;                         // 13,440 bytes
+constexpr uint32_t kPfThinLds = kPfThin * kPfThinX + kPfThinZero + kPfThinTile;
+
+__global__ __launch_bounds__(64) void k_pf_down_thin(PrefillArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
+    constexpr int NV = (kPfThinTile + 1023) / 1024;
+    constexpr uint32_t rb = 840, limb_bytes = 3 * 1024;
+    const int lane = threadIdx.x;
+    uint8_t *zero = sx + kPfThin * kPfThinX;
+    uint8_t *tb = zero + kPfThinZero;
+    const int n_thick = a.n_tiles[1], n_thin = a.n_tiles[0] - n_thick;
+    const int upt = a.H / (16 * kPfThinTPW), nunits = n_thin * upt;
+    if (lane < kPfThinZero / 16) *(uint4 *)(zero + 16 * lane) = make_uint4(0, 0, 0, 0);
+    const int r = lane & 15, g = lane >> 4, n = g >> 1, j = g & 1, L = r & 3;
+    const bool valid = (r >> 2) == g && L < 3;
+    const uint32_t aoff = (8 * n + j) * 48 + 16 * L, soff = limb_bytes + (8 * n + j) * 8;
+    for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
+        const int ti = n_thick + u / upt, row0 = (u % upt) * 16 * kPfThinTPW;
+        const int tile = a.tiles[4 * ti + 3];
+        const int4 t4 = *(const int4 *)(a.tiles + 4 * tile);
+        const bool shared = t4.x == a.E;
+        const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)t4.x * a.stride;
+        const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
+        const uint8_t *W = blob + down_off + (uint64_t)row0 * rb;
+        const int p0 = t4.y, np = t4.z;                  // np <= kPfThin
+        uint4 v[NV];
+        auto issue = [&](int tt) {
+            const uint8_t *tp = W + (uint64_t)tt * kPfThinTile;
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = ldw16(tp + min(i * 1024u + lane * 16u, kPfThinTile - 16));
+        };
+        issue(0);
+        __syncthreads();                                 // the previous unit's LDS reads are done
+        for (int m = 0; m < np; m++) {                   // lane = 16-value group of pair m
+            const uint16_t *src = a.act_hi + (uint64_t)(p0 + m) * a.F + 16 * lane;
+            const uint4 h0 = *(const uint4 *)src, h1 = *(const uint4 *)(src + 8);
+            const uint32_t w[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+            float vals[16];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                vals[2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] & 0xFFFFu));
+                vals[2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[q] >> 16));
+            }
+            int limb[kLimbs][4];
+            float scale, sum;
+            prep_group_vals<16>(vals, limb, scale, sum);
+            uint8_t *xm = sx + m * kPfThinX;
+#pragma unroll
+            for (int Lq = 0; Lq < kLimbs; Lq++)
+                *(uint4 *)(xm + lane * 48 + 16 * Lq) = make_uint4(limb[Lq][0], limb[Lq][1], limb[Lq][2], limb[Lq][3]);
+            *(float2 *)(xm + limb_bytes + lane * 8) = make_float2(scale, -32.f * sum);
+        }
+        __syncthreads();
+        for (int tt = 0; tt < kPfThinTPW; tt++) {
+#pragma unroll
+            for (int i = 0; i < NV; i++) *(uint4 *)(tb + min(i * 1024u + lane * 16u, kPfThinTile - 16)) = v[i];
+            if (tt + 1 < kPfThinTPW) issue(tt + 1);
+            Q6kSlot qs[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) q6k_slot_load(qs[b], tb + r * rb + b * 210, n, j);
+#pragma unroll 1
+            for (int m = 0; m < np; m++) {
+                {
+                    const uint8_t *xm = sx + m * kPfThinX;
+                    float acc = 0.f;
+#pragma unroll
+                    for (int b = 0; b < 4; b++)
+                        acc += q6k_sb_dot_mfma(qs[b], valid ? xm + aoff + 768 * b : zero, xm + soff + 128 * b, j);
+                    acc += __shfl_xor(acc, 16);
+                    acc += __shfl_xor(acc, 32);
+                    if (g == 0)
+                        a.outp[(uint64_t)(p0 + m) * a.H + row0 + 16 * tt + r] = ldexpf(acc, a.pexp[p0 + m]);
+                }
+            }
+        }
+    }
+}
 
 // ============================================================ P6 combine
 // One work-group per (token, kCombCols columns); each thread owns float4 columns and requests all
@@ -1379,9 +1480,11 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             }
             const int np = prefill_pairs(a.T, a.k, a.shared != nullptr);
             k_pf_actprep_w<<<(np + kApWaves - 1) / kApWaves, 64 * kApWaves, 0, s>>>(a, np);
+            a.thin_down = a.F == 1024 && a.H % (16 * kPfThinTPW) == 0;
             int dev = 0, n_cu = 256;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
             k_pf_down16<<<(kPfD16PerCU * n_cu + 7) & ~7, kPfD16Waves * 64, lds16, s>>>(a);   // persistent
+            if (a.thin_down) k_pf_down_thin<<<8 * n_cu, 64, kPfThinLds, s>>>(a);
         } else if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
         else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
     }
