@@ -687,6 +687,29 @@ def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid, H):
         assert inf_rel(w[:, shape.k], ow[:, shape.k]) < 1e-5
 
 
+@pytest.mark.parametrize("T", [1, 9, 70])
+def test_prefill_thin_tiles_f1024(gpu, T):
+    """Expert FFN 1024 wide (the config shape's F): tiles of at most 4 pairs
+    take the integer-MFMA down path (k_pf_down_thin), the others the fp16
+    GEMM; every token and output against the oracle's per-token composition,
+    with a mix of thin and thick tiles at T = 70 (32 experts, top-4)."""
+    from fomoe_amd import synthetic as S
+    say(f"prefill thin tiles F=1024 T={T}")
+    shape = S.LayerShape(n_embd=512, inter=1024, n_experts=32, k=4, shared=True)
+    L = S.build_layer(gpu, shape, 0, seed=31, zipf_s=1.1, norm=False)
+    dx = S.tokens_bf16(gpu, T, shape.n_embd, seed=33)
+    dout = gpu.alloc(4 * T * shape.n_embd)
+    gpu.moe_prefill(L.desc, dx, T, dout, 0)
+    got = gpu.download(dout, np.float32, T * shape.n_embd).reshape(T, shape.n_embd)
+    ids, w = gpu.prefill_routing(T, shape.k)
+    x = O.to_bf16(O.synth_f32(33, S.stream(0, 0, S.TOKENS), 1.0, T * shape.n_embd)).reshape(T, -1)
+    d, keep = _prefill_host_layer(shape, 0, 31, True)
+    want, oids, ow = pf_check(got, d, x, 0, shape)
+    assert np.array_equal(ids, oids)
+    counts = np.bincount(ids.ravel(), minlength=shape.n_experts)
+    say(f"  experts with 1-4 tokens: {int(((counts > 0) & (counts <= 4)).sum())}, with more: {int((counts > 4).sum())}")
+
+
 def test_prefill_token_scales(gpu):
     """Tokens whose magnitudes span 2^-40 .. 2^30 (one power of two per token,
     some rows zero): the fp16 gate/up path scales each token row by its own
