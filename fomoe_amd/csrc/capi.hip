@@ -26,24 +26,24 @@
 using namespace fo;
 
 // ------------------------------------------------------------------ no-allocation scratch
-// The device scratch of gpu_moe_layer_noalloc: one static array per device,
-// held until the process ends. Host code never passes `fo_noalloc_scratch`
-// itself to a kernel (in host code the name is a host-side stand-in): its
-// device address is looked up once per device with hipGetSymbolAddress in
-// gpu_init and kept in g_noalloc_ptr.
+// The device scratch of gpu_moe_layer_noalloc: one static array, held until
+// the process ends. Contexts always run on device 0 (gpu_init selects it, as
+// the reference's does), so one copy of the array is in use. Host code never
+// passes `fo_noalloc_scratch` itself to a kernel (in host code the name is a
+// host-side stand-in): its device address is looked up with
+// hipGetSymbolAddress in gpu_init, with device 0 current, and kept in
+// g_noalloc_ptr.
 static constexpr size_t kNoAllocBytes = 1u << 20;   // GPU_MOE_NOALLOC_SCRATCH_BYTES
 static_assert(kNoAllocBytes == GPU_MOE_NOALLOC_SCRATCH_BYTES, "header and library agree");
 static __device__ __align__(256) uint8_t fo_noalloc_scratch[kNoAllocBytes];
-static constexpr int kMaxDevices = 64;
-static void *g_noalloc_ptr[kMaxDevices];
+static void *g_noalloc_ptr;
 
-static hipError_t noalloc_setup(int device) {
-    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-    if (g_noalloc_ptr[device]) return hipSuccess;
+static hipError_t noalloc_setup() {
+    if (g_noalloc_ptr) return hipSuccess;
     void *p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(fo_noalloc_scratch));
     if (e != hipSuccess || !p) return e != hipSuccess ? e : hipErrorInvalidSymbol;
-    g_noalloc_ptr[device] = p;
+    g_noalloc_ptr = p;
     return hipSuccess;
 }
 
@@ -74,7 +74,7 @@ gpu_ctx_t *gpu_init(void) {
               hipMalloc((void **)&c->weights, 64 * sizeof(float)) == hipSuccess &&
               hipMemset(c->counter, 0, 256) == hipSuccess &&
               hipMemset(c->ids, 0, 64 * sizeof(int32_t)) == hipSuccess &&
-              noalloc_setup(c->device) == hipSuccess &&
+              noalloc_setup() == hipSuccess &&
               hipDeviceSynchronize() == hipSuccess;
     if (!ok) {
         gpu_free(c);
@@ -90,7 +90,7 @@ void gpu_free(gpu_ctx_t *c) {
     void *bufs[] = {c->logits, c->counter, c->ids, c->weights, c->xq_h, c->xq_act, c->act,
                     c->act2, c->vec_in, c->vec_out, c->staging, c->pf_logits, c->pf_ids,
                     c->pf_w, c->pf_pairpos, c->pf_pairtok, c->pf_tiles, c->pf_ntiles,
-                    c->pf_act, c->pf_outp, c->pf_xsum, c->pf_rsplit};
+                    c->pf_act, c->pf_outp, c->pf_xsum, c->pf_rsplit, c->sh_act, c->sh_ys};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     for (int b = 0; b < 2; b++) {
@@ -230,17 +230,30 @@ static int check_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L) {
     const uint64_t ds = fomoe_row_bytes(L->down_type, L->inter) * (uint64_t)L->n_embd;
     if (L->gate_size < gs || L->up_size < gs || L->expert_stride < L->gate_size + L->up_size + ds)
         return fail(ctx, -1, "moe layer: blob sizes too small for the shapes");
-    if (L->shared && (L->shared_inter != L->inter || L->shared_gate_size < gs || L->shared_up_size < gs))
-        return fail(ctx, -1, "moe layer: shared expert must match the routed shape");
+    if (L->shared) {   // its own types and intermediate size (reference include/model.h:104-108)
+        const int Fs = L->shared_inter;
+        if (Fs <= 0 || Fs % 256 || Fs > 8192)
+            return fail(ctx, -1, "moe layer: shared_inter %d (multiple of 256, <= 8192)", Fs);
+        if (!layer_type(L->shared_gate_type) || !layer_type(L->shared_up_type) || !layer_type(L->shared_down_type))
+            return fail(ctx, -1, "moe layer: shared types gate %d up %d down %d", L->shared_gate_type,
+                        L->shared_up_type, L->shared_down_type);
+        if (L->shared_gate_size < fomoe_row_bytes(L->shared_gate_type, L->n_embd) * (uint64_t)Fs ||
+            L->shared_up_size < fomoe_row_bytes(L->shared_up_type, L->n_embd) * (uint64_t)Fs)
+            return fail(ctx, -1, "moe layer: shared gate/up sizes too small for the shapes");
+    }
     return 0;
 }
 
 // Size every scratch buffer a layer needs (outside any graph capture).
 static int size_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *L) {
-    const int n_tot = L->k + (L->shared ? 1 : 0);
+    const int n_tot = L->k + (L->shared ? 1 : 0);   // slot k: a fused shared expert
     HIPC(ensure(ctx->xq_h, ctx->xq_h_cap, xq_stride(L->n_embd, gsz_of(L->gate_type))));
     HIPC(ensure(ctx->act, ctx->act_cap, sizeof(float) * (size_t)n_tot * L->inter));
     HIPC(ensure(ctx->xq_act, ctx->xq_act_cap, xq_stride(L->inter, gsz_of(L->down_type)) * (size_t)n_tot));
+    if (L->shared) {
+        HIPC(ensure(ctx->sh_act, ctx->sh_act_cap, sizeof(float) * (size_t)L->shared_inter));
+        HIPC(ensure(ctx->sh_ys, ctx->sh_ys_cap, sizeof(float) * (size_t)L->n_embd));
+    }
     return 0;
 }
 
@@ -263,10 +276,46 @@ struct LayerScratch {
     uint8_t *xq_h;       // prepared h
     uint8_t *xq_act;     // n_tot prepared activations
     float *act;          // [n_tot x F] fp32 activations (general path)
+    float *sh_act;       // [F_s] shared-expert activation
+    float *sh_ys;        // [H] weighted shared-expert output
 };
 
 static LayerScratch ctx_scratch(gpu_ctx_t *ctx) {
-    return LayerScratch{ctx->logits, ctx->counter, ctx->ids, ctx->weights, ctx->xq_h, ctx->xq_act, ctx->act};
+    return LayerScratch{ctx->logits, ctx->counter, ctx->ids, ctx->weights, ctx->xq_h, ctx->xq_act, ctx->act,
+                        ctx->sh_act, ctx->sh_ys};
+}
+
+// The shared expert's description for its roles (shared.h); w: where the
+// layer's kernels leave the shared-expert weight.
+static SharedArgs shared_args(const LayerScratch &sc, const gpu_moe_layer_t *L, const float *w) {
+    SharedArgs s{};
+    if (!L->shared) return s;
+    const int H = L->n_embd, Fs = L->shared_inter;
+    s.blob = (const uint8_t *)L->shared;
+    s.gate_type = L->shared_gate_type;
+    s.up_type = L->shared_up_type;
+    s.down_type = L->shared_down_type;
+    s.up_off = L->shared_gate_size;
+    s.down_off = L->shared_gate_size + L->shared_up_size;
+    s.gate_rb = fomoe_row_bytes(s.gate_type, H);
+    s.up_rb = fomoe_row_bytes(s.up_type, H);
+    s.down_rb = fomoe_row_bytes(s.down_type, Fs);
+    s.F = Fs;
+    s.H = H;
+    s.act = sc.sh_act;
+    s.w = w;
+    s.ys = sc.sh_ys;
+    s.down_rpw = shared_down_rpw(Fs);
+    s.down_waves = 4;
+    return s;
+}
+
+// True when the shared expert has the routed experts' types and
+// intermediate size: it then rides in the layer kernels as expert slot k;
+// otherwise it runs as the shared-expert kernels of its own (shared.h).
+static bool shared_fused(const gpu_moe_layer_t *L) {
+    return L->shared && L->shared_inter == L->inter && L->shared_gate_type == L->gate_type &&
+           L->shared_up_type == L->up_type && L->shared_down_type == L->down_type;
 }
 
 static int enqueue_layer_fast(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_moe_layer_t *L,
@@ -274,11 +323,13 @@ static int enqueue_layer_fast(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_
     const int H = L->n_embd, F = L->inter;
     const int dg = gsz_of(L->down_type);
     const uint64_t xs = xq_stride(F, dg);
-    const uint8_t *base = (const uint8_t *)L->experts, *sh = (const uint8_t *)L->shared;
+    const bool fused = shared_fused(L);
+    const uint8_t *base = (const uint8_t *)L->experts, *sh = fused ? (const uint8_t *)L->shared : nullptr;
     float *shared_w = sc.weights + kSharedW;
     RouteArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, sc.logits,
-                 sc.xq_h, gsz_of(L->gate_type), L->shared_gate_vec, shared_w};
+                 sc.xq_h, gsz_of(L->gate_type), L->shared_gate_vec, L->shared ? shared_w : nullptr};
     HIPC(launch_route(ra, ctx->stream));
+    if (L->shared && !fused) HIPC(launch_shared(shared_args(sc, L, shared_w), in, norm_w, L->eps, ctx->stream));
     ExpandArgs ea{sc.logits, L->n_experts, L->k, sc.ids, sc.weights, base, L->expert_stride,
                   L->gate_size, sh, L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H),
                   sc.xq_h, sc.xq_act, xs, dg, nullptr};
@@ -286,14 +337,14 @@ static int enqueue_layer_fast(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_
     ReduceArgs da{sc.ids, sc.weights, sh ? shared_w : nullptr, L->k, base, L->expert_stride,
                   L->gate_size + L->up_size, sh, L->shared_gate_size + L->shared_up_size, F, H,
                   fomoe_row_bytes(L->down_type, F), sc.xq_act, xs,
-                  (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out};
+                  (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out, (L->shared && !fused) ? sc.sh_ys : nullptr};
     HIPC(launch_reduce(L->down_type, da, ctx->stream, ctx->n_cu));
     return 0;
 }
 
 static int enqueue_layer(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_moe_layer_t *L,
                          const float *in, float *out, int flags) {
-    const int H = L->n_embd, F = L->inter, n_tot = L->k + (L->shared ? 1 : 0);
+    const int H = L->n_embd, F = L->inter, k = L->k;
     const float *norm_w = (flags & GPU_MOE_NORM) ? L->norm_w : nullptr;
     if ((flags & GPU_MOE_NORM) && !norm_w) return fail(ctx, -1, "moe layer: GPU_MOE_NORM without norm_w");
     const bool fast = fast_layer(L);
@@ -306,16 +357,19 @@ static int enqueue_layer(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_moe_l
     RouterArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, L->k,
                   sc.logits, sc.counter, sc.ids, sc.weights, L->shared_gate_vec};
     HIPC(launch_router(ra, sc.xq_h, gsz_of(L->gate_type), ctx->stream));
-    const uint8_t *base = (const uint8_t *)L->experts, *sh = (const uint8_t *)L->shared;
-    GateUpArgs ga{sc.ids, L->k, base, L->expert_stride, 0, L->gate_size, sh, 0,
-                  L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H), in, norm_w,
-                  L->eps, sc.act};
+    const uint8_t *base = (const uint8_t *)L->experts;
+    if (L->shared) {   // the shared expert first: the router leaves its weight at weights[k]
+        const SharedArgs sa = shared_args(sc, L, sc.weights + k);
+        HIPC(launch_shared(sa, in, norm_w, L->eps, ctx->stream));
+    }
+    GateUpArgs ga{sc.ids, k, base, L->expert_stride, 0, L->gate_size, F, H,
+                  fomoe_row_bytes(L->gate_type, H), in, norm_w, L->eps, sc.act};
     HIPC(launch_gateup(L->gate_type, ga, sc.xq_h, ctx->stream, ctx->n_cu));
     const int gsz = gsz_of(L->down_type);
     const uint64_t xs = xq_stride(F, gsz);
-    HIPC(launch_xprep(gsz, sc.act, (uint64_t)F, F, n_tot, sc.xq_act, xs, ctx->stream));
-    DownArgs da{sc.ids, sc.weights, L->k, base, L->expert_stride, L->gate_size + L->up_size,
-                sh, L->shared_gate_size + L->shared_up_size, sc.act, H, F,
+    HIPC(launch_xprep(gsz, sc.act, (uint64_t)F, F, k, sc.xq_act, xs, ctx->stream));
+    DownArgs da{sc.ids, sc.weights, k, base, L->expert_stride, L->gate_size + L->up_size,
+                L->shared ? sc.sh_ys : nullptr, sc.act, H, F,
                 fomoe_row_bytes(L->down_type, F), (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out};
     HIPC(launch_down(L->down_type, da, sc.xq_act, xs, ctx->stream, ctx->n_cu));
     return 0;
@@ -347,10 +401,12 @@ static size_t noalloc_layout(const gpu_moe_layer_t *L, uint8_t *base, LayerScrat
     uint8_t *logits = take(1024 * sizeof(float)), *counter = take(256), *ids = take(64 * sizeof(int32_t)),
             *weights = take(64 * sizeof(float)), *xq_h = take(xq_stride(L->n_embd, gsz_of(L->gate_type))),
             *xq_act = take(xq_stride(L->inter, gsz_of(L->down_type)) * (size_t)n_tot),
-            *act = take(sizeof(float) * (size_t)n_tot * L->inter);
+            *act = take(sizeof(float) * (size_t)n_tot * L->inter),
+            *sh_act = take(L->shared ? sizeof(float) * (size_t)L->shared_inter : 0),
+            *sh_ys = take(L->shared ? sizeof(float) * (size_t)L->n_embd : 0);
     if (sc)
         *sc = LayerScratch{(float *)logits, (unsigned *)counter, (int32_t *)ids, (float *)weights, xq_h, xq_act,
-                           (float *)act};
+                           (float *)act, (float *)sh_act, (float *)sh_ys};
     return off;
 }
 
@@ -361,8 +417,8 @@ int gpu_moe_layer_noalloc(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const float 
     if (need > kNoAllocBytes)
         return fail(ctx, -1, "gpu_moe_layer_noalloc: layer needs %zu bytes of scratch, the static area holds %zu",
                     need, kNoAllocBytes);
-    uint8_t *base = (ctx->device >= 0 && ctx->device < kMaxDevices) ? (uint8_t *)g_noalloc_ptr[ctx->device] : nullptr;
-    if (!base) return fail(ctx, -2, "gpu_moe_layer_noalloc: scratch address of device %d unknown", ctx->device);
+    uint8_t *base = (uint8_t *)g_noalloc_ptr;
+    if (!base) return fail(ctx, -2, "gpu_moe_layer_noalloc: scratch address unknown");
     LayerScratch sc;
     noalloc_layout(L, base, &sc);
     // the area keeps the previous call's contents: the general router's
@@ -506,8 +562,8 @@ int gpu_expert_ffn(gpu_ctx_t *ctx, const float *h, void **expert_buffers, const 
     if (gate_type == up_type) {
         const int gsz = gsz_of(gate_type);
         if (launch_xprep(gsz, ctx->vec_in, 0, H, 1, ctx->xq_h, xq_stride(H, gsz), s) != hipSuccess) return -1;
-        GateUpArgs ga{nullptr, n, ctx->staging, stride, 0, gate_size, nullptr, 0, 0, F, H, rb_g,
-                      ctx->vec_in, nullptr, 0.f, ctx->act};
+        GateUpArgs ga{nullptr, n, ctx->staging, stride, 0, gate_size, F, H, rb_g, ctx->vec_in, nullptr, 0.f,
+                      ctx->act};
         if (launch_gateup(gate_type, ga, ctx->xq_h, s, ctx->n_cu) != hipSuccess) return -1;
     } else {
         // gate and up in different formats: two batched matvecs + SiLU*up
@@ -525,7 +581,7 @@ int gpu_expert_ffn(gpu_ctx_t *ctx, const float *h, void **expert_buffers, const 
     const int gsz = gsz_of(down_type);
     const uint64_t xs = xq_stride(F, gsz);
     if (launch_xprep(gsz, ctx->act, (uint64_t)F, F, n, ctx->xq_act, xs, s) != hipSuccess) return -1;
-    DownArgs da{nullptr, ctx->weights, n, ctx->staging, stride, gate_size + up_size, nullptr, 0,
+    DownArgs da{nullptr, ctx->weights, n, ctx->staging, stride, gate_size + up_size, nullptr,
                 ctx->act, H, F, fomoe_row_bytes(down_type, F), nullptr, ctx->vec_out};
     if (launch_down(down_type, da, ctx->xq_act, xs, s, ctx->n_cu) != hipSuccess) return -1;
     if (hipMemcpyAsync(ffn_out, ctx->vec_out, sizeof(float) * H, hipMemcpyDeviceToHost, s) != hipSuccess)
@@ -580,6 +636,10 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     const bool pt = (L->gate_type == GGML_TYPE_Q4_K || L->gate_type == GGML_TYPE_Q6_K) &&
                     (L->down_type == GGML_TYPE_Q4_K || L->down_type == GGML_TYPE_Q6_K);
     if (!pt) return fail(ctx, -1, "moe prefill: gate/up/down types must be Q4_K or Q6_K");
+    if (L->shared && (L->shared_inter != L->inter || L->shared_gate_type != L->gate_type ||
+                      L->shared_up_type != L->up_type || L->shared_down_type != L->down_type))
+        return fail(ctx, -1, "moe prefill: the shared expert's types and intermediate size must equal the "
+                             "routed experts' (gpu_moe_layer takes any)");
     const int T = n_tokens, E = L->n_experts, k = L->k, H = L->n_embd, F = L->inter;
     if (E > 1023) return fail(ctx, -1, "moe prefill: n_experts %d > 1023", E);
     if (L->gate_type == GGML_TYPE_Q4_K) {   // its gate/up rows move by direct 16-byte global->LDS loads

@@ -29,6 +29,8 @@ struct gpu_ctx {
     uint8_t *xq_act = nullptr;     size_t xq_act_cap = 0;
     float *act = nullptr;          size_t act_cap = 0;
     float *act2 = nullptr;         size_t act2_cap = 0;
+    float *sh_act = nullptr;       size_t sh_act_cap = 0;   // shared-expert activation [F_s]
+    float *sh_ys = nullptr;        size_t sh_ys_cap = 0;    // weighted shared-expert output [H]
     float *vec_in = nullptr;       size_t vec_in_cap = 0;
     float *vec_out = nullptr;      size_t vec_out_cap = 0;
     uint8_t *staging = nullptr;    size_t staging_cap = 0;

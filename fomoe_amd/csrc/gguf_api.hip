@@ -254,11 +254,24 @@ int gpu_gguf_load_moe_layer(gpu_ctx_t *ctx, const gpu_gguf_t *g, int blk, gpu_mo
     if (!nw) nw = find("ffn_norm");
     const bool shared = sg && su && sd;
     uint64_t sgs = 0, sus = 0, sds = 0;
+    int64_t Fs = 0;
     if (shared) {
-        if (sg->dims[0] != H || sg->dims[1] != F || su->dims[0] != H || su->dims[1] != F || sd->dims[0] != F ||
-            sd->dims[1] != H || !layer_type(sg->type) || !layer_type(su->type) || !layer_type(sd->type))
+        // ggml dims: gate/up [H, F_s], down [F_s, H], each in its own type
+        // (reference src/model.c:164, 365-371)
+        Fs = sg->dims[1];
+        int64_t key_fs = 0;
+        if (arch && gpu_gguf_get_int(g, (std::string(arch) + ".expert_shared_feed_forward_length").c_str(),
+                                     &key_fs) == 0 && key_fs != Fs)
+            return fail(ctx, -1, "gguf layer: block %d shared expert has %lld rows, the model key says %lld", blk,
+                        (long long)Fs, (long long)key_fs);
+        if (sg->n_dims != 2 || su->n_dims != 2 || sd->n_dims != 2 || sg->dims[0] != H || su->dims[0] != H ||
+            su->dims[1] != Fs || sd->dims[0] != Fs || sd->dims[1] != H || Fs <= 0 || Fs > INT32_MAX ||
+            !layer_type(sg->type) || !layer_type(su->type) || !layer_type(sd->type))
             return fail(ctx, -1, "gguf layer: block %d shared expert shape/type unsupported", blk);
         sgs = sg->size; sus = su->size; sds = sd->size;
+        if (sgs != fomoe_row_bytes(sg->type, H) * Fs || sus != fomoe_row_bytes(su->type, H) * Fs ||
+            sds != fomoe_row_bytes(sd->type, Fs) * H)
+            return fail(ctx, -1, "gguf layer: block %d shared tensor sizes do not match their shapes", blk);
     }
     if (sv && elements(*sv) != H) return fail(ctx, -1, "gguf layer: block %d shared gate vector is not [H]", blk);
     if (nw && elements(*nw) != H) return fail(ctx, -1, "gguf layer: block %d norm weight is not [H]", blk);
@@ -275,9 +288,12 @@ int gpu_gguf_load_moe_layer(gpu_ctx_t *ctx, const gpu_gguf_t *g, int blk, gpu_mo
     out.gate_size = gs;
     out.up_size = us;
     out.expert_stride = (gs + us + ds + kStoreAlign - 1) / kStoreAlign * kStoreAlign;
-    out.shared_inter = shared ? (int)F : 0;
+    out.shared_inter = (int)Fs;
     out.shared_gate_size = sgs;
     out.shared_up_size = sus;
+    out.shared_gate_type = shared ? sg->type : 0;
+    out.shared_up_type = shared ? su->type : 0;
+    out.shared_down_type = shared ? sd->type : 0;
     out.eps = (float)eps;
 
     int rc = 0;

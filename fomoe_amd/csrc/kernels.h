@@ -45,33 +45,30 @@ struct RouterArgs {
 };
 
 // act[e][r] = silu(gate_e[r,:].h) * (up_e[r,:].h), e < n_sel routed experts
-// (blob = base + ids[e]*stride, or base + e*stride if ids is NULL), then the
-// shared expert as slot n_sel when shared != NULL.
+// (blob = base + ids[e]*stride, or base + e*stride if ids is NULL).
 struct GateUpArgs {
     const int32_t *ids;
     int n_sel;
     const uint8_t *base;
     uint64_t stride, gate_off, up_off;
-    const uint8_t *shared;
-    uint64_t sh_gate_off, sh_up_off;
     int F, H;
     uint64_t row_bytes;
     const float *x;
     const float *norm_w;    // h = rms_norm(x)*norm_w when non-NULL, else h = x
     float eps;
-    float *act;             // [(n_sel + has_shared) x F]
+    float *act;             // [n_sel x F]
 };
 
-// out[i] = (resid ? resid[i] : 0) + sum_e weights[e] * down_e[i,:].act_e
+// out[i] = (resid ? resid[i] : 0) + (sum_e weights[e] * down_e[i,:].act_e
+// + (ys ? ys[i] : 0)); ys = the weighted shared expert's output.
 struct DownArgs {
     const int32_t *ids;
-    const float *weights;   // [n_tot]
+    const float *weights;   // [n_sel]
     int n_sel;
     const uint8_t *base;
     uint64_t stride, down_off;
-    const uint8_t *shared;
-    uint64_t sh_down_off;
-    const float *act;       // [n_tot x F]
+    const float *ys;        // [H] or NULL
+    const float *act;       // [n_sel x F]
     int H, F;
     uint64_t row_bytes;
     const float *resid;

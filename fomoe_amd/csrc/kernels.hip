@@ -1009,7 +1009,7 @@ __global__ __launch_bounds__(256) void k_gateup(GateUpArgs a, const uint8_t *__r
     const int w = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int nw = (int)((gridDim.x * blockDim.x) >> 6);
     const int S = a.H / Fmt<T>::SLOT;
-    const int n_tot = a.n_sel + (a.shared ? 1 : 0);
+    const int n_tot = a.n_sel;
     const int tpe = (a.F + ROWS - 1) / ROWS;
     int64_t t0, t1;
     wave_share((int64_t)tpe * n_tot, w, nw, t0, t1);
@@ -1020,15 +1020,8 @@ __global__ __launch_bounds__(256) void k_gateup(GateUpArgs a, const uint8_t *__r
     X.load(L, xq_h, a.H);
     for (int64_t t = t0; t < t1; t++) {
         const int e = (int)(t / tpe), rb = (int)(t - (int64_t)e * tpe);
-        const uint8_t *blob;
-        uint64_t go, uo;
-        if (e < a.n_sel) {
-            const int id = a.ids ? a.ids[e] : e;
-            blob = a.base + (uint64_t)id * a.stride;
-            go = a.gate_off; uo = a.up_off;
-        } else {
-            blob = a.shared; go = a.sh_gate_off; uo = a.sh_up_off;
-        }
+        const uint8_t *blob = a.base + (uint64_t)(a.ids ? a.ids[e] : e) * a.stride;
+        const uint64_t go = a.gate_off, uo = a.up_off;
         RowRaw<T, U> rg[R], ru[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -1050,7 +1043,7 @@ template <int T, int R>
 static hipError_t gateup_t(const GateUpArgs &a, const uint8_t *xq_h, hipStream_t s, int n_cu) {
     int G, U;
     if (!geometry(T, a.H, G, U)) return hipErrorInvalidValue;
-    const int P = 64 / G, n_tot = a.n_sel + (a.shared ? 1 : 0);
+    const int P = 64 / G, n_tot = a.n_sel;
     const int64_t tasks = (int64_t)((a.F + P * R - 1) / (P * R)) * n_tot;
     const int blocks = (waves_for(tasks, n_cu, 16) + 3) / 4;
 #define FO_GU(GG, UU) \
@@ -1061,7 +1054,7 @@ static hipError_t gateup_t(const GateUpArgs &a, const uint8_t *xq_h, hipStream_t
 }
 
 hipError_t launch_gateup(int type, const GateUpArgs &a, const uint8_t *xq_h, hipStream_t s, int n_cu) {
-    if (a.F <= 0 || a.n_sel < 0 || a.n_sel + (a.shared ? 1 : 0) <= 0) return hipErrorInvalidValue;
+    if (a.F <= 0 || a.n_sel <= 0) return hipErrorInvalidValue;
     switch (type) {
         case GGML_TYPE_Q4_K: return gateup_t<GGML_TYPE_Q4_K, 2>(a, xq_h, s, n_cu);
         case GGML_TYPE_Q5_K: return gateup_t<GGML_TYPE_Q5_K, 2>(a, xq_h, s, n_cu);
@@ -1072,11 +1065,11 @@ hipError_t launch_gateup(int type, const GateUpArgs &a, const uint8_t *xq_h, hip
 }
 
 // ============================================================ down + combine
-// Tasks are blocks of P rows of the output; for each expert e (routed in rank
-// order, then shared) the wave loads NE experts' rows at a time and
-// accumulates weights[e] * down_e[row,:].act_e in the lanes before a single
-// group reduction per row; out = resid + sum (reference src/inference.c:
-// 574 vec_scaled_add in rank order, 595 shared add, 606 residual).
+// Tasks are blocks of P rows of the output; for each routed expert e (in rank
+// order) the wave loads NE experts' rows at a time and accumulates weights[e]
+// * down_e[row,:].act_e in the lanes before a single group reduction per row;
+// out = resid + (sum + ys) (reference src/inference.c: 574 vec_scaled_add in
+// rank order, 595 shared add, 606 residual).
 template <int T, int U, int G, int NE>
 __global__ __launch_bounds__(256) void k_down(DownArgs a, const uint8_t *__restrict__ xq_act,
                                               uint64_t xq_vstride) {
@@ -1085,7 +1078,7 @@ __global__ __launch_bounds__(256) void k_down(DownArgs a, const uint8_t *__restr
     const int w = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int nw = (int)((gridDim.x * blockDim.x) >> 6);
     const int S = a.F / Fmt<T>::SLOT;
-    const int n_tot = a.n_sel + (a.shared ? 1 : 0);
+    const int n_tot = a.n_sel;
     const int tasks = (a.H + P - 1) / P;
     int64_t t0, t1;
     wave_share(tasks, w, nw, t0, t1);
@@ -1101,9 +1094,7 @@ __global__ __launch_bounds__(256) void k_down(DownArgs a, const uint8_t *__restr
             for (int i = 0; i < NE; i++) {
                 const int e = e0 + i;
                 if (e < n_tot) {
-                    const uint8_t *m = (e < a.n_sel)
-                        ? a.base + (uint64_t)(a.ids ? a.ids[e] : e) * a.stride + a.down_off
-                        : a.shared + a.sh_down_off;
+                    const uint8_t *m = a.base + (uint64_t)(a.ids ? a.ids[e] : e) * a.stride + a.down_off;
                     load_row(raw[i], m + (uint64_t)row * a.row_bytes, L);
                 }
             }
@@ -1118,7 +1109,8 @@ __global__ __launch_bounds__(256) void k_down(DownArgs a, const uint8_t *__restr
             }
         }
         const float v = group_sum<G>(acc);
-        if ((lane % G) == 0 && row_u < a.H) a.out[row_u] = (a.resid ? a.resid[row_u] : 0.f) + v;
+        if ((lane % G) == 0 && row_u < a.H)
+            a.out[row_u] = (a.resid ? a.resid[row_u] : 0.f) + (a.ys ? v + a.ys[row_u] : v);
     }
 }
 

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "shared.h"
+
 namespace fo {
 
 // K1: logits[E] = router . h (+ bias), h = rms_norm(x) * norm_w (norm_w NULL:
@@ -46,7 +48,9 @@ struct ExpandArgs {
 
 // K3: out[i] = (resid ? resid[i] : 0) + sum_e w_e * down_e[i,:] . act_e over
 // the k routed experts in rank order, then the shared expert (weight
-// *shared_w, or 1 when NULL).
+// *shared_w, or 1 when NULL) — in the layer's kernels when it has the routed
+// types and F (shared != NULL), else from ys[i] (the weighted output of the
+// shared-expert kernels, shared.h; NULL: none).
 struct ReduceArgs {
     const int32_t *ids;
     const float *weights;
@@ -62,10 +66,15 @@ struct ReduceArgs {
     uint64_t xq_vstride;
     const float *resid;
     float *out;
+    const float *ys;
 };
 
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
 hipError_t launch_expand(int gate_type, const ExpandArgs &a, hipStream_t s, int n_cu);
 hipError_t launch_reduce(int down_type, const ReduceArgs &a, hipStream_t s, int n_cu);
+// A shared expert with its own types or intermediate size (shared.h):
+// act = silu(gate . h) * (up . h) with h = rms_norm(x) * norm_w (norm_w NULL:
+// h = x), then ys = w * down . act.
+hipError_t launch_shared(const SharedArgs &a, const float *x, const float *norm_w, float eps, hipStream_t s);
 
 }  // namespace fo

@@ -28,6 +28,7 @@
 #include "formats.h"
 #include "moe.h"
 #include "q4k_mfma.h"
+#include "shared.h"
 #include "topk.h"
 
 namespace fo {
@@ -462,6 +463,7 @@ __global__ __launch_bounds__(1024) void k_reduce(ReduceArgs a) {
         float acc = 0.f;
         for (int e = 0; e < a.k; e++) acc = fmaf(a.weights[e], part[e][tid], acc);
         if (a.shared) acc = fmaf(a.shared_w ? *a.shared_w : 1.0f, part[a.k][tid], acc);
+        else if (a.ys) acc += a.ys[row0 + tid];
         a.out[row0 + tid] = (a.resid ? a.resid[row0 + tid] : 0.f) + acc;
     }
 }
@@ -531,6 +533,7 @@ __global__ __launch_bounds__(64 * kTileMaxWaves) void k_reduce_tile(ReduceArgs a
         float acc = 0.f;
         for (int e = 0; e < a.k; e++) acc = fmaf(a.weights[e], part[e][tid], acc);
         if (a.shared) acc = fmaf(a.shared_w ? *a.shared_w : 1.0f, part[a.k][tid], acc);
+        else if (a.ys) acc += a.ys[row0 + tid];
         a.out[row0 + tid] = (a.resid ? a.resid[row0 + tid] : 0.f) + acc;
     }
 }
@@ -576,6 +579,51 @@ hipError_t launch_reduce(int type, const ReduceArgs &a, hipStream_t s, int n_cu)
 #undef FO_K3T
 #undef FO_K3
     return hipErrorInvalidValue;
+}
+
+// ============================================================ shared expert, standalone
+// A shared expert whose types or intermediate size differ from the routed
+// experts' runs as these two kernels (its weight matrices are not those the
+// layer kernels are specialised for): gate/up with its own RMSNorm of x (any
+// H = 256 n, 4 rows per work-group), then the down role.
+__global__ __launch_bounds__(256) void k_shared_gateup(SharedArgs s, const float *__restrict__ x,
+                                                       const float *__restrict__ norm_w, float eps) {
+    extern __shared__ __attribute__((aligned(16))) float hs[];   // h [H]
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, H = s.H;
+    const int r = blockIdx.x * 4 + wv;
+    GateUpRaw<8> raw;   // H <= 8192: at most eight 16-value pieces per lane
+    shared_gateup_load<8>(s, r, raw);
+    float scale = 1.0f;
+    if (norm_w) {
+        float ss = 0.f;
+        for (int i = tid; i < H; i += 256) ss += x[i] * x[i];
+        ss = wave_sum_dpp(ss);
+        if (lane == 0) red[wv] = ss;
+        __syncthreads();
+        scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + eps);
+    }
+    for (int i = tid; i < H; i += 256) hs[i] = norm_w ? x[i] * scale * norm_w[i] : x[i];
+    __syncthreads();
+    shared_gateup_finish<8>(s, r, raw, hs);
+}
+
+__global__ __launch_bounds__(256) void k_shared_down(SharedArgs s) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sd_lds[];
+    shared_down_role(s, blockIdx.x, sd_lds);
+}
+
+hipError_t launch_shared(const SharedArgs &a, const float *x, const float *norm_w, float eps, hipStream_t st) {
+    if (!a.blob || !a.act || !a.ys || a.H <= 0 || a.H % 256 || a.H > 8192 || a.F <= 0 || a.F % 256 || a.F > 8192 ||
+        a.down_rpw <= 0)
+        return hipErrorInvalidValue;
+    k_shared_gateup<<<(a.F + 3) / 4, 256, (size_t)a.H * 4, st>>>(a, x, norm_w, eps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    SharedArgs b = a;
+    b.down_waves = 4;
+    k_shared_down<<<shared_down_wgs(b), 256, (size_t)a.F * 4, st>>>(b);
+    return hipGetLastError();
 }
 
 }  // namespace fo

@@ -1246,15 +1246,25 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
 // tile leaves mostly empty. Work unit = (thin tile, kPfThinTPW * 16 rows),
 // one wave per work-group, units dealt round-robin; F == 1024.
 constexpr int kPfThinTPW = 8;
-constexpr uint32_t kPfThinX = 3 * 1024 + 64 * 8;                  // one pair's prepared activation
+constexpr int kPfThinF = 1024;                                     // the one F this kernel is built for
+constexpr uint32_t kPfThinRow = kPfThinF / 256 * 210;              // Q6_K row: 840 bytes
+constexpr uint32_t kPfThinX = 3 * kPfThinF + kPfThinF / 16 * 8;    // one pair's prepared activation
 constexpr uint32_t kPfThinZero = 304;                              // zero A operands (as kT6Zero)
-constexpr uint32_t kPfThinTile = 16 * 840;                         // 13,440 bytes
+constexpr uint32_t kPfThinTile = 16 * kPfThinRow;                  // 13,440 bytes
+// 64 lanes x 16 activation values = one F = 1024 row per pair (lane = 16-value group)
+static_assert(kPfThinF == 64 * 16 && kPfThinRow == 840, "k_pf_down_thin's lane layout covers F = 1024 only");
+
+// Whether the Q6_K down projection's thin tiles take k_pf_down_thin (the one
+// place that decides; k_pf_group orders thin tiles last whatever it says).
+__host__ inline bool pf_thin_down(const PrefillArgs &a) {
+    return a.down_type == GGML_TYPE_Q6_K && a.F == kPfThinF && a.H % (16 * kPfThinTPW) == 0;
+}
 constexpr uint32_t kPfThinLds = kPfThin * kPfThinX + kPfThinZero + kPfThinTile;
 
 __global__ __launch_bounds__(64) void k_pf_down_thin(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
     constexpr int NV = (kPfThinTile + 1023) / 1024;
-    constexpr uint32_t rb = 840, limb_bytes = 3 * 1024;
+    constexpr uint32_t rb = kPfThinRow, limb_bytes = 3 * kPfThinF;
     const int lane = threadIdx.x;
     uint8_t *zero = sx + kPfThin * kPfThinX;
     uint8_t *tb = zero + kPfThinZero;
@@ -1480,7 +1490,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             }
             const int np = prefill_pairs(a.T, a.k, a.shared != nullptr);
             k_pf_actprep_w<<<(np + kApWaves - 1) / kApWaves, 64 * kApWaves, 0, s>>>(a, np);
-            a.thin_down = a.F == 1024 && a.H % (16 * kPfThinTPW) == 0;
+            a.thin_down = pf_thin_down(a);
             int dev = 0, n_cu = 256;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
             k_pf_down16<<<(kPfD16PerCU * n_cu + 7) & ~7, kPfD16Waves * 64, lds16, s>>>(a);   // persistent

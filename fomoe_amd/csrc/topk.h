@@ -105,14 +105,35 @@ FO_DEV float select_weight(float v, int k, bool prob) {
 // (false for non-finite values as well).
 FO_DEV bool logit_selection_exact(float first, float last) { return last - first > -kSatGap; }
 
+// Whether the logit order of the kr values held by lanes 0..kr-1 (largest
+// first, equal values in index order; the last is the best value left out of
+// a selection of kr-1) is also the order of their fp32 probabilities. Two
+// distinct logits a > b can round to the same p = expf(l - l_max) * inv, and
+// the reference then takes the lower index first. With d = l - l_max, p's
+// relative change is a - b, while the rounding of d (half an ulp of |d|),
+// expf (about an ulp) and the product with inv (half an ulp) move p by less
+// than 2^-21 max(1, |d|) relative; so adjacent logits that are equal or
+// further apart than 2^-20 max(1, |d|) keep their order in p, and any other
+// pair sends the selection to the rerun on p.
+FO_DEV bool logit_order_exact(float v, int kr, float first) {
+    const int lane = threadIdx.x & 63;
+    const float nx = __shfl_down(v, 1, kWave);
+    bool ok = true;
+    if (lane + 1 < kr) ok = v == nx || v - nx > 0x1p-20f * fmaxf(1.0f, fabsf(nx - first));
+    return __ballot(!ok) == 0;
+}
+
 // Selection of k over v (logits, or probabilities when prob; E <= 64*NV;
-// consumed); returns false when a logit selection must rerun on p.
+// consumed); returns false when a logit selection must rerun on p. Over
+// logits one more value is taken, the best one left out, for the order check
+// at the selection's boundary.
 template <int NV>
 FO_DEV bool wave_topk_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w, bool prob) {
     const int lane = threadIdx.x & 63;
+    const int kr = (!prob && k < E) ? k + 1 : k;
     float my_v = -FLT_MAX;   // lane kk keeps selection kk (no indexed private arrays:
     int my_i = 0;            // those would put the kernel on scratch, which throttles residency)
-    for (int kk = 0; kk < k; kk++) {
+    for (int kk = 0; kk < kr; kk++) {
         float lb = v[0];
         int lj = 0;
 #pragma unroll
@@ -131,7 +152,7 @@ FO_DEV bool wave_topk_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w, bo
     }
     const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
     const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), k - 1));
-    if (!prob && !logit_selection_exact(first, last)) return false;
+    if (!prob && (!logit_selection_exact(first, last) || !logit_order_exact(my_v, kr, first))) return false;
     const float wv = s_w ? select_weight(my_v, k, prob) : 0.f;
     if (lane < k) { s_ids[lane] = my_i; if (s_w) s_w[lane] = wv; }
     return true;
@@ -156,7 +177,9 @@ FO_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *s_ids
 // (value desc, index asc) against the next n-1 entries of that doubled list
 // with wave-wide DPP shifts. Falls back to k arg-max rounds when k > 16 or
 // more than 32 values tie in at T (or NaNs leave fewer than k candidates).
-// s_cand: 64 (value, index) slots, s_val: k values, both in LDS.
+// Over logits it ranks k+1 values (the boundary check of logit_order_exact;
+// s_ids and s_val then receive k+1 entries). s_cand: 64 (value, index)
+// slots, s_val: k + 1 values, both in LDS.
 template <int CTRL>
 FO_DEV float dpp_keep(float v) {   // lanes whose source is outside the row keep v
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
@@ -168,6 +191,7 @@ template <int NV>
 FO_DEV bool wave_topk_thr_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w, float2 *s_cand,
                             float *s_val, bool prob) {
     const int lane = threadIdx.x & 63, r = lane & 15;
+    const int kr = (!prob && k < E) ? k + 1 : k;   // logits: also the best one left out
     float mx = -FLT_MAX;
 #pragma unroll
     for (int j = 0; j < NV; j++) mx = fmaxf(mx, v[j]);   // NaNs drop out
@@ -184,14 +208,14 @@ FO_DEV bool wave_topk_thr_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w
     cx(__shfl_xor(mx, 31, kWave), !(lane & 16)); x8(); x4(); x2(); x1();                     // size 32
     cx(__shfl_xor(mx, 63, kWave), !(lane & 32)); cx(__shfl_xor(mx, 16, kWave), !(lane & 16));
     x8(); x4(); x2(); x1();                                    // size 64
-    bool ok = k <= 16;
+    bool ok = kr <= 16;
     int n = 0;
     if (ok) {
-        const float T = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), k - 1));
+        const float T = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), kr - 1));
         uint64_t m[NV];
 #pragma unroll
         for (int j = 0; j < NV; j++) { m[j] = __ballot(v[j] >= T); n += __popcll(m[j]); }
-        ok = n >= k && n <= 32;
+        ok = n >= kr && n <= 32;
         if (ok) {   // candidates in (j, lane) order at [0, n) and again at [n, 2n)
             int base = 0;
 #pragma unroll
@@ -218,11 +242,13 @@ FO_DEV bool wave_topk_thr_v(float (&v)[NV], int E, int k, int *s_ids, float *s_w
         oi = dpp_keep_i<0x130>(oi);
         rank += (ov > c.x || (ov == c.x && oi < ci)) ? 1 : 0;
     }
-    if (lane < n && rank < k) {
+    if (lane < n && rank < kr) {
         s_ids[rank] = (ci >= 0 && ci < E) ? ci : 0;
         s_val[rank] = c.x;
     }
-    if (!prob && !logit_selection_exact(s_val[0], s_val[k - 1])) return false;
+    if (!prob && (!logit_selection_exact(s_val[0], s_val[k - 1]) ||
+                  !logit_order_exact(lane < kr ? s_val[lane] : 0.f, kr, s_val[0])))
+        return false;
     if (s_w) {
         const float wv = select_weight(lane < k ? s_val[lane] : 0.f, k, prob);
         if (lane < k) s_w[lane] = wv;

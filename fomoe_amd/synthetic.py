@@ -89,6 +89,7 @@ def build_layer(gpu: Gpu, shape: LayerShape, layer: int, seed: int = 4,
     d.experts = experts.ptr
     d.shared = experts.offset(E * s.stride) if s.shared else None
     d.shared_inter, d.shared_gate_size, d.shared_up_size = F, s.gate_size, s.gate_size
+    d.shared_gate_type, d.shared_up_type, d.shared_down_type = s.gate_type, s.gate_type, s.down_type
     d.shared_gate_vec = None
     d.norm_w = norm_w.ptr if norm_w else None
     d.eps = 1e-6

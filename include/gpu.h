@@ -134,12 +134,15 @@ typedef struct {
     const float *router;        /* device [E x H] fp32 */
     const float *router_bias;   /* device [E] added to the logits, or NULL */
     const void *experts;        /* device, E blobs gate|up|down, expert_stride apart */
-    const void *shared;         /* device shared-expert blob, or NULL */
-    int shared_inter;           /* must equal inter */
-    uint64_t shared_gate_size, shared_up_size;
+    const void *shared;         /* device shared-expert blob gate|up|down, or NULL */
+    int shared_inter;           /* F_s, the shared expert's intermediate size */
+    uint64_t shared_gate_size, shared_up_size;   /* up at gate_size, down at gate+up */
     const float *shared_gate_vec; /* device [H]: shared output *= sigmoid(h.v); NULL: 1 */
     const float *norm_w;        /* device [H] RMSNorm weight, used with GPU_MOE_NORM */
     float eps;
+    /* the shared expert's own tensor types, each of Q4_K/Q5_K/Q6_K/Q8_0
+     * (reference include/model.h:108; read from ffn_*_shexp, src/model.c:365-371) */
+    int shared_gate_type, shared_up_type, shared_down_type;
 } gpu_moe_layer_t;
 
 #define GPU_MOE_NORM     1  /* h = rms_norm(in) * norm_w before routing */
@@ -156,11 +159,13 @@ int gpu_moe_layer(gpu_ctx_t *ctx, const gpu_moe_layer_t *layer, const float *d_i
  * gpu_moe_layer, bit-identical results). No counterpart in the reference; it
  * is for callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation). Its scratch is one static
- * device area of GPU_MOE_NOALLOC_SCRATCH_BYTES per device, held until the
- * process ends; a layer whose scratch (router logits, routing, prepared h, the
- * k+1 activations) does not fit returns -1 with a message. Every call on a
- * device shares that area: calls that overlap on one device (two contexts,
- * or two host threads) race. gpu_moe_last_routing reports its routing too. */
+ * device area of GPU_MOE_NOALLOC_SCRATCH_BYTES (contexts run on device 0),
+ * held until the process ends; a layer whose scratch (router logits, routing,
+ * prepared h, the k+1 activations, a shared expert's activation and output)
+ * does not fit returns -1 with a message. Every call shares that area: calls
+ * that overlap (two contexts, or two host threads) race, and the routing that
+ * gpu_moe_last_routing reports after a no-allocation call is read from the
+ * area, so it is that of the latest no-allocation call of any context. */
 #define GPU_MOE_NOALLOC_SCRATCH_BYTES (1u << 20)
 int gpu_moe_layer_noalloc(gpu_ctx_t *ctx, const gpu_moe_layer_t *layer, const float *d_in,
                           float *d_out, int flags);
@@ -289,7 +294,7 @@ void gpu_gguf_free_moe_layer(gpu_ctx_t *ctx, gpu_moe_layer_t *L);
  * a per-pair power of two (within ~6e-4 of the exact layer per token); other
  * types dequantized to bf16 (round to nearest even), with the activation as
  * two bf16 terms (hi + lo, within 2^-18). gate/up/down types Q4_K or Q6_K;
- * n_experts <= 1023; with Q4_K gate/up, the experts and shared pointers,
+ * a shared expert with the routed types and intermediate size; n_experts <= 1023; with Q4_K gate/up, the experts and shared pointers,
  * expert_stride and the gate sizes must be multiples of 16 bytes (-1 else). A batch larger than the grouping table (n_experts *
  * ceil(n_tokens/32) > 16384) runs as consecutive chunks of
  * (16384 / n_experts) * 32 tokens with the same results per token. No

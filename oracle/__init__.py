@@ -43,7 +43,8 @@ class MoeDesc(C.Structure):
                 ("router", _vp), ("router_bias", _vp), ("experts", _vp), ("shared", _vp),
                 ("shared_inter", C.c_int), ("shared_gate_size", C.c_uint64),
                 ("shared_up_size", C.c_uint64), ("shared_gate_vec", _vp), ("norm_w", _vp),
-                ("eps", C.c_float)]
+                ("eps", C.c_float), ("shared_gate_type", C.c_int), ("shared_up_type", C.c_int),
+                ("shared_down_type", C.c_int)]
 
 
 MOE_NORM, MOE_RESIDUAL = 1, 2

@@ -509,8 +509,8 @@ void fo_moe_layer(const fo_moe_desc *L, const float *in, float *out, int flags,
         for (int j = 0; j < H; j++) ffn[j] += sc[i] * dn[j];
     }
     if (L->shared) {
-        expert_ffn(L->shared, L->gate_type, L->up_type, L->down_type, L->shared_gate_size,
-                   L->shared_up_size, h, H, L->shared_inter, dn);
+        expert_ffn(L->shared, L->shared_gate_type, L->shared_up_type, L->shared_down_type,
+                   L->shared_gate_size, L->shared_up_size, h, H, L->shared_inter, dn);
         if (L->shared_gate_vec) {
             float dot = 0.0f;
             for (int j = 0; j < H; j++) dot += h[j] * L->shared_gate_vec[j];

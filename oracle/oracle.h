@@ -83,6 +83,8 @@ typedef struct {
     const float *shared_gate_vec; /* [H] sigmoid gate for the shared expert, or NULL */
     const float *norm_w;        /* [H] RMSNorm weight (used with FO_MOE_NORM) */
     float eps;
+    /* the shared expert's own tensor types (reference include/model.h:108) */
+    int shared_gate_type, shared_up_type, shared_down_type;
 } fo_moe_desc;
 
 #define FO_MOE_NORM     1   /* h = rms_norm(x) before routing */

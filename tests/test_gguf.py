@@ -280,13 +280,22 @@ def test_upload_tensor_and_f32(gpu, tmp_path):
             gpu.gguf_upload_f32(g, g.find_tensor("f32"), gpu.alloc(4 * 96), 95)
 
 
-def moe_model(E, H, F, k, seed, down_type=FA.Q6_K, router_type=FA.F32, shared=True):
+def moe_model(E, H, F, k, seed, down_type=FA.Q6_K, router_type=FA.F32, shared=True, shared_types=None,
+              Fs=None, fs_key=None):
     """Tensors of one MoE block (blk.0) in GGUF form and the same weights as
-    .qmoe-layout host blobs for the oracle."""
+    .qmoe-layout host blobs for the oracle (the shared expert's blob after the
+    E routed ones). The shared expert has the routed types and F unless
+    shared_types (gate, up, down) / Fs say otherwise; fs_key writes
+    {arch}.expert_shared_feed_forward_length."""
     rb_g, rb_d = O.row_bytes(O.Q4_K, H), O.row_bytes(down_type, F)
-    gate = [O.synth_quant(O.Q4_K, seed, 100 + e, 0.02, F, H) for e in range(E + 1)]
-    up = [O.synth_quant(O.Q4_K, seed, 300 + e, 0.02, F, H) for e in range(E + 1)]
-    down = [O.synth_quant(down_type, seed, 500 + e, 0.02, H, F) for e in range(E + 1)]
+    st = shared_types or (FA.Q4_K, FA.Q4_K, down_type)
+    Fs = Fs or F
+    gate = [O.synth_quant(O.Q4_K, seed, 100 + e, 0.02, F, H) for e in range(E)] + \
+        [O.synth_quant(st[0], seed, 100 + E, 0.02, Fs, H)]
+    up = [O.synth_quant(O.Q4_K, seed, 300 + e, 0.02, F, H) for e in range(E)] + \
+        [O.synth_quant(st[1], seed, 300 + E, 0.02, Fs, H)]
+    down = [O.synth_quant(down_type, seed, 500 + e, 0.02, H, F) for e in range(E)] + \
+        [O.synth_quant(st[2], seed, 500 + E, 0.02, H, Fs)]
     gs, ds = F * rb_g, H * rb_d
     router = O.synth_f32(seed, 1, 0.02, E * H)
     norm = (1.0 + O.synth_f32(seed, 2, 0.1, H)).astype(np.float32)
@@ -304,31 +313,48 @@ def moe_model(E, H, F, k, seed, down_type=FA.Q6_K, router_type=FA.F32, shared=Tr
                ("blk.0.ffn_gate_inp.weight", [H, E], router_type, rdata),
                ("blk.0.post_attention_norm.weight", [H], FA.BF16, normbf)]
     if shared:
-        tensors += [("blk.0.ffn_gate_shexp.weight", [H, F], FA.Q4_K, gate[E]),
-                    ("blk.0.ffn_up_shexp.weight", [H, F], FA.Q4_K, up[E]),
-                    ("blk.0.ffn_down_shexp.weight", [F, H], down_type, down[E]),
+        tensors += [("blk.0.ffn_gate_shexp.weight", [H, Fs], st[0], gate[E]),
+                    ("blk.0.ffn_up_shexp.weight", [H, Fs], st[1], up[E]),
+                    ("blk.0.ffn_down_shexp.weight", [Fs, H], st[2], down[E]),
                     ("blk.0.ffn_gate_inp_shexp.weight", [H], FA.F32, gvec)]
     kvs = [("general.architecture", STR, "qwen35moe"), ("qwen35moe.expert_used_count", U32, k),
            ("qwen35moe.attention.layer_norm_rms_epsilon", VF32, 1e-6)]
+    if fs_key is not None:
+        kvs.append(("qwen35moe.expert_shared_feed_forward_length", U32, fs_key))
     stride = (2 * gs + ds + 4095) // 4096 * 4096
-    blobs = np.zeros(E * stride + 2 * gs + ds, np.uint8)
-    for e in range(E + 1):
+    blobs = np.zeros(E * stride, np.uint8)
+    for e in range(E):
         o = e * stride
         blobs[o:o + gs], blobs[o + gs:o + 2 * gs], blobs[o + 2 * gs:o + 2 * gs + ds] = gate[e], up[e], down[e]
+    blobs = np.concatenate([blobs, gate[E], up[E], down[E]])
     return kvs, tensors, blobs, gs, ds, stride, router, norm, gvec
 
 
+SHEXP_CASES = {   # shared expert (gate, up, down) types and F_s differing from the routed Q4_K/Q4_K/down
+    "shexp_q6k_down": ((FA.Q4_K, FA.Q4_K, FA.Q6_K), 256),
+    "shexp_q8_0_down_fs512": ((FA.Q4_K, FA.Q4_K, FA.Q8_0), 512),
+    "shexp_q5k_q8_0_q6k_fs768": ((FA.Q5_K, FA.Q8_0, FA.Q6_K), 768),
+}
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("case", ["q6k_down_f32_router", "q4k_down_f16_router_no_shared"])
+@pytest.mark.parametrize("case", ["q6k_down_f32_router", "q4k_down_f16_router_no_shared"] + list(SHEXP_CASES))
 def test_load_moe_layer_runs_against_oracle(gpu, tmp_path, case):
     """blk.0 of a GGUF model made resident by gpu_gguf_load_moe_layer (expert
     tensors regrouped per expert at the 4096-aligned stride, router / norm /
     shared gate converted to fp32) and run through gpu_moe_layer with norm and
     residual, against the oracle on the same weights (reference
-    src/inference.c:481-606)."""
+    src/inference.c:481-606). The shexp cases give ffn_*_shexp their own types
+    and row count, as the reference reads them (src/model.c:164, 365-371),
+    with routed down in Q4_K."""
     E, H, F, k = 12, 512, 256, 4
     dt, rt, shared = (FA.Q6_K, FA.F32, True) if case.startswith("q6k") else (FA.Q4_K, FA.F16, False)
-    kvs, tensors, blobs, gs, ds, stride, router, norm, gvec = moe_model(E, H, F, k, 94, dt, rt, shared)
+    st, Fs = (FA.Q4_K, FA.Q4_K, dt), F
+    if case in SHEXP_CASES:
+        (st, Fs), dt, rt, shared = SHEXP_CASES[case], FA.Q4_K, FA.F32, True
+    kvs, tensors, blobs, gs, ds, stride, router, norm, gvec = moe_model(
+        E, H, F, k, 94, dt, rt, shared, shared_types=st, Fs=Fs, fs_key=Fs if case in SHEXP_CASES else None)
+    sgs, sus = O.row_bytes(st[0], H) * Fs, O.row_bytes(st[1], H) * Fs
     p = str(tmp_path / "moe.gguf")
     write_gguf(p, kvs, tensors)
     with FA.Gguf(p) as g:
@@ -338,6 +364,10 @@ def test_load_moe_layer_runs_against_oracle(gpu, tmp_path, case):
         assert (L.gate_type, L.up_type, L.down_type) == (FA.Q4_K, FA.Q4_K, dt)
         assert (L.gate_size, L.up_size, L.expert_stride) == (gs, gs, stride)
         assert abs(L.eps - 1e-6) < 1e-12 and bool(L.shared) == shared and bool(L.shared_gate_vec) == shared
+        if shared:
+            assert (L.shared_inter, L.shared_gate_size, L.shared_up_size) == (Fs, sgs, sus)
+            assert (L.shared_gate_type, L.shared_up_type, L.shared_down_type) == st
+            assert np.array_equal(gpu.download(L.shared, np.uint8, blobs.size - E * stride), blobs[E * stride:])
         assert np.array_equal(gpu.download(L.experts, np.uint8, E * stride), blobs[:E * stride])
         assert np.array_equal(gpu.download(L.router, np.float32, E * H), router)
         assert np.array_equal(gpu.download(L.norm_w, np.float32, H), norm)
@@ -352,7 +382,8 @@ def test_load_moe_layer_runs_against_oracle(gpu, tmp_path, case):
         d.router, d.experts = router.ctypes.data, blobs.ctypes.data
         if shared:
             d.shared = blobs.ctypes.data + E * stride
-            d.shared_inter, d.shared_gate_size, d.shared_up_size = F, gs, gs
+            d.shared_inter, d.shared_gate_size, d.shared_up_size = Fs, sgs, sus
+            d.shared_gate_type, d.shared_up_type, d.shared_down_type = st
             d.shared_gate_vec = gvec.ctypes.data
         d.norm_w, d.eps = norm.ctypes.data, 1e-6
         want, ids, w = O.moe_layer(d, x, O.MOE_NORM | O.MOE_RESIDUAL)
@@ -382,4 +413,11 @@ def test_load_moe_layer_rejects_bad_models(gpu, tmp_path):
     write_gguf(p, [kv for kv in kvs if kv[0] != "qwen35moe.expert_used_count"], tensors)
     with FA.Gguf(p) as g:
         with pytest.raises(FA.GpuError, match="expert_used_count"):
+            gpu.gguf_load_moe_layer(g, 0)
+    # a shared expert whose row count disagrees with the model's
+    # expert_shared_feed_forward_length key
+    kvs2, tensors2, *_ = moe_model(E, H, F, k, 96, fs_key=2 * F)
+    write_gguf(p, kvs2, tensors2)
+    with FA.Gguf(p) as g:
+        with pytest.raises(FA.GpuError, match="model key says"):
             gpu.gguf_load_moe_layer(g, 0)

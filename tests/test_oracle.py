@@ -268,6 +268,7 @@ def moe_desc(E, k, H, F, router, experts, gs, ds, shared_off=None, bias=None, no
     d.experts = experts.ctypes.data
     d.shared = experts.ctypes.data + shared_off if shared_off is not None else None
     d.shared_inter, d.shared_gate_size, d.shared_up_size = F, gs, gs
+    d.shared_gate_type, d.shared_up_type, d.shared_down_type = O.Q4_K, O.Q4_K, O.Q6_K
     d.shared_gate_vec = gvec.ctypes.data if gvec is not None else None
     d.norm_w = norm_w.ctypes.data if norm_w is not None else None
     d.eps = 1e-6
@@ -316,6 +317,44 @@ def test_moe_layer_fp64_recomposition():
     ref = sum(wt[i] * ffn(int(sel[i]) * stride) for i in range(k))
     ref = ref + ffn(E * stride) / (1 + np.exp(-(hn @ gvec.astype(np.float64))))
     assert parity_err(out, x + ref) < 1e-4
+
+
+@pytest.mark.parametrize("Fs,st", [(512, (O.Q8_0, O.Q5_K, O.Q6_K)), (256, (O.Q6_K, O.Q4_K, O.Q8_0))])
+def test_moe_layer_shared_own_types_fp64(Fs, st):
+    """A shared expert in its own tensor types and intermediate size
+    (reference include/model.h:104-108, src/inference.c:361-374): the oracle's
+    layer equals an fp64 recomposition, and handing it the routed types
+    instead changes the output (the types are really read)."""
+    E, k, H, F = 8, 3, 256, 256
+    router, h, experts, gs, ds = _moe_inputs(79, E, H, F)
+    stride = 2 * gs + ds
+    sh = [O.synth_quant(st[0], 80, 0, 0.02, Fs, H), O.synth_quant(st[1], 80, 1, 0.02, Fs, H),
+          O.synth_quant(st[2], 80, 2, 0.02, H, Fs)]
+    table = np.concatenate([experts[:E * stride]] + sh)
+    d = moe_desc(E, k, H, F, router, table, gs, ds, shared_off=E * stride)
+    d.shared_inter, d.shared_gate_size, d.shared_up_size = Fs, sh[0].size, sh[1].size
+    d.shared_gate_type, d.shared_up_type, d.shared_down_type = st
+    out, ids, w = O.moe_layer(d, h, 0)
+    hn = h.astype(np.float64)
+
+    def ffn(types, mats, Fe):
+        G, U, D = (O.dequantize(t, m, r * c).reshape(r, c).astype(np.float64)
+                   for t, m, r, c in zip(types, mats, (Fe, Fe, H), (H, H, Fe)))
+        g = G @ hn
+        return D @ (g / (1 + np.exp(-g)) * (U @ hn))
+
+    routed = [(experts[e * stride:e * stride + gs], experts[e * stride + gs:e * stride + 2 * gs],
+               experts[e * stride + 2 * gs:(e + 1) * stride]) for e in ids]
+    lg = router.reshape(E, H).astype(np.float64) @ hn
+    p = np.exp(lg - lg.max())
+    wt = p[ids] / p[ids].sum()
+    ref = sum(wt[i] * ffn((O.Q4_K, O.Q4_K, O.Q6_K), routed[i], F) for i in range(k)) + ffn(st, sh, Fs)
+    # the fp32 oracle's own sequential sums: 1.1e-4 measured at the 1e-3 floor
+    assert parity_err(out, ref) < 3e-4
+    d.shared_gate_type, d.shared_up_type, d.shared_down_type = O.Q4_K, O.Q4_K, O.Q6_K
+    d.shared_inter = min(Fs, F)
+    wrong, _, _ = O.moe_layer(d, h, 0)
+    assert not parity_err(wrong, ref) <= 1e-2   # (NaN too: other bytes read as fp16 scales)
 
 
 # ------------------------------------------------------------------ synthetic generator

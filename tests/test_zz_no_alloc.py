@@ -85,6 +85,7 @@ def test_noalloc_rejects_layers_beyond_the_area(gpu):
     L.expert_stride = 2 * L.gate_size + 8192 * FA.row_bytes(FA.Q6_K, 8192)
     L.router, L.experts, L.shared = dummy.ptr, dummy.ptr, dummy.ptr
     L.shared_inter, L.shared_gate_size, L.shared_up_size, L.eps = 8192, L.gate_size, L.gate_size, 1e-6
+    L.shared_gate_type, L.shared_up_type, L.shared_down_type = FA.Q4_K, FA.Q4_K, FA.Q6_K
     out = gpu.alloc(4 * 8192)
     assert gpu.moe_layer_noalloc(L, out, out, 0) == -1
     assert "scratch" in gpu.last_error()
