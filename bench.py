@@ -46,6 +46,20 @@ def log(*a):
 LEG_WARMUP = 50   # warmup steps of the rotation legs timed before the headline
 
 
+def spread_of(gpu, fn, n, scale=1.0, prefix=""):
+    """fn() timed n times one by one with HIP events on the context stream
+    (each call synchronised, so the idle gaps between calls are included in
+    none); p10 / p50 / p90 of the per-call times (ms, times scale)."""
+    each = []
+    for _ in range(n):
+        gpu.timer_start()
+        fn()
+        each.append(gpu.timer_stop() * scale)
+    p10, p50, p90 = np.percentile(each, [10, 50, 90])
+    return {f"{prefix}p10": round(float(p10), 4), f"{prefix}p50": round(float(p50), 4),
+            f"{prefix}p90": round(float(p90), 4), f"{prefix}n": n}
+
+
 class Rotation:
     """n_mats distinct [M x K] matrices of type t (matrix m from stream m of
     wseed; matrix 0 is the BASELINE config's W) times one x, one launch per
@@ -288,6 +302,9 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
     for i in range(layer_calls):
         gpu.moe_layer(layers[i % n_layers].desc, h, out, 0)
     us_layer_call = gpu.timer_stop() * 1e3 / layer_calls
+    it = iter(range(10 ** 9))
+    sp3 = spread_of(gpu, lambda: gpu.moe_layer(layers[next(it) % n_layers].desc, h, out, 0),
+                    max(layer_calls, 100), 1e3, "config3_us_per_call_")
     # config 4: the decode stack, x <- x + moe_l(rms_norm(x)), graph-replayed
     x = S.hidden(gpu, shape.n_embd)
     descs = [L.desc for L in layers]
@@ -297,6 +314,9 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
     gpu.stack_decode(descs, x, stack_steps)
     ms = gpu.timer_stop()
     xs = gpu.download(x, np.float32, shape.n_embd)
+    # per-step spread (after the state is read): one step per call replays the
+    # same captured graph
+    sp4 = spread_of(gpu, lambda: gpu.stack_decode(descs, x, 1), 100, 1e3 / n_layers, "config4_us_per_layer_step_")
     layer_bytes = 4 * shape.n_experts * shape.n_embd + (shape.k + 1) * shape.expert_bytes()
     tok_s = stack_steps / (ms / 1e3)
     us_layer = ms * 1e3 / (stack_steps * n_layers)
@@ -306,7 +326,7 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
         if cl:
             res.update(cl)
             res["config3_speedup_vs_cpu_layer"] = round(cl["cpu_layer_us"] / us_layer_call, 1)
-    return {**res,
+    return {**res, **sp3, **sp4,
         "config3_us_per_layer_call": round(us_layer_call, 2),
         "config4_layers": n_layers, "config4_steps": stack_steps,
         "config4_tok_per_s": round(tok_s, 2),
@@ -333,12 +353,13 @@ def prefill_config5(gpu, layer, shape, reps):
     for _ in range(reps):
         gpu.moe_prefill(layer.desc, x, T, out, 0)
     ms = gpu.timer_stop() / reps
+    sp5 = spread_of(gpu, lambda: gpu.moe_prefill(layer.desc, x, T, out, 0), max(reps, 100), 1.0, "config5_ms_")
     ids, _ = gpu.prefill_routing(T, k)
     n_unique = len(np.unique(ids)) + 1                      # + the shared expert
     pairs = T * (k + 1)
     flops = pairs * 6.0 * H * F + 2.0 * T * E * H
     wbytes = n_unique * shape.expert_bytes() + 4 * E * H   # each touched weight byte once
-    return {"config5_ms": round(ms, 4), "config5_tok_per_s": round(T / (ms / 1e3), 1),
+    return {**sp5, "config5_ms": round(ms, 4), "config5_tok_per_s": round(T / (ms / 1e3), 1),
             "config5_experts_touched": n_unique, "config5_weight_bytes": wbytes,
             "config5_GB/s": round(wbytes / (ms * 1e6), 1),
             "config5_frac_hbm": round(wbytes / (ms * 1e6) / HBM_PEAK_GBS, 4),

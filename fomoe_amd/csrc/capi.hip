@@ -465,22 +465,34 @@ int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_la
         if (!layers[l].norm_w) return fail(ctx, -1, "gpu_moe_stack_decode: layer %d has no norm_w", l);
     }
     if (n_steps == 0) return 0;
-    if (ctx->graph_exec) {
-        (void)hipGraphExecDestroy(ctx->graph_exec);
-        ctx->graph_exec = nullptr;
+    // The captured graph bakes in every pointer it was built from: the layer
+    // descriptors, x and the context's scratch. A call with the same ones
+    // replays it; anything else captures anew.
+    const LayerScratch sc = ctx_scratch(ctx);
+    std::vector<uint8_t> key(sizeof(gpu_moe_layer_t) * (size_t)n_layers + sizeof x + sizeof sc);
+    memcpy(key.data(), layers, sizeof(gpu_moe_layer_t) * (size_t)n_layers);
+    memcpy(key.data() + sizeof(gpu_moe_layer_t) * (size_t)n_layers, &x, sizeof x);
+    memcpy(key.data() + sizeof(gpu_moe_layer_t) * (size_t)n_layers + sizeof x, &sc, sizeof sc);
+    if (!ctx->graph_exec || key != ctx->graph_key) {
+        if (ctx->graph_exec) {
+            (void)hipGraphExecDestroy(ctx->graph_exec);
+            ctx->graph_exec = nullptr;
+        }
+        ctx->graph_key.clear();
+        HIPC(hipStreamSynchronize(ctx->stream));
+        HIPC(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        int rc = 0;
+        for (int l = 0; l < n_layers && !rc; l++)
+            rc = enqueue_layer(ctx, sc, &layers[l], x, x, GPU_MOE_NORM | GPU_MOE_RESIDUAL);
+        hipGraph_t g = nullptr;
+        hipError_t ce = hipStreamEndCapture(ctx->stream, &g);
+        if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+        if (ce != hipSuccess) return fail(ctx, -2, "graph capture failed: %s", hipGetErrorString(ce));
+        hipError_t ie = hipGraphInstantiate(&ctx->graph_exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ie != hipSuccess) return fail(ctx, -2, "graph instantiate failed: %s", hipGetErrorString(ie));
+        ctx->graph_key = std::move(key);
     }
-    HIPC(hipStreamSynchronize(ctx->stream));
-    HIPC(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    int rc = 0;
-    for (int l = 0; l < n_layers && !rc; l++)
-        rc = enqueue_layer(ctx, ctx_scratch(ctx), &layers[l], x, x, GPU_MOE_NORM | GPU_MOE_RESIDUAL);
-    hipGraph_t g = nullptr;
-    hipError_t ce = hipStreamEndCapture(ctx->stream, &g);
-    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
-    if (ce != hipSuccess) return fail(ctx, -2, "graph capture failed: %s", hipGetErrorString(ce));
-    hipError_t ie = hipGraphInstantiate(&ctx->graph_exec, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);
-    if (ie != hipSuccess) return fail(ctx, -2, "graph instantiate failed: %s", hipGetErrorString(ie));
     for (int s = 0; s < n_steps; s++) HIPC(hipGraphLaunch(ctx->graph_exec, ctx->stream));
     ctx->last_k = layers[n_layers - 1].k;
     ctx->last_ids = ctx->ids;

@@ -7,6 +7,7 @@
 #include <stdio.h>
 
 #include <string>
+#include <vector>
 
 #include "common.h"
 #include "gpu.h"
@@ -60,8 +61,10 @@ struct gpu_ctx {
     // values given to gpu_set_{ram,vram}_cache_mb (recorded; no cache tiers here)
     int ram_cache_mb = -1, vram_cache_mb = -1;
 
-    // captured stack-decode graph
+    // captured stack-decode graph and the bytes it was captured from
+    // (descriptors, x, scratch pointers)
     hipGraphExec_t graph_exec = nullptr;
+    std::vector<uint8_t> graph_key;
 };
 
 inline int fail(gpu_ctx *c, int code, const char *fmt, ...) {

@@ -179,7 +179,9 @@ int gpu_router_topk(gpu_ctx_t *ctx, const float *d_router, const float *d_bias,
 
 /* n_steps decode steps through n_layers layers, x <- x + moe_l(rms_norm(x))
  * per layer, in place on d_x[n_embd]. The per-step launch sequence is
- * captured once into a HIP graph and replayed. Async. */
+ * captured into a HIP graph and replayed; the next call with the same
+ * descriptors (byte for byte) and d_x replays that graph without capturing
+ * again (one call per decoded token costs one graph launch). Async. */
 int gpu_moe_stack_decode(gpu_ctx_t *ctx, const gpu_moe_layer_t *layers, int n_layers,
                          float *d_x, int n_steps);
 

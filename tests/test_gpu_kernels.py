@@ -770,6 +770,15 @@ def test_stack_decode_small_vs_oracle(gpu):
     e = parity_err(got, x)
     say(f"  parity_err {e:.3e}")
     assert e <= TOL
+    # one step per call replays the cached graph: bit-identical to two steps
+    # in one call; a call with other descriptors in between captures anew
+    descs = [L.desc for L in layers]
+    gpu.upload_to(dx, x0)
+    gpu.stack_decode(descs, dx, 1)
+    gpu.stack_decode(descs[:2], gpu.alloc(4 * shape.n_embd), 1)
+    gpu.stack_decode(descs, dx, 1)
+    gpu.sync()
+    assert np.array_equal(gpu.download(dx, np.float32, shape.n_embd), got)
 
 
 # ------------------------------------------------------------------ prefill (config 5)
@@ -815,6 +824,9 @@ PF_PARITY, PF_INF = 6e-3, 1e-5
 # 5.1-6.2e-4 per token on the oracle (the bf16 down weights it replaced:
 # 2.4-2.7e-3); bar 1.2e-3 per token.
 PF16_INF, PF16_EXACT = 3e-4, 1.2e-3
+# Per-element parity_err (1e-3 * ||ref||_inf floor) of config-5 tokens against
+# the exact layer: 2x the measured worst over all 512 tokens
+CONFIG5_PARITY_BAR = 0.85
 
 
 def pf_thin_tokens(ids, shape):
@@ -1055,22 +1067,41 @@ def test_prefill_config5_sampled(gpu):
         oi, ov = O.top_k(p, k)
         assert np.array_equal(ids[t], oi), t
         assert inf_rel(w[t, :k], ov / ov.sum()) < 1e-5
+    # every token against the batch-1 decode layer on its own (bf16) input:
+    # an independent GPU path, pinned to the oracle and to exact arithmetic
+    # by the config-3 tests (within ~1e-6 of exact)
+    dh = gpu.alloc(4 * H)
+    dl = gpu.alloc(4 * H)
+    dec = np.empty((T, H), np.float32)
+    for t in range(T):
+        gpu.upload_to(dh, xf[t])
+        gpu.moe_layer(L.desc, dh, dl, 0)
+        dec[t] = gpu.download(dl, np.float32, H)
+        gids, _, _ = gpu.last_routing(k)
+        assert np.array_equal(gids, ids[t]), t
+    ir = np.array([inf_rel(got[t], dec[t]) for t in range(T)])
+    pe = np.array([parity_err(got[t], dec[t]) for t in range(T)])
+    say(f"  PARITY config5 all {T} tokens vs decode layer: inf_rel worst {ir.max():.3e} median "
+        f"{np.median(ir):.3e}; parity_err worst {pe.max():.3e} median {np.median(pe):.3e}")
+    # the prefill's fp16 operand rounding is <= 6.2e-4 of ||out|| per token
+    # (PF16_EXACT's measurement) and the decode layer ~1e-6: inf_rel bar 1.5e-3
+    # (measured worst 5.2e-4 over the 512 tokens). Per element, that rounding
+    # is a few 1e-4 of ||out||_inf wherever an output is small, so parity_err
+    # (1e-3 floor) reaches 0.42 (median 0.18); bar about 2x the measured worst.
+    assert ir.max() < 1.5e-3
+    assert pe.max() < CONFIG5_PARITY_BAR
     sample = [0, 257, 511]
     need = sorted({int(v) for t in sample for v in ids[t]} | {E})
     d, keep = _prefill_host_layer(shape, 0, 4, True, None, need)
-    dh = gpu.alloc(4 * H)
-    dl = gpu.alloc(4 * H)
     for t in sample:
         say(f"  token {t}:")
         want, oids, _ = pf_check(got[t:t + 1], d, x, t, shape)
         assert np.array_equal(oids[0], ids[t])
-        gpu.upload_to(dh, xf[t])
-        gpu.moe_layer(L.desc, dh, dl, 0)
-        dec = gpu.download(dl, np.float32, H)
-        say(f"  token {t}: vs decode inf_rel {inf_rel(got[t], dec):.3e}")
-        # the decode layer is within ~1e-6 of exact; the prefill's own operand
-        # rounding is <= 6.2e-4 per token (PF16_EXACT's measurement)
-        assert inf_rel(got[t], dec) < 1.5e-3
+        exact, _, _ = O.moe_prefill(d, x, t, 1, 0, bf16_mask=pf_bf16_mask(shape) & 3)
+        say(f"  token {t}: parity_err vs same-rounding oracle {parity_err(got[t], want[0]):.3e}, "
+            f"vs exact {parity_err(got[t], exact[0]):.3e}, vs decode {pe[t]:.3e}; "
+            f"inf_rel vs same-rounding {inf_rel(got[t], want[0]):.3e}, vs exact {inf_rel(got[t], exact[0]):.3e}")
+        assert parity_err(got[t], exact[0]) < CONFIG5_PARITY_BAR
 
 
 def test_stack_decode_norm_and_shared_gate(gpu):
