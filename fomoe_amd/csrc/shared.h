@@ -4,19 +4,20 @@
 // shared_expert_ffn at src/inference.c:361-374: gate -> silu, up, mul, down,
 // then the sigmoid gate and the add of src/inference.c:585-595).
 //
-// It needs no routing, so it runs beside the routed experts rather than
-// after the top-k, in two "roles" that ride in work-groups of the layer's
-// kernels (moe.hip) or run as kernels of their own (the general path):
+// A shared expert with the routed experts' types and intermediate size rides
+// in the layer kernels as one more expert slot; any other runs as the two
+// kernels built from the roles below (moe.hip k_shared_gateup, k_shared_down),
+// after the router kernel and before the routed down projection, which adds
+// ys to its combine:
 //   gate/up role  act[r] = silu(gate[r,:] . h) * (up[r,:] . h), one row r per
 //                 wave, h = the (normed) layer input, in LDS;
 //   down role     ys[i] = w * (down[i,:] . act), w = the shared-expert weight
 //                 (sigmoid(h . v), or 1), act staged in LDS.
-// The kernels hosting a role keep its registers few: a lane holds one
-// 16-value piece per row in flight.
+// A lane holds one 16-value piece per row in flight.
 // Both are fp32 dot products over exactly dequantized weights — per value the
 // operation of the reference's vec_dot_*_f32 (src/quant.c:109-143, 177-212,
 // 249-262, 276-288): w = d1*q - m1 (Q4_K/Q5_K), (d*sc)*q (Q6_K), d*q (Q8_0),
-// then sum += w*x, with the partial sums of 64-value units added in a
+// then sum += w*x, with the partial sums of 16-value pieces added in a
 // different order. The shared expert is one matrix set per layer (8 MB at the
 // benchmark shape), so this path favours generality (any of the four layer
 // types per matrix, any F_s) over the integer-limb decoders of the routed

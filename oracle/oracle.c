@@ -384,14 +384,21 @@ float fo_vec_dot_q4_K_q8_K(const block_q4_K *x, const block_q8_K *y, int nb) {
     for (int i = 0; i < nb; i++) {
         const float d = y[i].d * fo_fp16_to_fp32(x[i].d);
         const float dmin = -y[i].d * fo_fp16_to_fp32(x[i].dmin);
+        /* the block's codes in value order, then exact integer sums per
+         * sub-block (integer order does not matter: vectorisable) */
+        uint8_t q[QK_K];
+        for (int c = 0; c < 4; c++)
+            for (int l = 0; l < 32; l++) {
+                q[64 * c + l] = x[i].qs[32 * c + l] & 0xF;
+                q[64 * c + 32 + l] = x[i].qs[32 * c + l] >> 4;
+            }
         int32_t sumi = 0, summ = 0;
         for (int j = 0; j < 8; j++) {
             uint8_t sc, m;
             fo_get_scale_min_k4(j, x[i].scales, &sc, &m);
-            const uint8_t *q = x[i].qs + 32 * (j / 2);
             const int8_t *q8 = y[i].qs + 32 * j;
             int32_t s = 0;
-            for (int l = 0; l < 32; l++) s += ((j & 1) ? (q[l] >> 4) : (q[l] & 0xF)) * q8[l];
+            for (int l = 0; l < 32; l++) s += q[32 * j + l] * q8[l];
             sumi += sc * s;
             summ += m * (y[i].bsums[2 * j] + y[i].bsums[2 * j + 1]);
         }
@@ -407,10 +414,22 @@ float fo_vec_dot_q6_K_q8_K(const block_q6_K *x, const block_q8_K *y, int nb) {
     float acc = 0.0f;
     for (int i = 0; i < nb; i++) {
         const float d = y[i].d * fo_fp16_to_fp32(x[i].d);
+        /* the block's codes in value order (q6_code), then exact integer
+         * sums per 16-wide scale group: the order of integer additions does
+         * not change them, so these loops may be vectorised freely */
+        int8_t q[QK_K];
+        for (int n = 0; n < 2; n++)
+            for (int l = 0; l < 32; l++) {
+                const uint8_t a = x[i].ql[64 * n + l], b = x[i].ql[64 * n + l + 32], h = x[i].qh[32 * n + l];
+                q[128 * n + l] = (int8_t)(((a & 0xF) | ((h & 3) << 4)) - 32);
+                q[128 * n + l + 32] = (int8_t)(((b & 0xF) | (((h >> 2) & 3) << 4)) - 32);
+                q[128 * n + l + 64] = (int8_t)(((a >> 4) | (((h >> 4) & 3) << 4)) - 32);
+                q[128 * n + l + 96] = (int8_t)(((b >> 4) | (((h >> 6) & 3) << 4)) - 32);
+            }
         int32_t sumi = 0;
         for (int s = 0; s < 16; s++) {
             int32_t p = 0;
-            for (int l = 0; l < 16; l++) p += q6_code(&x[i], 16 * s + l) * y[i].qs[16 * s + l];
+            for (int l = 0; l < 16; l++) p += q[16 * s + l] * y[i].qs[16 * s + l];
             sumi += x[i].scales[s] * p;
         }
         acc += d * (float)sumi;
