@@ -302,6 +302,7 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
     for i in range(layer_calls):
         gpu.moe_layer(layers[i % n_layers].desc, h, out, 0)
     us_layer_call = gpu.timer_stop() * 1e3 / layer_calls
+    shexp = shared_own_type_legs(gpu, layers, shape, h, out, min(n_layers, 30), layer_calls)
     it = iter(range(10 ** 9))
     sp3 = spread_of(gpu, lambda: gpu.moe_layer(layers[next(it) % n_layers].desc, h, out, 0),
                     max(layer_calls, 100), 1e3, "config3_us_per_call_")
@@ -326,7 +327,7 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
         if cl:
             res.update(cl)
             res["config3_speedup_vs_cpu_layer"] = round(cl["cpu_layer_us"] / us_layer_call, 1)
-    return {**res, **sp3, **sp4,
+    return {**res, **sp3, **sp4, **shexp,
         "config3_us_per_layer_call": round(us_layer_call, 2),
         "config4_layers": n_layers, "config4_steps": stack_steps,
         "config4_tok_per_s": round(tok_s, 2),
@@ -339,6 +340,39 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
         "weights_generation_s": round(gen_s, 1),
         "layer_algorithmic_bytes": layer_bytes,
     }
+
+
+def shared_own_type_legs(gpu, layers, shape, h, out, n, calls):
+    """Config 3 with the shared expert in its own tensor types, as GGUF
+    models carry it: (a) only ffn_down_shexp differs (Q8_0; gate/up ride in
+    the layer kernels, the down projection on the Q8_0 matvec kernel), (b)
+    gate Q5_K / up Q4_K / down Q8_0 at F_s = 512 (the fp32 shared-expert
+    kernels). n layers each get their own shared blob (no Infinity-Cache
+    reuse); us per layer call, event-timed over `calls` calls."""
+    H, F = shape.n_embd, shape.inter
+    res = {}
+    for name, (gt, ut, dt, Fs) in {"q8_0_down": (FA.Q4_K, FA.Q4_K, FA.Q8_0, F),
+                                  "q5k_q4k_q8_0_fs512": (FA.Q5_K, FA.Q4_K, FA.Q8_0, 512)}.items():
+        gs, us, ds = (FA.row_bytes(gt, H) * Fs, FA.row_bytes(ut, H) * Fs, FA.row_bytes(dt, Fs) * H)
+        blobs, descs = [], []
+        for l in range(n):
+            bl = gpu.alloc(gs + us + ds)
+            for t, off, M, K, kind in ((gt, 0, Fs, H, 0), (ut, gs, Fs, H, 1), (dt, gs + us, H, Fs, 2)):
+                gpu.synth_quant(t, 9, (l << 8) | kind, 0, 0.02, M, K, 1, bl.offset(off), 0)
+            d = FA.MoeLayer.from_buffer_copy(layers[l].desc)
+            d.shared, d.shared_inter, d.shared_gate_size, d.shared_up_size = bl.ptr, Fs, gs, us
+            d.shared_gate_type, d.shared_up_type, d.shared_down_type = gt, ut, dt
+            blobs.append(bl)
+            descs.append(d)
+        for i in range(3):
+            gpu.moe_layer(descs[i % n], h, out, 0)
+        gpu.sync()
+        gpu.timer_start()
+        for i in range(calls):
+            gpu.moe_layer(descs[i % n], h, out, 0)
+        res[f"config3_shexp_{name}_us_per_layer_call"] = round(gpu.timer_stop() * 1e3 / calls, 2)
+        del blobs
+    return res
 
 
 def prefill_config5(gpu, layer, shape, reps):

@@ -310,12 +310,23 @@ static SharedArgs shared_args(const LayerScratch &sc, const gpu_moe_layer_t *L, 
     return s;
 }
 
-// True when the shared expert has the routed experts' types and
-// intermediate size: it then rides in the layer kernels as expert slot k;
-// otherwise it runs as the shared-expert kernels of its own (shared.h).
-static bool shared_fused(const gpu_moe_layer_t *L) {
-    return L->shared && L->shared_inter == L->inter && L->shared_gate_type == L->gate_type &&
-           L->shared_up_type == L->up_type && L->shared_down_type == L->down_type;
+// How the fast path runs the shared expert: fused = with the routed experts'
+// types and intermediate size it is expert slot k of the layer kernels;
+// down-only = only its down projection differs in type (the usual GGUF mix):
+// its gate/up ride in k_expand as slot k (fp32 activation kept) and its down
+// projection runs on the matvec kernel; otherwise the shared-expert kernels
+// of shared.h.
+enum SharedMode { kSharedNone, kSharedFused, kSharedDownOnly, kSharedOwn };
+
+static SharedMode shared_mode(const gpu_moe_layer_t *L) {
+    if (!L->shared) return kSharedNone;
+    const bool gu = L->shared_inter == L->inter && L->shared_gate_type == L->gate_type &&
+                    L->shared_up_type == L->up_type && L->shared_gate_size == L->gate_size &&
+                    L->shared_up_size == L->up_size;
+    if (gu && L->shared_down_type == L->down_type) return kSharedFused;
+    if (gu && matvec_self_prep(L->shared_down_type, fomoe_row_bytes(L->shared_down_type, L->inter), L->inter, 0))
+        return kSharedDownOnly;
+    return kSharedOwn;
 }
 
 static int enqueue_layer_fast(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_moe_layer_t *L,
@@ -323,21 +334,37 @@ static int enqueue_layer_fast(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_
     const int H = L->n_embd, F = L->inter;
     const int dg = gsz_of(L->down_type);
     const uint64_t xs = xq_stride(F, dg);
-    const bool fused = shared_fused(L);
-    const uint8_t *base = (const uint8_t *)L->experts, *sh = fused ? (const uint8_t *)L->shared : nullptr;
+    const SharedMode mode = shared_mode(L);
+    const uint8_t *base = (const uint8_t *)L->experts, *sh = (const uint8_t *)L->shared;
+    const uint8_t *sh2 = (mode == kSharedFused || mode == kSharedDownOnly) ? sh : nullptr;   // slot k of k_expand
     float *shared_w = sc.weights + kSharedW;
     RouteArgs ra{L->router, L->router_bias, in, norm_w, L->eps, L->n_experts, H, sc.logits,
                  sc.xq_h, gsz_of(L->gate_type), L->shared_gate_vec, L->shared ? shared_w : nullptr};
     HIPC(launch_route(ra, ctx->stream));
-    if (L->shared && !fused) HIPC(launch_shared(shared_args(sc, L, shared_w), in, norm_w, L->eps, ctx->stream));
+    if (mode == kSharedOwn) HIPC(launch_shared(shared_args(sc, L, nullptr), in, norm_w, L->eps, ctx->stream));
     ExpandArgs ea{sc.logits, L->n_experts, L->k, sc.ids, sc.weights, base, L->expert_stride,
-                  L->gate_size, sh, L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H),
-                  sc.xq_h, sc.xq_act, xs, dg, nullptr};
+                  L->gate_size, sh2, L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H),
+                  sc.xq_h, sc.xq_act, xs, dg, mode == kSharedDownOnly ? sc.act : nullptr};
     HIPC(launch_expand(L->gate_type, ea, ctx->stream, ctx->n_cu));
-    ReduceArgs da{sc.ids, sc.weights, sh ? shared_w : nullptr, L->k, base, L->expert_stride,
-                  L->gate_size + L->up_size, sh, L->shared_gate_size + L->shared_up_size, F, H,
+    const bool fused = mode == kSharedFused;
+    ReduceArgs da{sc.ids, sc.weights, L->shared ? shared_w : nullptr, L->k, base, L->expert_stride,
+                  L->gate_size + L->up_size, fused ? sh : nullptr, L->shared_gate_size + L->shared_up_size, F, H,
                   fomoe_row_bytes(L->down_type, F), sc.xq_act, xs,
-                  (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out, (L->shared && !fused) ? sc.sh_ys : nullptr};
+                  (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out, mode == kSharedOwn ? sc.sh_ys : nullptr,
+                  -1, nullptr};
+    if (mode == kSharedDownOnly) {
+        const int sdt = L->shared_down_type;
+        if (reduce_takes_shared_type(L->down_type, da, sdt)) {   // one more block in k_reduce_tile
+            da.shared = sh;
+            da.sh_type = sdt;
+            da.sh_act = sc.act + (size_t)L->k * F;
+        } else {   // ys = down_s . act_s on the matvec kernel, unweighted
+            MatvecArgs ma{sh + L->shared_gate_size + L->shared_up_size, 0, fomoe_row_bytes(sdt, F), nullptr, 0,
+                          sc.sh_ys, 0, 1, H, F, sc.act + (size_t)L->k * F, 0};
+            HIPC(launch_matvec(sdt, ma, ctx->stream, ctx->n_cu));
+            da.ys = sc.sh_ys;
+        }
+    }
     HIPC(launch_reduce(L->down_type, da, ctx->stream, ctx->n_cu));
     return 0;
 }

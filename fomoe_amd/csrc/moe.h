@@ -49,8 +49,8 @@ struct ExpandArgs {
 // K3: out[i] = (resid ? resid[i] : 0) + sum_e w_e * down_e[i,:] . act_e over
 // the k routed experts in rank order, then the shared expert (weight
 // *shared_w, or 1 when NULL) — in the layer's kernels when it has the routed
-// types and F (shared != NULL), else from ys[i] (the weighted output of the
-// shared-expert kernels, shared.h; NULL: none).
+// types and F (shared != NULL), else from ys[i] (its down projection computed
+// by another kernel, weighted here by *shared_w; NULL: none).
 struct ReduceArgs {
     const int32_t *ids;
     const float *weights;
@@ -67,14 +67,20 @@ struct ReduceArgs {
     const float *resid;
     float *out;
     const float *ys;
+    int sh_type;            // -1: the shared block has the routed down type; else its own
+                            // type (F = 1024, reduce_takes_shared_type), from sh_act
+    const float *sh_act;    // [F] fp32 shared activation (sh_type >= 0)
 };
 
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
 hipError_t launch_expand(int gate_type, const ExpandArgs &a, hipStream_t s, int n_cu);
 hipError_t launch_reduce(int down_type, const ReduceArgs &a, hipStream_t s, int n_cu);
+// Whether launch_reduce runs a shared block of type sh_type beside routed
+// down projections of down_type for this shape.
+bool reduce_takes_shared_type(int down_type, const ReduceArgs &a, int sh_type);
 // A shared expert with its own types or intermediate size (shared.h):
 // act = silu(gate . h) * (up . h) with h = rms_norm(x) * norm_w (norm_w NULL:
-// h = x), then ys = w * down . act.
+// h = x), then ys = w * down . act (w = a.w, or 1 when NULL).
 hipError_t launch_shared(const SharedArgs &a, const float *x, const float *norm_w, float eps, hipStream_t s);
 
 }  // namespace fo

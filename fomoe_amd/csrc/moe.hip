@@ -463,7 +463,7 @@ __global__ __launch_bounds__(1024) void k_reduce(ReduceArgs a) {
         float acc = 0.f;
         for (int e = 0; e < a.k; e++) acc = fmaf(a.weights[e], part[e][tid], acc);
         if (a.shared) acc = fmaf(a.shared_w ? *a.shared_w : 1.0f, part[a.k][tid], acc);
-        else if (a.ys) acc += a.ys[row0 + tid];
+        else if (a.ys) acc = fmaf(a.shared_w ? *a.shared_w : 1.0f, a.ys[row0 + tid], acc);
         a.out[row0 + tid] = (a.resid ? a.resid[row0 + tid] : 0.f) + acc;
     }
 }
@@ -482,50 +482,93 @@ constexpr uint32_t kTileLdsMax = 152 * 1024;
 
 constexpr int kTileMaxWaves = 12;   // 3 waves per SIMD: room for a whole block in registers
 
+// One wave's 16-row block of matrix m (row0.., RBYTES per row) against the
+// prepared activation X: the block streams through the wave's LDS area `dst`
+// and its row dots land in part_w[0..16).
+template <int T, int G, int RBYTES>
+FO_DEV void tile_block_dots(const uint8_t *m, const typename Fmt<T>::X &X, uint8_t *dst, float *part_w, int row0,
+                            int H, int slot, float live) {
+    using F = Fmt<T>;
+    constexpr int P = kWave / G, RP = kTileRows / P;
+    constexpr uint32_t TB = kTileRows * RBYTES;
+    constexpr int NV = (TB + 1023) / 1024;
+    const int lane = threadIdx.x & 63, sub = lane / G;
+    const uint8_t *src = m + (uint64_t)row0 * RBYTES;
+    const uint32_t nb = (uint32_t)min(kTileRows, H - row0) * RBYTES;
+    // a piece that straddles the end is read from the last 16 valid bytes
+    // and written to that same position (identical bytes overlap)
+    auto pos = [&](uint32_t o) { return o + 16 <= nb ? o : nb - 16; };
+    uint4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = ldw16(src + pos(i * 1024 + lane * 16));
+    // keep the scheduler from sinking weight loads below the arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+    int written = 0;
+#pragma unroll
+    for (int p = 0; p < RP; p++) {
+        const int need = ((p + 1) * P * RBYTES + 1023) / 1024;   // pieces covering rows < (p+1)*P
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            if (i >= written && i < need) *(uint4 *)(dst + pos(i * 1024 + lane * 16)) = v[i];
+        written = need;
+        const int r = p * P + sub;
+        const typename F::Raw raw = F::load(dst + r * RBYTES, slot);
+        const float d = group_sum<G>(live * F::dot(raw, slot, X));
+        if ((lane % G) == 0) part_w[r] = d;
+    }
+}
+
+// The shared expert's block when its down projection has its own type TS
+// (F = 1024): the lane's activation slot is prepared from the fp32 shared
+// activation k_expand left (prep_group_regs, bit-identical to the prepared
+// form the routed experts read), then the block runs as a routed one.
+template <int TS>
+FO_DEV void shared_block_dots(const ReduceArgs &a, uint8_t *dst, float *part_w, int row0) {
+    using F = Fmt<TS>;
+    constexpr int S = 1024 / F::SLOT, G = S, RB = 1024 / (F::SLOT == 64 ? 256 : 32) * F::BLOCK;
+    const int slot = (threadIdx.x & 63) % G;
+    typename F::X X;
+    int gi[F::NG];
+    F::groups(slot, gi);
+#pragma unroll
+    for (int g = 0; g < F::NG; g++) prep_group_regs<F::GSZ>(a.sh_act + gi[g] * F::GSZ, X.l[g], X.sc[g], X.sum[g]);
+    tile_block_dots<TS, G, RB>(a.shared + a.sh_down_off, X, dst, part_w, row0, a.H, slot, 1.f);
+}
+
+// Tile bytes of a 16-row block of a 1024-wide row in type t.
+__host__ __device__ constexpr uint32_t tile_stride_1024(int t) {
+    return (uint32_t)kTileRows * (t == GGML_TYPE_Q4_K ? 576u : t == GGML_TYPE_Q5_K ? 704u
+                                  : t == GGML_TYPE_Q6_K ? 840u : 1088u);
+}
+
 template <int T, int G, int RBYTES>
 __global__ __launch_bounds__(64 * kTileMaxWaves) void k_reduce_tile(ReduceArgs a) {
     using F = Fmt<T>;
-    constexpr int P = kWave / G, RP = kTileRows / P;
     constexpr uint32_t TB = kTileRows * RBYTES, TSTRIDE = (TB + 15) & ~15u;
-    constexpr int NV = (TB + 1023) / 1024;
     extern __shared__ __attribute__((aligned(16))) uint8_t tiles[];
     __shared__ float part[kMaxK + 1][kTileRows];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, sub = lane / G;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const bool own = a.shared && a.sh_type >= 0;          // shared down in its own type
     const int n_tot = a.k + (a.shared ? 1 : 0);
     const int S = a.F / F::SLOT;
     const int slot = min(lane % G, S - 1);          // lanes past S mirror the last slot ...
     const float live = (lane % G) < S ? 1.f : 0.f;  // ... and contribute nothing
     const int row0 = blockIdx.x * kTileRows;
-    if (wv < n_tot) {
+    if (wv < n_tot && !(own && wv == a.k)) {
         const uint8_t *m = (wv < a.k) ? a.base + (uint64_t)a.ids[wv] * a.stride + a.down_off
                                       : a.shared + a.sh_down_off;
         typename F::X X;
         int gi[F::NG];
         F::groups(slot, gi);
         load_xslot(X, a.xq_act + (uint64_t)wv * a.xq_vstride, a.F, gi);
-        const uint8_t *src = m + (uint64_t)row0 * RBYTES;
-        const uint32_t nb = (uint32_t)min(kTileRows, a.H - row0) * RBYTES;
-        // a piece that straddles the end is read from the last 16 valid bytes
-        // and written to that same position (identical bytes overlap)
-        auto pos = [&](uint32_t o) { return o + 16 <= nb ? o : nb - 16; };
-        uint4 v[NV];
-#pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = ldw16(src + pos(i * 1024 + lane * 16));
-        // keep the scheduler from sinking weight loads below the arithmetic
-        __builtin_amdgcn_sched_barrier(0);
-        uint8_t *dst = tiles + wv * TSTRIDE;
-        int written = 0;
-#pragma unroll
-        for (int p = 0; p < RP; p++) {
-            const int need = ((p + 1) * P * RBYTES + 1023) / 1024;   // pieces covering rows < (p+1)*P
-#pragma unroll
-            for (int i = 0; i < NV; i++)
-                if (i >= written && i < need) *(uint4 *)(dst + pos(i * 1024 + lane * 16)) = v[i];
-            written = need;
-            const int r = p * P + sub;
-            const typename F::Raw raw = F::load(dst + r * RBYTES, slot);
-            const float d = group_sum<G>(live * F::dot(raw, slot, X));
-            if ((lane % G) == 0) part[wv][r] = d;
+        tile_block_dots<T, G, RBYTES>(m, X, tiles + wv * TSTRIDE, part[wv], row0, a.H, slot, live);
+    } else if (own && wv == a.k) {
+        uint8_t *dst = tiles + a.k * TSTRIDE;
+        switch (a.sh_type) {
+            case GGML_TYPE_Q4_K: shared_block_dots<GGML_TYPE_Q4_K>(a, dst, part[wv], row0); break;
+            case GGML_TYPE_Q5_K: shared_block_dots<GGML_TYPE_Q5_K>(a, dst, part[wv], row0); break;
+            case GGML_TYPE_Q6_K: shared_block_dots<GGML_TYPE_Q6_K>(a, dst, part[wv], row0); break;
+            default: shared_block_dots<GGML_TYPE_Q8_0>(a, dst, part[wv], row0); break;
         }
     }
     __syncthreads();
@@ -533,9 +576,26 @@ __global__ __launch_bounds__(64 * kTileMaxWaves) void k_reduce_tile(ReduceArgs a
         float acc = 0.f;
         for (int e = 0; e < a.k; e++) acc = fmaf(a.weights[e], part[e][tid], acc);
         if (a.shared) acc = fmaf(a.shared_w ? *a.shared_w : 1.0f, part[a.k][tid], acc);
-        else if (a.ys) acc += a.ys[row0 + tid];
+        else if (a.ys) acc = fmaf(a.shared_w ? *a.shared_w : 1.0f, a.ys[row0 + tid], acc);
         a.out[row0 + tid] = (a.resid ? a.resid[row0 + tid] : 0.f) + acc;
     }
+}
+
+// LDS of k_reduce_tile: k routed blocks of tstride bytes, then the shared
+// expert's block (its own type's size when sh_type >= 0).
+static uint32_t reduce_tile_lds(const ReduceArgs &a, uint32_t tstride) {
+    return a.k * tstride + (a.shared ? (a.sh_type >= 0 ? tile_stride_1024(a.sh_type) : tstride) : 0);
+}
+
+bool reduce_takes_shared_type(int down_type, const ReduceArgs &a, int sh_type) {
+    if (a.F != 1024 || a.H < kTileRows || a.k + 1 > kTileMaxWaves) return false;
+    if (down_type != GGML_TYPE_Q6_K && down_type != GGML_TYPE_Q4_K && down_type != GGML_TYPE_Q5_K) return false;
+    if (sh_type != GGML_TYPE_Q4_K && sh_type != GGML_TYPE_Q5_K && sh_type != GGML_TYPE_Q6_K && sh_type != GGML_TYPE_Q8_0)
+        return false;
+    ReduceArgs b = a;
+    b.shared = (const uint8_t *)1;
+    b.sh_type = sh_type;
+    return reduce_tile_lds(b, tile_stride_1024(down_type)) <= kTileLdsMax;
 }
 
 template <int T, int G, int RBYTES>
@@ -548,7 +608,7 @@ static hipError_t reduce_tile(const ReduceArgs &a, hipStream_t s) {
         attr = true;
     }
     const int n_tot = a.k + (a.shared ? 1 : 0);
-    const uint32_t lds = n_tot * ((kTileRows * RBYTES + 15) & ~15u);
+    const uint32_t lds = reduce_tile_lds(a, (kTileRows * RBYTES + 15) & ~15u);
     k_reduce_tile<T, G, RBYTES><<<(a.H + kTileRows - 1) / kTileRows, 64 * n_tot, lds, s>>>(a);
     return hipGetLastError();
 }
@@ -561,9 +621,11 @@ hipError_t launch_reduce(int type, const ReduceArgs &a, hipStream_t s, int n_cu)
     const int S = a.F / slot;
     int G = 4;
     while (G < S) G <<= 1;
-    // the LDS-staged variant when all n_tot 16-row blocks fit at once
-    if (n_tot <= kTileMaxWaves && n_tot * kTileRows * a.row_bytes <= kTileLdsMax && a.H >= kTileRows &&
-        a.F == 1024) {
+    // the LDS-staged variant when all n_tot 16-row blocks fit at once (and
+    // the only one that takes a shared block in its own type)
+    if (a.shared && a.sh_type >= 0 && !reduce_takes_shared_type(type, a, a.sh_type)) return hipErrorInvalidValue;
+    if (n_tot <= kTileMaxWaves && reduce_tile_lds(a, (uint32_t)(kTileRows * a.row_bytes + 15) & ~15u) <= kTileLdsMax &&
+        a.H >= kTileRows && a.F == 1024) {
         if (type == GGML_TYPE_Q6_K) return reduce_tile<GGML_TYPE_Q6_K, 16, 840>(a, s);
         if (type == GGML_TYPE_Q4_K) return reduce_tile<GGML_TYPE_Q4_K, 16, 576>(a, s);
         if (type == GGML_TYPE_Q5_K) return reduce_tile<GGML_TYPE_Q5_K, 16, 704>(a, s);

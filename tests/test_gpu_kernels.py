@@ -469,6 +469,12 @@ def test_moe_layer_shapes_vs_fp64(gpu, H, F, E, k, shared):
     (2048, 512, 1024, (O.Q6_K, O.Q6_K, O.Q5_K), 16, 5),
     (8192, 256, 256, (O.Q4_K, O.Q5_K, O.Q6_K), 6, 2),      # two 64-value units per lane in K1's role
     (768, 256, 1024, (O.Q8_0, O.Q5_K, O.Q4_K), 8, 2),      # general path (n_embd = 256 * odd)
+    # only the down projection differs: gate/up in the layer kernels, down in
+    # k_reduce_tile (F = 1024) or on the matvec kernel
+    (4096, 1024, 1024, (O.Q4_K, O.Q4_K, O.Q8_0), 8, 2),
+    (1024, 1024, 1024, (O.Q4_K, O.Q4_K, O.Q5_K), 12, 4),
+    (2048, 1024, 1024, (O.Q4_K, O.Q4_K, O.Q4_K), 16, 10),   # F = 1024: one more block in k_reduce_tile
+    (512, 256, 256, (O.Q4_K, O.Q4_K, O.Q4_K), 8, 3),      # routed down Q6_K, shared Q4_K (general matvec)
 ])
 @pytest.mark.parametrize("gate_vec", [False, True])
 def test_moe_layer_shared_own_types(gpu, H, F, Fs, stypes, E, k, gate_vec):
