@@ -474,6 +474,9 @@ def test_moe_layer_shapes_vs_fp64(gpu, H, F, E, k, shared):
     (4096, 1024, 1024, (O.Q4_K, O.Q4_K, O.Q8_0), 8, 2),
     (1024, 1024, 1024, (O.Q4_K, O.Q4_K, O.Q5_K), 12, 4),
     (2048, 1024, 1024, (O.Q4_K, O.Q4_K, O.Q4_K), 16, 10),   # F = 1024: one more block in k_reduce_tile
+    # own gate/up types at F_s = F = 1024: matvec kernels, down as k_reduce_tile's extra block
+    (4096, 1024, 1024, (O.Q5_K, O.Q5_K, O.Q6_K), 8, 2),
+    (4096, 1024, 1024, (O.Q8_0, O.Q4_K, O.Q8_0), 8, 2),
     (512, 256, 256, (O.Q4_K, O.Q4_K, O.Q4_K), 8, 3),      # routed down Q6_K, shared Q4_K (general matvec)
 ])
 @pytest.mark.parametrize("gate_vec", [False, True])
