@@ -649,13 +649,16 @@ hipError_t launch_reduce(int type, const ReduceArgs &a, hipStream_t s, int n_cu)
 // layer kernels are specialised for): gate/up with its own RMSNorm of x (any
 // H = 256 n, 4 rows per work-group), then the down role.
 __global__ __launch_bounds__(256) void k_shared_gateup(SharedArgs s, const float *__restrict__ x,
-                                                       const float *__restrict__ norm_w, float eps) {
+                                                       const float *__restrict__ norm_w, float eps, int split) {
     extern __shared__ __attribute__((aligned(16))) float hs[];   // h [H]
     __shared__ float red[4];
+    __shared__ float2 s_gu[4];
+    constexpr int PL = 4;   // pieces per lane and round: H / (16 * 64 * split * PL) rounds
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, H = s.H;
-    const int r = blockIdx.x * 4 + wv;
-    GateUpRaw<8> raw;   // H <= 8192: at most eight 16-value pieces per lane
-    shared_gateup_load<8>(s, r, raw);
+    const int r = blockIdx.x * (4 / split) + wv / split, part = wv % split;
+    const int rounds = (H / 16 + 64 * split * PL - 1) / (64 * split * PL);
+    GateUpRaw<PL> raw;
+    shared_gateup_load<PL>(s, r, part, split, 0, raw);
     float scale = 1.0f;
     if (norm_w) {
         float ss = 0.f;
@@ -667,7 +670,21 @@ __global__ __launch_bounds__(256) void k_shared_gateup(SharedArgs s, const float
     }
     for (int i = tid; i < H; i += 256) hs[i] = norm_w ? x[i] * scale * norm_w[i] : x[i];
     __syncthreads();
-    shared_gateup_finish<8>(s, r, raw, hs);
+    float g = 0.f, v = 0.f;
+    shared_gateup_finish<PL>(s, part, split, 0, raw, hs, g, v);
+    for (int q = 1; q < rounds; q++) {
+        shared_gateup_load<PL>(s, r, part, split, q, raw);
+        shared_gateup_finish<PL>(s, part, split, q, raw, hs, g, v);
+    }
+    g = group_sum<kWave>(g);
+    v = group_sum<kWave>(v);
+    if (lane == 0) s_gu[wv] = make_float2(g, v);
+    __syncthreads();
+    if (part == 0 && lane == 0 && r < s.F) {
+        float gs = s_gu[wv].x, us = s_gu[wv].y;
+        for (int q = 1; q < split; q++) { gs += s_gu[wv + q].x; us += s_gu[wv + q].y; }
+        s.act[r] = (gs / (1.0f + expf(-gs))) * us;
+    }
 }
 
 __global__ __launch_bounds__(256) void k_shared_down(SharedArgs s) {
@@ -679,7 +696,8 @@ hipError_t launch_shared(const SharedArgs &a, const float *x, const float *norm_
     if (!a.blob || !a.act || !a.ys || a.H <= 0 || a.H % 256 || a.H > 8192 || a.F <= 0 || a.F % 256 || a.F > 8192 ||
         a.down_rpw <= 0)
         return hipErrorInvalidValue;
-    k_shared_gateup<<<(a.F + 3) / 4, 256, (size_t)a.H * 4, st>>>(a, x, norm_w, eps);
+    const int split = shared_gateup_split(a.F);
+    k_shared_gateup<<<(a.F * split + 3) / 4, 256, (size_t)a.H * 4, st>>>(a, x, norm_w, eps, split);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     SharedArgs b = a;

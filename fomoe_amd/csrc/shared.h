@@ -190,41 +190,40 @@ __host__ __device__ inline int lanes_for(int K) {
     return g;
 }
 
-// Gate/up role, one row r per wave: the gate and up rows' pieces (PL per
-// lane, K = H) are requested by shared_gateup_load before the caller stages
-// h in LDS, so they are in flight meanwhile; shared_gateup_finish writes
-// act[r] = silu(gate . h) * (up . h).
+// Gate/up role: row r is split over `split` waves (split = 1, 2, 4), wave
+// `part` taking pieces part*64 + lane + 64*split*i of the H/16 pieces (at
+// most 4*ROUNDS per lane). The rows' pieces are requested by
+// shared_gateup_load before the caller stages h in LDS, so they are in flight
+// meanwhile; shared_gateup_finish returns this wave's partial gate and up sums
+// (the caller adds the parts in order and writes act[r] = silu(g) * u).
 template <int PL>
 struct GateUpRaw { PRaw g[PL], u[PL]; };
 
 template <int PL>
-FO_DEV void shared_gateup_load(const SharedArgs &s, int r, GateUpRaw<PL> &raw) {
+FO_DEV void shared_gateup_load(const SharedArgs &s, int r, int part, int split, int round, GateUpRaw<PL> &raw) {
     const int lane = threadIdx.x & 63, np = s.H / 16;
     const int rr = min(r, s.F - 1);
     const uint8_t *gr = s.blob + (uint64_t)rr * s.gate_rb, *ur = s.blob + s.up_off + (uint64_t)rr * s.up_rb;
 #pragma unroll
     for (int i = 0; i < PL; i++) {
-        const int p = min(lane + 64 * i, np - 1);
+        const int p = min(part * 64 + lane + 64 * split * (PL * round + i), np - 1);
         raw.g[i] = pload_t(s.gate_type, gr, p);
         raw.u[i] = pload_t(s.up_type, ur, p);
     }
 }
 
 template <int PL>
-FO_DEV void shared_gateup_finish(const SharedArgs &s, int r, const GateUpRaw<PL> &raw, const float *h_lds) {
+FO_DEV void shared_gateup_finish(const SharedArgs &s, int part, int split, int round, const GateUpRaw<PL> &raw,
+                                 const float *h_lds, float &g, float &v) {
     const int lane = threadIdx.x & 63, np = s.H / 16;
-    float g = 0.f, v = 0.f;
 #pragma unroll
     for (int i = 0; i < PL; i++) {
-        const int p = lane + 64 * i;
+        const int p = part * 64 + lane + 64 * split * (PL * round + i);
         if (p < np) {
             g += pdot_t(s.gate_type, raw.g[i], p, h_lds);
             v += pdot_t(s.up_type, raw.u[i], p, h_lds);
         }
     }
-    g = group_sum<kWave>(g);
-    v = group_sum<kWave>(v);
-    if (lane == 0 && r < s.F) s.act[r] = (g / (1.0f + expf(-g))) * v;
 }
 
 // Down role, work-group `wg` of down_waves waves (= blockDim.x / 64): rows
@@ -277,12 +276,11 @@ __host__ inline int shared_down_wgs(const SharedArgs &s) {
     const int rows = s.down_waves * s.down_rpw;
     return (s.H + rows - 1) / rows;
 }
-// Down rows per wave for F_s: ~16 Ki values of fp32-dot work per wave, whole
-// passes of four rows per lane group.
-__host__ inline int shared_down_rpw(int F) {
-    const int P = 64 / lanes_for(F);
-    const int r = (16384 / F) > 1 ? 16384 / F : 1;
-    return (r + 4 * P - 1) / (4 * P) * (4 * P);
-}
+// Down rows per wave for F_s: one pass of four rows per lane group (the
+// work-group count then reaches ~256 at the benchmark H).
+__host__ inline int shared_down_rpw(int F) { return 4 * (64 / lanes_for(F)); }
+// Waves per gate/up row: ~512 work-groups of 4 waves (two per CU) to spread
+// the fp32 dot arithmetic.
+__host__ inline int shared_gateup_split(int F) { return F >= 2048 ? 1 : F >= 1024 ? 2 : 4; }
 
 }  // namespace fo
