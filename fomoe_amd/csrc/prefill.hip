@@ -1098,25 +1098,29 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x tile
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), col = lane & 15, kg = lane >> 4;
     // items (tile, block of 256 rows) of this work-group's XCD (work-group i
-    // runs on XCD i % 8): the XCD takes every eighth tile in decreasing cost
-    // (the order k_pf_group records), so the XCDs get like work; its
-    // work-groups take its items u = i / 8, + G8, ..., the costliest first
+    // runs on XCD i % 8): the XCD takes row blocks x, x + 8 of every tile, in
+    // decreasing tile cost (the order k_pf_group records), so the XCDs get like
+    // work and all tiles of one expert read a row block through the same L2
+    // (an expert's tiles are neighbours in that order; down16 HBM reads -15 %
+    // against every eighth tile per XCD); its work-groups take its items
+    // u = i / 8, + G8, ..., the costliest first
     const int nt = a.n_tiles[a.thin_down ? 1 : 0], nrb = a.H / (32 * kPfD16Waves);   // thin tiles: k_pf_down_thin
-    const int x = blockIdx.x & 7, G8 = gridDim.x >> 3, per = (nt - x + 7) >> 3, n_u = per * nrb;
+    const int x = blockIdx.x & 7, G8 = gridDim.x >> 3;
+    const int nrbx = (nrb - x + 7) >> 3, n_u = nt * nrbx;     // row blocks x, x + 8, ... of every tile
     const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
     const int NK = a.F / 256;
     struct Item { int p0, n, row; const uint8_t *drow; bool ok; };
     auto item_at = [&](int u) {
         Item it;
-        const int tl = u / nrb;
+        const int tl = u / nrbx, rbk = x + 8 * (u - tl * nrbx);
         it.ok = u < n_u;
-        const int tile = a.tiles[4 * (it.ok ? x + 8 * tl : 0) + 3];
+        const int tile = a.tiles[4 * (it.ok ? tl : 0) + 3];
         const int4 t4 = *(const int4 *)(a.tiles + 4 * tile);
         const bool shared = t4.x == a.E;
         const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)t4.x * a.stride;
         const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
         it.p0 = t4.y; it.n = t4.z;
-        it.row = (u - tl * nrb) * (32 * kPfD16Waves) + 32 * wave + col;   // rows row, row + 16
+        it.row = rbk * (32 * kPfD16Waves) + 32 * wave + col;   // rows row, row + 16
         it.drow = blob + down_off + (uint64_t)it.row * db;
         return it;
     };
