@@ -19,9 +19,19 @@ def say(*a):
     print(*a, flush=True)
 
 
-def _layer_pair(gpu, shape, seed, flags):
+def _layer_pair(gpu, shape, seed, flags, shared_types=None):
     from fomoe_amd import synthetic as S
     L = S.build_layer(gpu, shape, 0, seed=seed, zipf_s=1.1, norm=True)
+    if shared_types is not None:   # a shared blob in its own (gate, up, down) types and F_s
+        (gt, ut, dt), Fs, H = shared_types[:3], shared_types[3], shape.n_embd
+        gs, us, ds = FA.row_bytes(gt, H) * Fs, FA.row_bytes(ut, H) * Fs, FA.row_bytes(dt, Fs) * H
+        blob = gpu.alloc(gs + us + ds)
+        for t, off, M, K, kind in ((gt, 0, Fs, H, 0), (ut, gs, Fs, H, 1), (dt, gs + us, H, Fs, 2)):
+            gpu.synth_quant(t, seed, 900 + kind, 0, 0.02, M, K, 1, blob.offset(off), 0)
+        L.buffers.append(blob)
+        d = L.desc
+        d.shared, d.shared_inter, d.shared_gate_size, d.shared_up_size = blob.ptr, Fs, gs, us
+        d.shared_gate_type, d.shared_up_type, d.shared_down_type = gt, ut, dt
     x = O.synth_f32(seed + 1, 0, 1.0, shape.n_embd)
     dx = gpu.upload(x)
     ref, got = gpu.alloc(4 * shape.n_embd), gpu.alloc(4 * shape.n_embd)
@@ -71,6 +81,19 @@ def test_noalloc_matches_moe_layer_on_consecutive_calls(gpu):
     shape = S.LayerShape(n_embd=768, inter=256, n_experts=8, k=2)
     say("noalloc call 3", shape)
     _layer_pair(gpu, shape, 53, FA.MOE_NORM)
+
+
+@pytest.mark.parametrize("st", [((FA.Q4_K, FA.Q4_K, FA.Q8_0), 1024), ((FA.Q5_K, FA.Q4_K, FA.Q8_0), 512)])
+def test_noalloc_shared_expert_own_types(gpu, st):
+    """A shared expert whose down type alone differs (its block in the
+    reduce kernel) and one in types and F_s of its own (the fp32 shared-expert
+    kernels): the no-allocation call stays bit-identical to gpu_moe_layer,
+    twice in a row."""
+    from fomoe_amd import synthetic as S
+    shape = S.LayerShape(n_embd=4096, inter=1024, n_experts=32, k=8)
+    say("noalloc shared own types", st)
+    for seed in (81, 82):
+        _layer_pair(gpu, shape, seed, FA.MOE_NORM | FA.MOE_RESIDUAL, shared_types=(*st[0], st[1]))
 
 
 def test_noalloc_rejects_layers_beyond_the_area(gpu):
