@@ -90,7 +90,8 @@ void gpu_free(gpu_ctx_t *c) {
     void *bufs[] = {c->logits, c->counter, c->ids, c->weights, c->xq_h, c->xq_act, c->act,
                     c->act2, c->vec_in, c->vec_out, c->staging, c->pf_logits, c->pf_ids,
                     c->pf_w, c->pf_pairpos, c->pf_pairtok, c->pf_tiles, c->pf_ntiles,
-                    c->pf_act, c->pf_outp, c->pf_xsum, c->pf_rsplit, c->sh_act, c->sh_ys};
+                    c->pf_act, c->pf_outp, c->pf_xsum, c->pf_rsplit, c->sh_act, c->sh_ys,
+                    c->pf_ys, c->pf_ids2, c->pf_zrouter};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     for (int b = 0; b < 2; b++) {
@@ -675,23 +676,30 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     const bool pt = (L->gate_type == GGML_TYPE_Q4_K || L->gate_type == GGML_TYPE_Q6_K) &&
                     (L->down_type == GGML_TYPE_Q4_K || L->down_type == GGML_TYPE_Q6_K);
     if (!pt) return fail(ctx, -1, "moe prefill: gate/up/down types must be Q4_K or Q6_K");
-    if (L->shared && (L->shared_inter != L->inter || L->shared_gate_type != L->gate_type ||
-                      L->shared_up_type != L->up_type || L->shared_down_type != L->down_type))
-        return fail(ctx, -1, "moe prefill: the shared expert's types and intermediate size must equal the "
-                             "routed experts' (gpu_moe_layer takes any)");
+    // a shared expert in other types or F_s runs as a one-expert pass of its
+    // own (every token routed to it), whose output the routed pass combines
+    const bool own = L->shared && (L->shared_inter != L->inter || L->shared_gate_type != L->gate_type ||
+                                   L->shared_up_type != L->up_type || L->shared_down_type != L->down_type);
+    auto pf_type = [](int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K; };
+    if (own && !(pf_type(L->shared_gate_type) && pf_type(L->shared_up_type) && pf_type(L->shared_down_type)))
+        return fail(ctx, -1, "moe prefill: shared-expert types must be Q4_K or Q6_K");
     const int T = n_tokens, E = L->n_experts, k = L->k, H = L->n_embd, F = L->inter;
     if (E > 1023) return fail(ctx, -1, "moe prefill: n_experts %d > 1023", E);
     if (L->gate_type == GGML_TYPE_Q4_K) {   // its gate/up rows move by direct 16-byte global->LDS loads
         auto a16 = [](uint64_t v) { return v % 16 == 0; };
         if (!a16((uintptr_t)L->experts) || !a16(L->expert_stride) || !a16(L->gate_size) ||
-            (L->shared && (!a16((uintptr_t)L->shared) || !a16(L->shared_gate_size))))
+            (L->shared && !own && (!a16((uintptr_t)L->shared) || !a16(L->shared_gate_size))))
             return fail(ctx, -1, "moe prefill: Q4_K gate/up blobs must be 16-byte aligned "
                                  "(experts, shared, expert_stride, gate sizes)");
     }
     // the grouping table holds n_experts x ceil(tokens/32) words: larger
     // batches run as consecutive chunks (the results per token are the same)
     const int Tc = std::min(T, (16384 / E) * 32);
-    const bool sh = L->shared != nullptr;
+    if (own && L->shared_gate_type == GGML_TYPE_Q4_K &&
+        ((uintptr_t)L->shared % 16 || L->shared_gate_size % 16))
+        return fail(ctx, -1, "moe prefill: a Q4_K shared blob and its gate size must be 16-byte aligned");
+    const bool sh = L->shared != nullptr && !own;
+    const int Fs = own ? L->shared_inter : F;
     const size_t P = (size_t)fo::prefill_pairs(Tc, k, sh);
     const int max_tiles = fo::prefill_max_tiles(Tc, k, E, sh);
     HIPC(ensure(ctx->pf_logits, ctx->pf_logits_cap, sizeof(float) * (size_t)Tc * E));
@@ -699,9 +707,19 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     HIPC(ensure(ctx->pf_w, ctx->pf_w_cap, sizeof(float) * (size_t)T * (k + 1)));
     HIPC(ensure(ctx->pf_pairpos, ctx->pf_pairpos_cap, sizeof(int32_t) * (size_t)Tc * (k + 1)));
     HIPC(ensure(ctx->pf_pairtok, ctx->pf_pairtok_cap, sizeof(int32_t) * P));
-    HIPC(ensure(ctx->pf_tiles, ctx->pf_tiles_cap, sizeof(int32_t) * 4 * (size_t)max_tiles));
+    HIPC(ensure(ctx->pf_tiles, ctx->pf_tiles_cap,
+                sizeof(int32_t) * 4 * (size_t)std::max(max_tiles, fo::prefill_max_tiles(Tc, 1, 1, false))));
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
-    HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * P * F));
+    const size_t Pact = std::max(P * F, (size_t)Tc * Fs);   // activation elements of either pass
+    HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * Pact));
+    if (own) {   // the shared pass: its output [Tc x H], routing [Tc] / [Tc x 2], a zero router row
+        HIPC(ensure(ctx->pf_ys, ctx->pf_ys_cap, sizeof(float) * (size_t)Tc * H));
+        HIPC(ensure(ctx->pf_ids2, ctx->pf_ids2_cap, sizeof(int32_t) * (size_t)Tc * 3));
+        if (ctx->pf_zrouter_cap < sizeof(float) * (size_t)H) {
+            HIPC(ensure(ctx->pf_zrouter, ctx->pf_zrouter_cap, sizeof(float) * (size_t)H));
+            HIPC(hipMemsetAsync(ctx->pf_zrouter, 0, sizeof(float) * (size_t)H, ctx->stream));
+        }
+    }
     HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
     HIPC(ensure(ctx->pf_rsplit, ctx->pf_rsplit_cap, sizeof(uint16_t) * fo::prefill_router_ws_elems(E, Tc, H)));
     // xsum [Tc x H/32] fp32, then x16 [Tc x H] fp16, then xexp [Tc] int32, then pexp [P] int32
@@ -713,12 +731,14 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.router = L->router; a.router_bias = L->router_bias;
     a.experts = (const uint8_t *)L->experts; a.stride = L->expert_stride;
     a.gate_size = L->gate_size; a.up_size = L->up_size;
-    a.shared = (const uint8_t *)L->shared; a.sh_gate_size = L->shared_gate_size; a.sh_up_size = L->shared_up_size;
+    a.shared = sh ? (const uint8_t *)L->shared : nullptr;
+    a.sh_gate_size = L->shared_gate_size; a.sh_up_size = L->shared_up_size;
+    a.ys = own ? ctx->pf_ys : nullptr;
     a.shared_gate_vec = L->shared_gate_vec;
     a.residual = (flags & GPU_MOE_RESIDUAL) ? 1 : 0;
     a.logits = ctx->pf_logits; a.pairpos = ctx->pf_pairpos;
     a.pair_tok = ctx->pf_pairtok; a.tiles = ctx->pf_tiles; a.n_tiles = ctx->pf_ntiles;
-    a.act_hi = ctx->pf_act; a.act_lo = ctx->pf_act + P * F; a.outp = ctx->pf_outp;
+    a.act_hi = ctx->pf_act; a.act_lo = ctx->pf_act + Pact; a.outp = ctx->pf_outp;
     a.xsum = ctx->pf_xsum;
     a.x16 = (uint16_t *)((uint8_t *)ctx->pf_xsum + xs_bytes);
     a.xexp = (int32_t *)((uint8_t *)ctx->pf_xsum + xs_bytes + x16_bytes);
@@ -732,6 +752,21 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
         a.out = d_out + (size_t)t0 * H;
         a.ids = ctx->pf_ids + (size_t)t0 * k;
         a.w = ctx->pf_w + (size_t)t0 * (k + 1);
+        if (own) {   // shared pass first: ys = shared_ffn(x) for the chunk's tokens
+            fo::PrefillArgs b = a;
+            b.E = 1; b.k = 1; b.F = Fs;
+            b.gate_type = L->shared_gate_type; b.up_type = L->shared_up_type; b.down_type = L->shared_down_type;
+            b.router = ctx->pf_zrouter; b.router_bias = nullptr;   // every logit 0: one expert, weight 1
+            b.experts = (const uint8_t *)L->shared;
+            const uint64_t sds = fomoe_row_bytes(L->shared_down_type, Fs) * (uint64_t)H;
+            b.stride = (L->shared_gate_size + L->shared_up_size + sds + 15) & ~(uint64_t)15;
+            b.gate_size = L->shared_gate_size; b.up_size = L->shared_up_size;
+            b.shared = nullptr; b.shared_gate_vec = nullptr; b.ys = nullptr;
+            b.residual = 0; b.out = ctx->pf_ys;
+            b.ids = ctx->pf_ids2; b.w = (float *)(ctx->pf_ids2 + Tc);
+            b.max_tiles = fo::prefill_max_tiles(n, 1, 1, false);
+            HIPC(fo::launch_prefill(b, ctx->stream));
+        }
         HIPC(fo::launch_prefill(a, ctx->stream));
     }
     ctx->pf_T = T;

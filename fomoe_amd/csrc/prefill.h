@@ -25,6 +25,8 @@ struct PrefillArgs {
     const uint8_t *shared;       // shared blob or NULL
     uint64_t sh_gate_size, sh_up_size;
     const float *shared_gate_vec;  // [H] or NULL
+    const float *ys;             // [T x H] or NULL: a shared expert's output computed by a pass of
+                                 // its own, combined as the shared pair (weight w[t, k])
     // tokens
     int T;
     const uint16_t *x;           // [T x H] bf16

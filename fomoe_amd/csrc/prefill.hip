@@ -1367,11 +1367,12 @@ __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
                 acc.x = acc.x + s_w[r] * o[r].x; acc.y = acc.y + s_w[r] * o[r].y;
                 acc.z = acc.z + s_w[r] * o[r].z; acc.w = acc.w + s_w[r] * o[r].w;
             }
-        if (a.shared) {
+        if (a.shared || a.ys) {
             float4 sh = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (a.ys) sh = *(const float4 *)(a.ys + (uint64_t)t * a.H + 4 * i4);
 #pragma unroll
             for (int r = 0; r <= kMaxK; r++)
-                if (r == a.k) sh = o[r];
+                if (r == a.k && a.shared) sh = o[r];
             const float ws = s_w[a.k];
             acc.x = acc.x + sh.x * ws; acc.y = acc.y + sh.y * ws;
             acc.z = acc.z + sh.z * ws; acc.w = acc.w + sh.w * ws;

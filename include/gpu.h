@@ -296,7 +296,11 @@ void gpu_gguf_free_moe_layer(gpu_ctx_t *ctx, gpu_moe_layer_t *L);
  * a per-pair power of two (within ~6e-4 of the exact layer per token); other
  * types dequantized to bf16 (round to nearest even), with the activation as
  * two bf16 terms (hi + lo, within 2^-18). gate/up/down types Q4_K or Q6_K;
- * a shared expert with the routed types and intermediate size; n_experts <= 1023; with Q4_K gate/up, the experts and shared pointers,
+ * shared expert types Q4_K or Q6_K too: with the routed types and
+ * intermediate size it is one more pair per token in the routed pass, in
+ * types or an intermediate size of its own it runs first as a one-expert
+ * pass whose output the routed pass adds at the shared weight;
+ * n_experts <= 1023; with Q4_K gate/up, the experts and shared pointers,
  * expert_stride and the gate sizes must be multiples of 16 bytes (-1 else). A batch larger than the grouping table (n_experts *
  * ceil(n_tokens/32) > 16384) runs as consecutive chunks of
  * (16384 / n_experts) * 32 tokens with the same results per token. No

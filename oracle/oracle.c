@@ -621,21 +621,25 @@ static void matvec_f64(float *out, const float *m, const float *v, int rows, int
 
 /* bf16_mask: bit 0 gate, bit 1 up, bit 2 down weights rounded to bf16;
  * bit 3: a Q6_K down projection on fp16 operands (deq_q6_K_f16ops weights,
- * act_f16 activation) instead */
-static void expert_ffn_bf16(const uint8_t *blob, const fo_moe_desc *L, uint64_t gs, uint64_t us,
+ * act_f16 activation) instead; bit 4: bits 0-3 chosen per expert from its
+ * types as the GPU prefill does (exact Q4_K/Q4_K gate/up, else bf16; fp16
+ * operands for a Q6_K down projection with F <= 4096, else bf16) */
+static void expert_ffn_bf16(const uint8_t *blob, int gt, int ut, int dt, int H, int F, uint64_t gs, uint64_t us,
                             const float *x, float *out, int bf16_mask) {
-    const int H = L->n_embd, F = L->inter;
+    if (bf16_mask & 16)
+        bf16_mask = ((gt == GGML_TYPE_Q4_K && ut == GGML_TYPE_Q4_K) ? 0 : 3) |
+                    ((dt == GGML_TYPE_Q6_K && F <= 4096) ? 8 : 4);
     float *g = (float *)malloc(sizeof(float) * (size_t)F * 2), *u = g + F;
-    float *wg = deq_bf16(blob, L->gate_type, F, H, (bf16_mask & 1) ? 1 : 0);
+    float *wg = deq_bf16(blob, gt, F, H, (bf16_mask & 1) ? 1 : 0);
     matvec_f64(g, wg, x, F, H);
     free(wg);
-    float *wu = deq_bf16(blob + gs, L->up_type, F, H, (bf16_mask & 2) ? 1 : 0);
+    float *wu = deq_bf16(blob + gs, ut, F, H, (bf16_mask & 2) ? 1 : 0);
     matvec_f64(u, wu, x, F, H);
     free(wu);
     for (int i = 0; i < F; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
-    const int f16 = (bf16_mask & 8) && L->down_type == GGML_TYPE_Q6_K;
+    const int f16 = (bf16_mask & 8) && dt == GGML_TYPE_Q6_K;
     const int s = f16 ? act_f16(g, F) : 0;
-    float *wd = deq_bf16(blob + gs + us, L->down_type, H, F, f16 ? 2 : (bf16_mask & 4) ? 1 : 0);
+    float *wd = deq_bf16(blob + gs + us, dt, H, F, f16 ? 2 : (bf16_mask & 4) ? 1 : 0);
     matvec_f64(out, wd, g, H, F);
     if (f16)
         for (int r = 0; r < H; r++) out[r] = ldexpf(out[r], s);
@@ -662,13 +666,14 @@ void fo_moe_prefill_w(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, f
         if (ssum > 0.0f) { const float inv = 1.0f / ssum; for (int i = 0; i < k; i++) sc[i] *= inv; }
         memset(ffn, 0, sizeof(float) * (size_t)H);
         for (int i = 0; i < k; i++) {
-            expert_ffn_bf16(L->experts + (uint64_t)ids[i] * L->expert_stride, L, L->gate_size, L->up_size, h, dn,
-                            bf16_mask);
+            expert_ffn_bf16(L->experts + (uint64_t)ids[i] * L->expert_stride, L->gate_type, L->up_type,
+                            L->down_type, H, L->inter, L->gate_size, L->up_size, h, dn, bf16_mask);
             for (int j = 0; j < H; j++) ffn[j] += sc[i] * dn[j];
         }
         float gsc = 1.0f;
         if (L->shared) {
-            expert_ffn_bf16(L->shared, L, L->shared_gate_size, L->shared_up_size, h, dn, bf16_mask);
+            expert_ffn_bf16(L->shared, L->shared_gate_type, L->shared_up_type, L->shared_down_type, H,
+                            L->shared_inter, L->shared_gate_size, L->shared_up_size, h, dn, bf16_mask);
             if (L->shared_gate_vec) {
                 float dot = 0.0f;
                 for (int j = 0; j < H; j++) dot += h[j] * L->shared_gate_vec[j];

@@ -110,7 +110,9 @@ void     fo_fp32_to_bf16_n(const float *x, uint16_t *y, int64_t n);
 void fo_moe_prefill(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
                     int *ids_out, float *w_out);
 /* As fo_moe_prefill with a choice of which weight matrices are rounded to
- * bf16 (bit 0 gate, bit 1 up, bit 2 down; fo_moe_prefill = all three). */
+ * bf16 (bit 0 gate, bit 1 up, bit 2 down; fo_moe_prefill = all three); bit
+ * 3: a Q6_K down projection on the GPU's fp16 operands; bit 4 (value 16): the choice
+ * made per expert from its own types, as the GPU prefill makes it. */
 void fo_moe_prefill_w(const fo_moe_desc *L, const uint16_t *x, int t0, int nt, float *out, int flags,
                       int *ids_out, float *w_out, int bf16_mask);
 

@@ -809,6 +809,7 @@ def _prefill_host_layer(shape, layer, seed, zipf, gvec=None, experts_needed=None
     d = moe_desc(E, k, H, F, router, experts, shape.gate_size, shape.down_size,
                  shared_off=E * shape.stride if shape.shared else None, bias=bias, gvec=gvec)
     d.gate_type, d.up_type, d.down_type = shape.gate_type, shape.gate_type, shape.down_type
+    d.shared_gate_type, d.shared_up_type, d.shared_down_type = d.gate_type, d.up_type, d.down_type
     d.expert_stride = shape.stride
     return d, (router, experts, bias, gvec)
 
@@ -963,6 +964,66 @@ def test_prefill_thin_tiles_f1024(gpu, T):
         assert thick >= 1                 # beside full fp16 tiles
     if T == 68:
         assert T % 64 in range(1, 5)      # the shared expert's last tile is thin, after a full one
+
+
+@pytest.mark.parametrize("down,Fs,sdown", [(O.Q6_K, 512, O.Q6_K), (O.Q6_K, 256, O.Q4_K), (O.Q4_K, 256, O.Q6_K),
+                                           (O.Q6_K, 1024, O.Q6_K)])
+def test_prefill_shared_own_types(gpu, down, Fs, sdown):
+    """Prefill with a shared expert in its own intermediate size and down type
+    (Q4_K gate/up): the shared expert runs as a one-expert pass of its own and
+    the routed pass combines its output as the shared pair. Every token
+    against the oracle with each expert's own operand rounding (bf16_mask
+    16) and against the exact composition; routing equal."""
+    from fomoe_amd import synthetic as S
+    from test_oracle import moe_desc
+    T, E, k, H, F = 70, 16, 4, 512, 256
+    say(f"prefill shared own types down={down} Fs={Fs} sdown={sdown}")
+    gs, ds = O.row_bytes(O.Q4_K, H) * F, O.row_bytes(down, F) * H
+    stride = (2 * gs + ds + 255) // 256 * 256
+    experts = np.zeros(E * stride, np.uint8)
+    for e in range(E):
+        c = np.concatenate([O.synth_quant(O.Q4_K, 90, 3 * e, 0.02, F, H), O.synth_quant(O.Q4_K, 90, 3 * e + 1, 0.02, F, H),
+                            O.synth_quant(down, 90, 3 * e + 2, 0.02, H, F)])
+        experts[e * stride:e * stride + c.size] = c
+    sh = [O.synth_quant(O.Q4_K, 91, 0, 0.02, Fs, H), O.synth_quant(O.Q4_K, 91, 1, 0.02, Fs, H),
+          O.synth_quant(sdown, 91, 2, 0.02, H, Fs)]
+    sblob = np.concatenate(sh)
+    router = O.synth_f32(92, 0, 0.02, E * H)
+    bias = O.zipf_bias(92, 1, E, 1.1)
+    gvec = O.synth_f32(92, 2, 0.05, H)
+    x = O.to_bf16(O.synth_f32(93, 0, 1.0, T * H)).reshape(T, H)
+    bufs = [gpu.upload(a) for a in (router, experts, sblob, bias, gvec)]
+    L = FA.MoeLayer()
+    L.n_embd, L.inter, L.n_experts, L.k = H, F, E, k
+    L.gate_type, L.up_type, L.down_type = O.Q4_K, O.Q4_K, down
+    L.gate_size, L.up_size, L.expert_stride = gs, gs, stride
+    L.router, L.router_bias, L.experts, L.shared = bufs[0].ptr, bufs[3].ptr, bufs[1].ptr, bufs[2].ptr
+    L.shared_inter, L.shared_gate_size, L.shared_up_size = Fs, sh[0].size, sh[1].size
+    L.shared_gate_type, L.shared_up_type, L.shared_down_type = O.Q4_K, O.Q4_K, sdown
+    L.shared_gate_vec, L.norm_w, L.eps = bufs[4].ptr, None, 1e-6
+    dx, dout = gpu.upload(x), gpu.alloc(4 * T * H)
+    gpu.moe_prefill(L, dx, T, dout, FA.MOE_RESIDUAL)
+    got = gpu.download(dout, np.float32, T * H).reshape(T, H)
+    ids, w = gpu.prefill_routing(T, k)
+    table = np.concatenate([experts, sblob])
+    d = moe_desc(E, k, H, F, router, table, gs, ds, shared_off=E * stride, bias=bias, gvec=gvec)
+    d.expert_stride = stride
+    d.down_type = down
+    d.shared_inter, d.shared_gate_size, d.shared_up_size = Fs, sh[0].size, sh[1].size
+    d.shared_gate_type, d.shared_up_type, d.shared_down_type = O.Q4_K, O.Q4_K, sdown
+    want, oids, ow = O.moe_prefill(d, x, 0, T, O.MOE_RESIDUAL, bf16_mask=16)
+    exact, _, _ = O.moe_prefill(d, x, 0, T, O.MOE_RESIDUAL, bf16_mask=0)
+    assert np.array_equal(ids, oids)
+    assert inf_rel(w, ow) < 1e-5
+    e1 = max(inf_rel(got[t] - O.bf16_to_f32(x[t]), want[t] - O.bf16_to_f32(x[t])) for t in range(T))
+    e2 = max(inf_rel(got[t] - O.bf16_to_f32(x[t]), exact[t] - O.bf16_to_f32(x[t])) for t in range(T))
+    say(f"  worst token inf_rel (ffn) vs same rounding {e1:.3e}, vs exact {e2:.3e}")
+    # a Q4_K down projection runs on bf16 weights (2^-9 relative), which the
+    # exact composition does not share; a Q6_K one on fp16 operands. Measured
+    # worst: 3.3e-5 same rounding, 2.2e-3 exact (bf16 down), 5.8e-4 (fp16 down)
+    bf16_down = O.Q4_K in (down, sdown)
+    assert e1 <= 1e-4
+    assert e2 <= (4.5e-3 if bf16_down else PF16_EXACT)
 
 
 @pytest.mark.parametrize("F", [256, 1024])
