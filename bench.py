@@ -22,6 +22,7 @@ usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--stack-layers 60]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -279,7 +280,7 @@ def cpu_layer_baseline(gpu, layers, shape, seconds, n_sample=4):
                               f"{len(sample)} sampled layers (reference cpu_expert engine)"}
 
 
-def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0, cpu_seconds=0.0):
+def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0, cpu_seconds=0.0, probes=False):
     shape = S.LayerShape()
     t0 = time.perf_counter()
     layers = []
@@ -303,6 +304,9 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
         gpu.moe_layer(layers[i % n_layers].desc, h, out, 0)
     us_layer_call = gpu.timer_stop() * 1e3 / layer_calls
     shexp = shared_own_type_legs(gpu, layers, shape, h, out, min(n_layers, 30), layer_calls)
+    if probes:
+        shexp.update(floor_probes(gpu, layers[:min(n_layers, 30)], shape, h, out))
+        log(f"floor probes: {shexp['floor_probes']}")
     it = iter(range(10 ** 9))
     sp3 = spread_of(gpu, lambda: gpu.moe_layer(layers[next(it) % n_layers].desc, h, out, 0),
                     max(layer_calls, 100), 1e3, "config3_us_per_call_")
@@ -340,6 +344,33 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
         "weights_generation_s": round(gen_s, 1),
         "layer_algorithmic_bytes": layer_bytes,
     }
+
+
+def floor_probes(gpu, layers, shape, h, out, iters=20):
+    """Load-only twins of k_route / k_expand_q4t / k_reduce_tile
+    (fomoe_amd/csrc/floor_probe.hip, a diagnostic library of its own) over the
+    same rotation of layers, each layer with the routing its real call chose:
+    the floor the three-kernel structure sets without arithmetic, beside the
+    real kernels' per-launch times (HIP events, launches back to back)."""
+    path = os.path.join(ROOT, "fomoe_amd", "libfomoe_probe_gfx950.so")
+    lib = ctypes.CDLL(path)
+    f = lib.fo_probe_layer_floors
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    ids = []
+    for L in layers:
+        gpu.moe_layer(L.desc, h, out, 0)
+        ids.append(gpu.last_routing(shape.k)[0])
+    d_ids = gpu.upload(np.concatenate(ids).astype(np.int32))
+    arr = (FA.MoeLayer * len(layers))(*[L.desc for L in layers])
+    us = np.zeros(5, np.float32)
+    rc = f(ctypes.addressof(arr), len(layers), d_ids.ptr, iters, us.ctypes.data)
+    if rc != 0:
+        raise RuntimeError(f"fo_probe_layer_floors returned {rc}")
+    names = ["empty_kernel_us", "route_loads_us", "expand_loads_us", "reduce_loads_us", "three_probes_us_per_layer"]
+    res = {n: round(float(v), 2) for n, v in zip(names, us)}
+    res["layers"], res["iters"] = len(layers), iters
+    return {"floor_probes": res}
 
 
 def shared_own_type_legs(gpu, layers, shape, h, out, n, calls):
@@ -411,6 +442,8 @@ def main():
     ap.add_argument("--layer-calls", type=int, default=600)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--floor-probes", action="store_true",
+                    help="also time load-only twins of the layer kernels (libfomoe_probe_gfx950.so)")
     ap.add_argument("--skip", default="", help="comma list: q4k,q8_0,q5k,stack,cpu,prefill")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -469,7 +502,7 @@ def main():
     if "stack" not in skip and args.stack_layers > 0:
         extra.update(moe_layer_and_stack(gpu, args.stack_layers, args.stack_steps, args.layer_calls,
                                          0 if "prefill" in skip else args.prefill_reps,
-                                         0.0 if "cpu" in skip else args.cpu_seconds / 2))
+                                         0.0 if "cpu" in skip else args.cpu_seconds / 2, args.floor_probes))
         log(f"stack: {extra['config4_tok_per_s']} tok/s, {extra['config4_us_per_layer']} us/layer")
         if "config5_ms" in extra:
             log(f"prefill: {extra['config5_ms']} ms per 512 tokens, {extra['config5_TFLOP/s']} TFLOP/s, "
