@@ -673,16 +673,16 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     if (int rc = check_layer(ctx, L)) return rc;
     if (!d_x || !d_out || n_tokens <= 0) return fail(ctx, -1, "moe prefill: null buffer or n_tokens %d", n_tokens);
     if (flags & ~GPU_MOE_RESIDUAL) return fail(ctx, -1, "moe prefill: flags %d (only GPU_MOE_RESIDUAL)", flags);
-    const bool pt = (L->gate_type == GGML_TYPE_Q4_K || L->gate_type == GGML_TYPE_Q6_K) &&
-                    (L->down_type == GGML_TYPE_Q4_K || L->down_type == GGML_TYPE_Q6_K);
-    if (!pt) return fail(ctx, -1, "moe prefill: gate/up/down types must be Q4_K or Q6_K");
+    if (!fo::prefill_types_ok(L->gate_type, L->up_type, L->down_type))
+        return fail(ctx, -1, "moe prefill: types gate %d up %d down %d (gate/up Q4_K/Q6_K, or both Q5_K or "
+                             "both Q8_0; down Q4_K, Q5_K, Q6_K or Q8_0)", L->gate_type, L->up_type, L->down_type);
     // a shared expert in other types or F_s runs as a one-expert pass of its
     // own (every token routed to it), whose output the routed pass combines
     const bool own = L->shared && (L->shared_inter != L->inter || L->shared_gate_type != L->gate_type ||
                                    L->shared_up_type != L->up_type || L->shared_down_type != L->down_type);
-    auto pf_type = [](int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K; };
-    if (own && !(pf_type(L->shared_gate_type) && pf_type(L->shared_up_type) && pf_type(L->shared_down_type)))
-        return fail(ctx, -1, "moe prefill: shared-expert types must be Q4_K or Q6_K");
+    if (own && !fo::prefill_types_ok(L->shared_gate_type, L->shared_up_type, L->shared_down_type))
+        return fail(ctx, -1, "moe prefill: shared-expert types gate %d up %d down %d", L->shared_gate_type,
+                    L->shared_up_type, L->shared_down_type);
     const int T = n_tokens, E = L->n_experts, k = L->k, H = L->n_embd, F = L->inter;
     if (E > 1023) return fail(ctx, -1, "moe prefill: n_experts %d > 1023", E);
     if (L->gate_type == GGML_TYPE_Q4_K) {   // its gate/up rows move by direct 16-byte global->LDS loads

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "quant_types.h"
+
 namespace fo {
 
 constexpr int kPfMT = 64;        // tokens per GEMM tile (4 MFMA row blocks of 16)
@@ -53,6 +55,15 @@ struct PrefillArgs {
 };
 
 // Number of pair slots and an upper bound on the GEMM tiles for T tokens.
+// Weight types the prefill runs: gate/up both Q4_K (exact fp16 operands), a
+// Q4_K/Q6_K mix, or both Q5_K or both Q8_0 (bf16 operands); down Q4_K, Q5_K,
+// Q6_K or Q8_0.
+inline bool prefill_types_ok(int gate, int up, int down) {
+    auto k46 = [](int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K; };
+    const bool gu = (k46(gate) && k46(up)) || (gate == up && (gate == GGML_TYPE_Q5_K || gate == GGML_TYPE_Q8_0));
+    const bool dn = k46(down) || down == GGML_TYPE_Q5_K || down == GGML_TYPE_Q8_0;
+    return gu && dn;
+}
 inline int prefill_pairs(int T, int k, bool shared) { return T * (k + (shared ? 1 : 0)); }
 inline int prefill_max_tiles(int T, int k, int E, bool shared) {
     return (prefill_pairs(T, k, shared) + kPfMT - 1) / kPfMT + E + (shared ? 1 : 0);

@@ -475,6 +475,70 @@ template <> struct PfDec<GGML_TYPE_Q6_K> {
     }
 };
 
+// Q5_K (reference src/quant.c:216-247): Q4_K's header and nibbles plus a
+// fifth bit per value, bit j of qh[l] for value l of sub-block j.
+template <> struct PfDec<GGML_TYPE_Q5_K> {
+    static constexpr int TYPE = GGML_TYPE_Q5_K, BLOCK = 176;
+    struct Sb { uint4 hdr; uint2 qh; uint2 q[4]; };
+    static FO_DEV Sb load(const uint8_t *sb, int kg) {
+        Sb s;
+        s.hdr = ld16(sb);
+        s.qh = ld8(sb + 16 + 8 * kg);
+#pragma unroll
+        for (int c = 0; c < 4; c++) s.q[c] = ld8(sb + 48 + 32 * c + 8 * kg);
+        return s;
+    }
+    // chunk ch = sub-block ch, values 8kg..8kg+7 of it
+    static FO_DEV u32x4 decode(const Sb &s, int ch, int) {
+        const uint32_t sc4[3] = {s.hdr.y, s.hdr.z, s.hdr.w};
+        const int j = ch;
+        auto byte = [&](int i) -> uint32_t { return (sc4[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
+        uint32_t sc, mn;
+        if (j < 4) { sc = byte(j) & 63; mn = byte(j + 4) & 63; }
+        else {
+            sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
+            mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+        }
+        const float d1 = h2f(s.hdr.x) * (float)sc, m1 = h2f(s.hdr.x >> 16) * (float)mn;
+        const uint2 q = s.q[ch >> 1];
+        const int sh = 4 * (ch & 1);
+        const uint32_t w0 = ((q.x >> sh) & 0x0F0F0F0Fu) | (((s.qh.x >> ch) & 0x01010101u) << 4);
+        const uint32_t w1 = ((q.y >> sh) & 0x0F0F0F0Fu) | (((s.qh.y >> ch) & 0x01010101u) << 4);
+        u32x4 r;
+        r[0] = pack_bf16(fmaf(d1, ub0(w0), -m1), fmaf(d1, ub1(w0), -m1));
+        r[1] = pack_bf16(fmaf(d1, ub2(w0), -m1), fmaf(d1, ub3(w0), -m1));
+        r[2] = pack_bf16(fmaf(d1, ub0(w1), -m1), fmaf(d1, ub1(w1), -m1));
+        r[3] = pack_bf16(fmaf(d1, ub2(w1), -m1), fmaf(d1, ub3(w1), -m1));
+        return r;
+    }
+};
+
+// Q8_0 (reference src/quant.c:266-274) in groups of eight 34-byte blocks
+// (256 values, the unit the grouped GEMMs step by): chunk ch = block ch.
+template <> struct PfDec<GGML_TYPE_Q8_0> {
+    static constexpr int TYPE = GGML_TYPE_Q8_0, BLOCK = 8 * 34;
+    struct Sb { uint32_t d[4]; uint2 q[8]; };   // d: the blocks' fp16 scales, two per word
+    static FO_DEV Sb load(const uint8_t *sb, int kg) {
+        Sb s;
+#pragma unroll
+        for (int c = 0; c < 4; c++) s.d[c] = ld2(sb + 68 * c) | (ld2(sb + 68 * c + 34) << 16);
+#pragma unroll
+        for (int c = 0; c < 8; c++) s.q[c] = ld8(sb + 34 * c + 2 + 8 * kg);
+        return s;
+    }
+    static FO_DEV u32x4 decode(const Sb &s, int ch, int) {
+        const float d = h2f(s.d[ch >> 1] >> (16 * (ch & 1)));
+        const uint2 q = s.q[ch];
+        auto v = [&](uint32_t w, int i) { return d * (float)(int8_t)((w >> (8 * i)) & 0xFFu); };
+        u32x4 r;
+        r[0] = pack_bf16(v(q.x, 0), v(q.x, 1));
+        r[1] = pack_bf16(v(q.x, 2), v(q.x, 3));
+        r[2] = pack_bf16(v(q.y, 0), v(q.y, 1));
+        r[3] = pack_bf16(v(q.y, 2), v(q.y, 3));
+        return r;
+    }
+};
+
 template <int T>
 FO_DEV u32x4 pf_decode(const typename PfDec<T>::Sb &s, int ch, int kg) {
     if constexpr (T == GGML_TYPE_Q4_K) return PfDec<T>::decode(s, ch);
@@ -1406,9 +1470,7 @@ static hipError_t launch_gateup_t(const PrefillArgs &a, hipStream_t s) {
 
 hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
     PrefillArgs a = a_;
-    const bool okt = (a.gate_type == GGML_TYPE_Q4_K || a.gate_type == GGML_TYPE_Q6_K) &&
-                     (a.up_type == GGML_TYPE_Q4_K || a.up_type == GGML_TYPE_Q6_K) &&
-                     (a.down_type == GGML_TYPE_Q4_K || a.down_type == GGML_TYPE_Q6_K);
+    const bool okt = prefill_types_ok(a.gate_type, a.up_type, a.down_type);
     const int W = (a.T + 31) / 32;
     if (!okt || a.T <= 0 || a.E <= 0 || a.E > 1023 || a.k <= 0 || a.k > a.E || a.k > kMaxK ||
         a.H <= 0 || a.H % 256 || a.H % (32 * kPfDownWaves) || a.H % (32 * kPfD16Waves) || a.F <= 0 || a.F % 256 || a.F % kPfGateRows || a.E * W > kPfGroupLds ||
@@ -1469,6 +1531,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
 #define FO_GU(G, U) if (a.gate_type == G && a.up_type == U) err = launch_gateup_t<G, U>(a, s);
     FO_GU(GGML_TYPE_Q4_K, GGML_TYPE_Q6_K)
     FO_GU(GGML_TYPE_Q6_K, GGML_TYPE_Q4_K) FO_GU(GGML_TYPE_Q6_K, GGML_TYPE_Q6_K)
+    FO_GU(GGML_TYPE_Q5_K, GGML_TYPE_Q5_K) FO_GU(GGML_TYPE_Q8_0, GGML_TYPE_Q8_0)
 #undef FO_GU
     if (err != hipSuccess) return err;
     {
@@ -1476,12 +1539,12 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         const unsigned grid = pf_grid(a.H / (32 * kPfDownWaves), a.max_tiles);
         static bool down_attr = false;
         if (!down_attr) {
-            hipError_t e1 = hipFuncSetAttribute((const void *)k_pf_down<GGML_TYPE_Q4_K>,
-                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            hipError_t e2 = hipFuncSetAttribute((const void *)k_pf_down<GGML_TYPE_Q6_K>,
-                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e1 != hipSuccess) return e1;
-            if (e2 != hipSuccess) return e2;
+            const void *fns[4] = {(const void *)k_pf_down<GGML_TYPE_Q4_K>, (const void *)k_pf_down<GGML_TYPE_Q5_K>,
+                                  (const void *)k_pf_down<GGML_TYPE_Q6_K>, (const void *)k_pf_down<GGML_TYPE_Q8_0>};
+            for (const void *f : fns) {
+                const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return e;
+            }
             down_attr = true;
         }
         if (a.down_type == GGML_TYPE_Q6_K && a.F <= 4096) {   // fp16 operands, one activation plane
@@ -1501,6 +1564,8 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             k_pf_down16<<<(kPfD16PerCU * n_cu + 7) & ~7, kPfD16Waves * 64, lds16, s>>>(a);   // persistent
             if (a.thin_down) k_pf_down_thin<<<8 * n_cu, 64, kPfThinLds, s>>>(a);
         } else if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
+        else if (a.down_type == GGML_TYPE_Q5_K) k_pf_down<GGML_TYPE_Q5_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
+        else if (a.down_type == GGML_TYPE_Q8_0) k_pf_down<GGML_TYPE_Q8_0><<<grid, kPfDownWaves * 64, lds, s>>>(a);
         else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
     }
     k_pf_combine<<<dim3(a.T, (a.H + kCombCols - 1) / kCombCols), 256, 0, s>>>(a);

@@ -295,8 +295,9 @@ void gpu_gguf_free_moe_layer(gpu_ctx_t *ctx, gpu_moe_layer_t *L);
  * as fp16(q - 32) * fp16(d * sc) against the SwiGLU activation as fp16 under
  * a per-pair power of two (within ~6e-4 of the exact layer per token); other
  * types dequantized to bf16 (round to nearest even), with the activation as
- * two bf16 terms (hi + lo, within 2^-18). gate/up/down types Q4_K or Q6_K;
- * shared expert types Q4_K or Q6_K too: with the routed types and
+ * two bf16 terms (hi + lo, within 2^-18). Types: gate/up Q4_K or Q6_K (any
+ * mix), or both Q5_K or both Q8_0; down Q4_K, Q5_K, Q6_K or Q8_0; the same
+ * sets for the shared expert: with the routed types and
  * intermediate size it is one more pair per token in the routed pass, in
  * types or an intermediate size of its own it runs first as a one-expert
  * pass whose output the routed pass adds at the shared weight;

@@ -966,8 +966,34 @@ def test_prefill_thin_tiles_f1024(gpu, T):
         assert T % 64 in range(1, 5)      # the shared expert's last tile is thin, after a full one
 
 
+@pytest.mark.parametrize("gate,down", [(O.Q4_K, O.Q5_K), (O.Q4_K, O.Q8_0), (O.Q5_K, O.Q5_K), (O.Q8_0, O.Q8_0),
+                                       (O.Q5_K, O.Q6_K)])
+def test_prefill_other_types(gpu, gate, down):
+    """Prefill with Q5_K / Q8_0 weights (the real model's down projections are
+    partly Q5_K): gate/up both of one type, bf16 operands; every token against
+    the oracle's composition with bf16-rounded weights, routing equal."""
+    from fomoe_amd import synthetic as S
+    T = 70
+    say(f"prefill types gate/up={gate} down={down} T={T}")
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=16, k=4, shared=True, gate_type=gate, down_type=down)
+    L = S.build_layer(gpu, shape, 0, seed=21, zipf_s=1.1, norm=False)
+    gv = O.synth_f32(22, 0, 0.05, shape.n_embd)
+    dgv = gpu.upload(gv)
+    L.desc.shared_gate_vec = dgv.ptr
+    dx = S.tokens_bf16(gpu, T, shape.n_embd, seed=23)
+    dout = gpu.alloc(4 * T * shape.n_embd)
+    gpu.moe_prefill(L.desc, dx, T, dout, 0)
+    got = gpu.download(dout, np.float32, T * shape.n_embd).reshape(T, shape.n_embd)
+    ids, w = gpu.prefill_routing(T, shape.k)
+    x = O.to_bf16(O.synth_f32(23, S.stream(0, 0, S.TOKENS), 1.0, T * shape.n_embd)).reshape(T, -1)
+    d, keep = _prefill_host_layer(shape, 0, 21, True, gv)
+    want, oids, ow = pf_check(got, d, x, 0, shape)
+    assert np.array_equal(ids, oids)
+    assert inf_rel(w, ow) < 1e-5
+
+
 @pytest.mark.parametrize("down,Fs,sdown", [(O.Q6_K, 512, O.Q6_K), (O.Q6_K, 256, O.Q4_K), (O.Q4_K, 256, O.Q6_K),
-                                           (O.Q6_K, 1024, O.Q6_K)])
+                                           (O.Q6_K, 1024, O.Q6_K), (O.Q6_K, 512, O.Q5_K), (O.Q6_K, 256, O.Q8_0)])
 def test_prefill_shared_own_types(gpu, down, Fs, sdown):
     """Prefill with a shared expert in its own intermediate size and down type
     (Q4_K gate/up): the shared expert runs as a one-expert pass of its own and
@@ -1018,10 +1044,11 @@ def test_prefill_shared_own_types(gpu, down, Fs, sdown):
     e1 = max(inf_rel(got[t] - O.bf16_to_f32(x[t]), want[t] - O.bf16_to_f32(x[t])) for t in range(T))
     e2 = max(inf_rel(got[t] - O.bf16_to_f32(x[t]), exact[t] - O.bf16_to_f32(x[t])) for t in range(T))
     say(f"  worst token inf_rel (ffn) vs same rounding {e1:.3e}, vs exact {e2:.3e}")
-    # a Q4_K down projection runs on bf16 weights (2^-9 relative), which the
-    # exact composition does not share; a Q6_K one on fp16 operands. Measured
-    # worst: 3.3e-5 same rounding, 2.2e-3 exact (bf16 down), 5.8e-4 (fp16 down)
-    bf16_down = O.Q4_K in (down, sdown)
+    # a Q4_K/Q5_K/Q8_0 down projection runs on bf16 weights (2^-9 relative),
+    # which the exact composition does not share; a Q6_K one on fp16 operands.
+    # Measured worst: 3.3e-5 same rounding, 2.2e-3 exact (bf16 down), 5.8e-4
+    # (fp16 down)
+    bf16_down = down != O.Q6_K or sdown != O.Q6_K
     assert e1 <= 1e-4
     assert e2 <= (4.5e-3 if bf16_down else PF16_EXACT)
 
