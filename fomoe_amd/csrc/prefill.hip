@@ -1406,7 +1406,9 @@ __global__ __launch_bounds__(64) void k_pf_down_thin(PrefillArgs a) {
 
 // ============================================================ P6 combine
 // One work-group per (token, kCombCols columns); each thread owns float4 columns and requests all
-// of the token's pair rows for a column before summing them in rank order.
+// of the token's pair rows for a column before summing them in rank order. The pair rows are read
+// once: non-temporal loads (20.7 against 21.8 us at config 5; 512 or 2048 columns per work-group
+// 25.7 / 23.0 us).
 constexpr int kCombCols = 1024;   // columns of one token per work-group
 
 __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
@@ -1423,7 +1425,10 @@ __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
         float4 o[kMaxK + 1];
 #pragma unroll
         for (int r = 0; r <= kMaxK; r++)
-            if (r < n) o[r] = *(const float4 *)(a.outp + (uint64_t)s_pp[r] * a.H + 4 * i4);
+            if (r < n) {
+                const uint4 u = ldw16((const uint8_t *)(a.outp + (uint64_t)s_pp[r] * a.H + 4 * i4));
+                o[r] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+            }
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int r = 0; r < kMaxK; r++)
