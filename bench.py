@@ -411,7 +411,11 @@ def prefill_config5(gpu, layer, shape, reps):
     T, H, F, E, k = 512, shape.n_embd, shape.inter, shape.n_experts, shape.k
     x = S.tokens_bf16(gpu, T, H, seed=4)
     out = gpu.alloc(4 * T * H)
-    for _ in range(2):
+    # warmup as for the rotation legs: ~15 ms of back-to-back calls, so that
+    # the timed loop does not run on clocks still rising after the idle gap
+    # before this leg (with 2 warmup calls its mean was 5-11 % above the
+    # median of the individually timed calls that follow it)
+    for _ in range(20):
         gpu.moe_prefill(layer.desc, x, T, out, 0)
     gpu.sync()
     gpu.timer_start()
@@ -441,7 +445,7 @@ def main():
     ap.add_argument("--stack-steps", type=int, default=256)
     ap.add_argument("--layer-calls", type=int, default=600)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--floor-probes", action="store_true",
                     help="also time load-only twins of the layer kernels (libfomoe_probe_gfx950.so)")
     ap.add_argument("--skip", default="", help="comma list: q4k,q8_0,q5k,stack,cpu,prefill")
