@@ -1311,39 +1311,47 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
 // applied to the result. The code building is shared by the tile's pairs, so
 // a weight costs ~0.75 + 0.5 n VALU instructions per code against ~3.4 for
 // the fp16 operand decode of k_pf_down16, whose 16-token MFMA blocks a thin
-// tile leaves mostly empty. Work unit = (thin tile, kPfThinTPW * 16 rows),
-// one wave per work-group, units dealt round-robin; F == 1024.
-constexpr int kPfThinTPW = 8;
+// tile leaves mostly empty. Work unit = (thin tile, kPfThinWaves *
+// kPfThinTPW * 16 rows): the work-group's waves prepare one pair's
+// activation each into LDS shared by all of them (one copy per work-group,
+// so that 8 waves per CU fit in LDS: with a copy per one-wave work-group
+// only 5 did: 121.5 -> 109.3 us at config 5), then each wave streams its
+// kPfThinTPW tiles; units dealt round-robin; F == 1024. (4 waves x 4 tiles,
+// 8 x 4, 8 x 2, 2 x 8: 115 / 119 / 127 / 122 us; the results held in LDS
+// and stored once per unit: no change.)
+constexpr int kPfThinTPW = 8, kPfThinWaves = 4;
 constexpr int kPfThinF = 1024;                                     // the one F this kernel is built for
 constexpr uint32_t kPfThinRow = kPfThinF / 256 * 210;              // Q6_K row: 840 bytes
 constexpr uint32_t kPfThinX = 3 * kPfThinF + kPfThinF / 16 * 8;    // one pair's prepared activation
 constexpr uint32_t kPfThinZero = 304;                              // zero A operands (as kT6Zero)
 constexpr uint32_t kPfThinTile = 16 * kPfThinRow;                  // 13,440 bytes
+constexpr int kPfThinUnitRows = 16 * kPfThinTPW * kPfThinWaves;    // 512 rows
 // 64 lanes x 16 activation values = one F = 1024 row per pair (lane = 16-value group)
 static_assert(kPfThinF == 64 * 16 && kPfThinRow == 840, "k_pf_down_thin's lane layout covers F = 1024 only");
+static_assert(kPfThin <= kPfThinWaves, "one wave prepares each pair's activation");
 
 // Whether the Q6_K down projection's thin tiles take k_pf_down_thin (the one
 // place that decides; k_pf_group orders thin tiles last whatever it says).
 __host__ inline bool pf_thin_down(const PrefillArgs &a) {
-    return a.down_type == GGML_TYPE_Q6_K && a.F == kPfThinF && a.H % (16 * kPfThinTPW) == 0;
+    return a.down_type == GGML_TYPE_Q6_K && a.F == kPfThinF && a.H % kPfThinUnitRows == 0;
 }
-constexpr uint32_t kPfThinLds = kPfThin * kPfThinX + kPfThinZero + kPfThinTile;
+constexpr uint32_t kPfThinLds = kPfThin * kPfThinX + kPfThinZero + kPfThinWaves * kPfThinTile;   // 68.3 KiB
 
-__global__ __launch_bounds__(64) void k_pf_down_thin(PrefillArgs a) {
+__global__ __launch_bounds__(64 * kPfThinWaves) void k_pf_down_thin(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
     constexpr int NV = (kPfThinTile + 1023) / 1024;
     constexpr uint32_t rb = kPfThinRow, limb_bytes = 3 * kPfThinF;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     uint8_t *zero = sx + kPfThin * kPfThinX;
-    uint8_t *tb = zero + kPfThinZero;
+    uint8_t *tb = zero + kPfThinZero + wv * kPfThinTile;
     const int n_thick = a.n_tiles[1], n_thin = a.n_tiles[0] - n_thick;
-    const int upt = a.H / (16 * kPfThinTPW), nunits = n_thin * upt;
-    if (lane < kPfThinZero / 16) *(uint4 *)(zero + 16 * lane) = make_uint4(0, 0, 0, 0);
+    const int upt = a.H / kPfThinUnitRows, nunits = n_thin * upt;
+    if ((int)threadIdx.x < kPfThinZero / 16) *(uint4 *)(zero + 16 * threadIdx.x) = make_uint4(0, 0, 0, 0);
     const int r = lane & 15, g = lane >> 4, n = g >> 1, j = g & 1, L = r & 3;
     const bool valid = (r >> 2) == g && L < 3;
     const uint32_t aoff = (8 * n + j) * 48 + 16 * L, soff = limb_bytes + (8 * n + j) * 8;
     for (int u = blockIdx.x; u < nunits; u += gridDim.x) {
-        const int ti = n_thick + u / upt, row0 = (u % upt) * 16 * kPfThinTPW;
+        const int ti = n_thick + u / upt, row0 = (u % upt) * kPfThinUnitRows + wv * 16 * kPfThinTPW;
         const int tile = a.tiles[4 * ti + 3];
         const int4 t4 = *(const int4 *)(a.tiles + 4 * tile);
         const bool shared = t4.x == a.E;
@@ -1359,8 +1367,8 @@ __global__ __launch_bounds__(64) void k_pf_down_thin(PrefillArgs a) {
         };
         issue(0);
         __syncthreads();                                 // the previous unit's LDS reads are done
-        for (int m = 0; m < np; m++) {                   // lane = 16-value group of pair m
-            const uint16_t *src = a.act_hi + (uint64_t)(p0 + m) * a.F + 16 * lane;
+        if (wv < np) {                                   // wave m prepares pair m (lane = 16-value group)
+            const uint16_t *src = a.act_hi + (uint64_t)(p0 + wv) * a.F + 16 * lane;
             const uint4 h0 = *(const uint4 *)src, h1 = *(const uint4 *)(src + 8);
             const uint32_t w[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
             float vals[16];
@@ -1372,7 +1380,7 @@ __global__ __launch_bounds__(64) void k_pf_down_thin(PrefillArgs a) {
             int limb[kLimbs][4];
             float scale, sum;
             prep_group_vals<16>(vals, limb, scale, sum);
-            uint8_t *xm = sx + m * kPfThinX;
+            uint8_t *xm = sx + wv * kPfThinX;
 #pragma unroll
             for (int Lq = 0; Lq < kLimbs; Lq++)
                 *(uint4 *)(xm + lane * 48 + 16 * Lq) = make_uint4(limb[Lq][0], limb[Lq][1], limb[Lq][2], limb[Lq][3]);
@@ -1388,17 +1396,15 @@ __global__ __launch_bounds__(64) void k_pf_down_thin(PrefillArgs a) {
             for (int b = 0; b < 4; b++) q6k_slot_load(qs[b], tb + r * rb + b * 210, n, j);
 #pragma unroll 1
             for (int m = 0; m < np; m++) {
-                {
-                    const uint8_t *xm = sx + m * kPfThinX;
-                    float acc = 0.f;
+                const uint8_t *xm = sx + m * kPfThinX;
+                float acc = 0.f;
 #pragma unroll
-                    for (int b = 0; b < 4; b++)
-                        acc += q6k_sb_dot_mfma(qs[b], valid ? xm + aoff + 768 * b : zero, xm + soff + 128 * b, j);
-                    acc += __shfl_xor(acc, 16);
-                    acc += __shfl_xor(acc, 32);
-                    if (g == 0)
-                        a.outp[(uint64_t)(p0 + m) * a.H + row0 + 16 * tt + r] = ldexpf(acc, a.pexp[p0 + m]);
-                }
+                for (int b = 0; b < 4; b++)
+                    acc += q6k_sb_dot_mfma(qs[b], valid ? xm + aoff + 768 * b : zero, xm + soff + 128 * b, j);
+                acc += __shfl_xor(acc, 16);
+                acc += __shfl_xor(acc, 32);
+                if (g == 0)
+                    a.outp[(uint64_t)(p0 + m) * a.H + row0 + 16 * tt + r] = ldexpf(acc, a.pexp[p0 + m]);
             }
         }
     }
@@ -1559,6 +1565,9 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
                 hipError_t e = hipFuncSetAttribute((const void *)k_pf_down16,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds16);
                 if (e != hipSuccess) return e;
+                e = hipFuncSetAttribute((const void *)k_pf_down_thin, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)kPfThinLds);
+                if (e != hipSuccess) return e;
                 d16_attr = true;
             }
             const int np = prefill_pairs(a.T, a.k, a.shared != nullptr);
@@ -1567,7 +1576,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             int dev = 0, n_cu = 256;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
             k_pf_down16<<<(kPfD16PerCU * n_cu + 7) & ~7, kPfD16Waves * 64, lds16, s>>>(a);   // persistent
-            if (a.thin_down) k_pf_down_thin<<<8 * n_cu, 64, kPfThinLds, s>>>(a);
+            if (a.thin_down) k_pf_down_thin<<<2 * n_cu, 64 * kPfThinWaves, kPfThinLds, s>>>(a);
         } else if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
         else if (a.down_type == GGML_TYPE_Q5_K) k_pf_down<GGML_TYPE_Q5_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
         else if (a.down_type == GGML_TYPE_Q8_0) k_pf_down<GGML_TYPE_Q8_0><<<grid, kPfDownWaves * 64, lds, s>>>(a);
