@@ -707,8 +707,8 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     HIPC(ensure(ctx->pf_w, ctx->pf_w_cap, sizeof(float) * (size_t)T * (k + 1)));
     HIPC(ensure(ctx->pf_pairpos, ctx->pf_pairpos_cap, sizeof(int32_t) * (size_t)Tc * (k + 1)));
     HIPC(ensure(ctx->pf_pairtok, ctx->pf_pairtok_cap, sizeof(int32_t) * P));
-    HIPC(ensure(ctx->pf_tiles, ctx->pf_tiles_cap,
-                sizeof(int32_t) * 4 * (size_t)std::max(max_tiles, fo::prefill_max_tiles(Tc, 1, 1, false))));
+    const size_t tcap = (size_t)std::max(max_tiles, fo::prefill_max_tiles(Tc, 1, 1, false));
+    HIPC(ensure(ctx->pf_tiles, ctx->pf_tiles_cap, sizeof(int32_t) * 8 * tcap));   // tiles, then double tiles
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
     const size_t Pact = std::max(P * F, (size_t)Tc * Fs);   // activation elements of either pass
     HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * Pact));
@@ -738,6 +738,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.residual = (flags & GPU_MOE_RESIDUAL) ? 1 : 0;
     a.logits = ctx->pf_logits; a.pairpos = ctx->pf_pairpos;
     a.pair_tok = ctx->pf_pairtok; a.tiles = ctx->pf_tiles; a.n_tiles = ctx->pf_ntiles;
+    a.dtiles = ctx->pf_tiles + 4 * tcap;
     a.act_hi = ctx->pf_act; a.act_lo = ctx->pf_act + Pact; a.outp = ctx->pf_outp;
     a.xsum = ctx->pf_xsum;
     a.x16 = (uint16_t *)((uint8_t *)ctx->pf_xsum + xs_bytes);

@@ -40,8 +40,10 @@ struct PrefillArgs {
     float *w;                    // [T x (k+1)]: renormalised weights, then the shared weight
     int32_t *pairpos;            // [T x (k+1)]: pair slot of (token, rank); rank k = shared
     int32_t *pair_tok;           // [P] token of each pair slot, grouped by expert
-    int32_t *tiles;              // [max_tiles x 4] {expert (E = shared), first pair, n, 0}
-    int32_t *n_tiles;            // [3]: tiles, tiles before the thin ones, work counter of the gate/up kernel
+    int32_t *tiles;              // [max_tiles x 4] {expert (E = shared), first pair, n, order}
+    int32_t *dtiles;             // [max_tiles x 4] the same in tiles of up to 2 kPfMT pairs (k_pf_down16)
+    int32_t *n_tiles;            // [5]: tiles, tiles before the thin ones, work counter of the gate/up
+                                 // kernel, double tiles, double tiles before those of thin experts
     int max_tiles;
     uint16_t *act_hi, *act_lo;   // [P x F] SwiGLU activation as bf16 hi + lo terms (a Q6_K
                                  // down projection rewrites act_hi as fp16 rows, scale in pexp)

@@ -358,7 +358,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     // down projection runs on its integer path). Per expert: its full tiles
     // (count 4) and its last, partial tile (count cb).
     const int nfull = cnt / kPfMT, rem = cnt - kPfMT * nfull, cb = (rem + 15) >> 4;   // cb = 0: no partial tile
-    const int thin = cb == 1 && rem <= kPfThin;
+    const int thin = cnt > 0 && cnt <= kPfThin;   // an expert of at most kPfThin pairs: its one tile
     const int c4 = nfull + (cb == 4), c3 = cb == 3, c2 = cb == 2, c1 = cb == 1 && !thin;
     const int o43 = block_exclusive_scan(c4 | (c3 << 16), scan_buf);
     const int o21 = block_exclusive_scan(c2 | (c1 << 16), scan_buf);
@@ -380,6 +380,49 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     }
     // [0]: tiles, [1]: tiles before the thin ones, [2]: k_pf_gateup_f16 work counter
     if (tid == 1023) { a.n_tiles[0] = toff + nt; a.n_tiles[1] = toff + nt - s_tot[2]; a.n_tiles[2] = 0; }
+    // Double tiles for k_pf_down16: per expert ceil(cnt / 128) tiles of up to
+    // 2 kPfMT pairs (its weights are read and decoded once per 128 pairs), in
+    // decreasing token-block count (8 .. 1), those of thin experts last.
+    {
+        constexpr int DT = 2 * kPfMT;
+        const int dn = (cnt + DT - 1) / DT, dfull = cnt / DT, drem = cnt - DT * dfull, dcb = (drem + 15) >> 4;
+        const int doff = block_exclusive_scan(dn, scan_buf);   // storage index of the expert's first
+        // count per class: c[8] = full double tiles (+ a partial one of 8 blocks), c[1..7] = the partial one
+        auto cls = [&](int b) { return b == 8 ? dfull + (dcb == 8) : (dcb == b && !thin ? 1 : 0); };
+        const int o87 = block_exclusive_scan(cls(8) | (cls(7) << 16), scan_buf);
+        const int o65 = block_exclusive_scan(cls(6) | (cls(5) << 16), scan_buf);
+        const int o43 = block_exclusive_scan(cls(4) | (cls(3) << 16), scan_buf);
+        const int o21 = block_exclusive_scan(cls(2) | (cls(1) << 16), scan_buf);
+        const int oth = block_exclusive_scan(thin, scan_buf);
+        __shared__ int s_dt[5];
+        if (tid == 1023) {
+            s_dt[0] = o87 + (cls(8) | (cls(7) << 16)); s_dt[1] = o65 + (cls(6) | (cls(5) << 16));
+            s_dt[2] = o43 + (cls(4) | (cls(3) << 16)); s_dt[3] = o21 + (cls(2) | (cls(1) << 16));
+            s_dt[4] = oth + thin;
+            a.n_tiles[3] = doff + dn;
+            a.n_tiles[4] = doff + dn - (oth + thin);
+        }
+        __syncthreads();
+        int tot[9], base[9];   // per class count and first rank, classes in order 8, 7, .., 1
+        tot[8] = s_dt[0] & 0xFFFF; tot[7] = s_dt[0] >> 16; tot[6] = s_dt[1] & 0xFFFF; tot[5] = s_dt[1] >> 16;
+        tot[4] = s_dt[2] & 0xFFFF; tot[3] = s_dt[2] >> 16; tot[2] = s_dt[3] & 0xFFFF; tot[1] = s_dt[3] >> 16;
+        base[8] = 0;
+        for (int b = 7; b >= 1; b--) base[b] = base[b + 1] + tot[b + 1];
+        const int thin_base = base[1] + tot[1];
+        const int mine[9] = {0, o21 >> 16, o21 & 0xFFFF, o43 >> 16, o43 & 0xFFFF, o65 >> 16, o65 & 0xFFFF,
+                             o87 >> 16, o87 & 0xFFFF};
+        if (tid <= E) {
+            for (int i = 0; i < dn; i++) {
+                int32_t *tp = a.dtiles + 4 * (doff + i);
+                tp[0] = tid; tp[1] = off + DT * i; tp[2] = min(DT, cnt - DT * i);
+                int rank;
+                if (thin) rank = thin_base + oth;
+                else if (i < dfull) rank = base[8] + mine[8] + i;
+                else rank = dcb == 8 ? base[8] + mine[8] + dfull : base[dcb] + mine[dcb];
+                a.dtiles[4 * rank + 3] = doff + i;
+            }
+        }
+    }
     // pair offsets of each expert for the placement pass
     __shared__ int s_off[1025];
     if (tid <= E) s_off[tid] = off;
@@ -1157,18 +1200,22 @@ __global__ __launch_bounds__(64 * kApWaves) void k_pf_actprep_w(PrefillArgs a, i
 // against 358 µs for two work-groups per CU at 128 VGPRs, whose spill
 // reloads waited for every outstanding load).
 constexpr int kPfD16Waves = 8, kPfD16PerCU = 1;   // waves per work-group (32 rows each), work-groups per CU
+constexpr int kPfD16Tile = 2 * kPfTile;           // activation rows of a double tile (128 pairs) per step
 __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) void k_pf_down16(PrefillArgs a) {
     using D = PfDec<GGML_TYPE_Q6_K>;
-    extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x tile
+    extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x double tile
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), col = lane & 15, kg = lane >> 4;
-    // items (tile, block of 256 rows) of this work-group's XCD (work-group i
+    // items (double tile of up to 128 pairs of one expert, block of 256
+    // rows: the expert's weights are read and decoded once per 128 pairs;
+    // 188 -> 164 us at config 5 against 64-pair tiles) of this work-group's
+    // XCD (work-group i
     // runs on XCD i % 8): the XCD takes row blocks x, x + 8 of every tile, in
     // decreasing tile cost (the order k_pf_group records), so the XCDs get like
     // work and all tiles of one expert read a row block through the same L2
     // (an expert's tiles are neighbours in that order; down16 HBM reads -15 %
     // against every eighth tile per XCD); its work-groups take its items
     // u = i / 8, + G8, ..., the costliest first
-    const int nt = a.n_tiles[a.thin_down ? 1 : 0], nrb = a.H / (32 * kPfD16Waves);   // thin tiles: k_pf_down_thin
+    const int nt = a.n_tiles[a.thin_down ? 4 : 3], nrb = a.H / (32 * kPfD16Waves);   // thin experts: k_pf_down_thin
     const int x = blockIdx.x & 7, G8 = gridDim.x >> 3;
     const int nrbx = (nrb - x + 7) >> 3, n_u = nt * nrbx;     // row blocks x, x + 8, ... of every tile
     const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
@@ -1178,8 +1225,8 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
         Item it;
         const int tl = u / nrbx, rbk = x + 8 * (u - tl * nrbx);
         it.ok = u < n_u;
-        const int tile = a.tiles[4 * (it.ok ? tl : 0) + 3];
-        const int4 t4 = *(const int4 *)(a.tiles + 4 * tile);
+        const int tile = a.dtiles[4 * (it.ok ? tl : 0) + 3];
+        const int4 t4 = *(const int4 *)(a.dtiles + 4 * tile);
         const bool shared = t4.x == a.E;
         const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)t4.x * a.stride;
         const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
@@ -1193,7 +1240,7 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     // makes every LDS read of the current step wait for them); the wait at
     // the top of each step covers them
     auto stage = [&](const Item &it, int kb, int buf_i) {
-        const uint32_t buf = lds_addr(d16s + buf_i * kPfTile);
+        const uint32_t buf = lds_addr(d16s + buf_i * kPfD16Tile);
         const int nb = (it.n + 15) >> 4;
         for (int q = wave; q < nb * 8; q += kPfD16Waves) {
             const int m = 2 * q + (lane >> 5), cs = lane & 31;
@@ -1258,7 +1305,7 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
                 s0_next = D::load(nxt.drow, kg);
                 s1_next = D::load(nxt.drow + 16 * db, kg);
             }
-            const uint16_t *xh = d16s + (gs & 1) * kPfTile;
+            const uint16_t *xh = d16s + (gs & 1) * kPfD16Tile;
 #pragma unroll
             for (int ch = 0; ch < 8; ch++) {
                 const f16x8 b0 = dec(s0, ch), b1 = dec(s1, ch);
@@ -1292,7 +1339,11 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
             case 1: run(std::integral_constant<int, 1>{}, nxt); break;
             case 2: run(std::integral_constant<int, 2>{}, nxt); break;
             case 3: run(std::integral_constant<int, 3>{}, nxt); break;
-            default: run(std::integral_constant<int, 4>{}, nxt); break;
+            case 4: run(std::integral_constant<int, 4>{}, nxt); break;
+            case 5: run(std::integral_constant<int, 5>{}, nxt); break;
+            case 6: run(std::integral_constant<int, 6>{}, nxt); break;
+            case 7: run(std::integral_constant<int, 7>{}, nxt); break;
+            default: run(std::integral_constant<int, 8>{}, nxt); break;
         }
         if (!nxt.ok) break;
         cur = nxt;
@@ -1559,7 +1610,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             down_attr = true;
         }
         if (a.down_type == GGML_TYPE_Q6_K && a.F <= 4096) {   // fp16 operands, one activation plane
-            const size_t lds16 = 2 * (size_t)kPfTile * sizeof(uint16_t);   // 64 KiB
+            const size_t lds16 = 2 * (size_t)kPfD16Tile * sizeof(uint16_t);   // 128 KiB
             static bool d16_attr = false;
             if (!d16_attr) {
                 hipError_t e = hipFuncSetAttribute((const void *)k_pf_down16,

@@ -840,11 +840,11 @@ CONFIG5_PARITY_BAR = 0.85
 
 
 def pf_thin_tokens(ids, shape):
-    """Tokens with a pair in a thin tile (an expert's last tile of 1-4 pairs,
-    pairs in token order; the shared expert takes every token). At F = 1024
-    the Q6_K down projection runs those pairs on its integer path with exact
-    weights instead of fp16(q-32)*fp16(d*sc), so the same-rounding oracle
-    does not describe them; they are held to the exact bar."""
+    """Tokens routed to a thin expert (1-4 pairs in all; the shared expert
+    takes every token). At F = 1024 the Q6_K down projection runs those
+    pairs on its integer path with exact weights instead of
+    fp16(q-32)*fp16(d*sc), so the same-rounding oracle does not describe
+    them; they are held to the exact bar."""
     if not (shape.down_type == O.Q6_K and shape.inter == 1024):
         return set()
     T = ids.shape[0]
@@ -856,9 +856,8 @@ def pf_thin_tokens(ids, shape):
         per[shape.n_experts] = list(range(T))
     out = set()
     for toks in per:
-        rem = len(toks) % 64
-        if 1 <= rem <= 4:
-            out.update(toks[-rem:])
+        if 1 <= len(toks) <= 4:
+            out.update(toks)
     return out
 
 
@@ -937,12 +936,12 @@ def test_prefill_small_vs_oracle(gpu, T, shared, gate_vec, resid, H):
 
 @pytest.mark.parametrize("T", [1, 9, 68, 70])
 def test_prefill_thin_tiles_f1024(gpu, T):
-    """Expert FFN 1024 wide (the config shape's F): tiles of at most 4 pairs
-    take the integer-MFMA down path (k_pf_down_thin), the others the fp16
-    GEMM; every token and output against the oracle's per-token composition,
-    with a mix of thin and thick tiles at T = 68 / 70 (32 experts, top-4). At
-    T = 68 the shared expert's 68 pairs make a 64-pair tile followed by a
-    4-pair thin tile (a thin tile whose first pair is not 0)."""
+    """Expert FFN 1024 wide (the config shape's F): experts of at most 4
+    pairs take the integer-MFMA down path (k_pf_down_thin), the others the
+    fp16 GEMM in tiles of up to 128 pairs; every token and output against the
+    oracle's per-token composition, with a mix of thin and thick experts at
+    T = 68 / 70 (32 experts, top-4). At T = 68 the shared expert's 68 pairs
+    are one 64-pair gate/up tile and a 4-pair one, and one 5-block down tile."""
     from fomoe_amd import synthetic as S
     say(f"prefill thin tiles F=1024 T={T}")
     shape = S.LayerShape(n_embd=512, inter=1024, n_experts=32, k=4, shared=True)
@@ -963,7 +962,7 @@ def test_prefill_thin_tiles_f1024(gpu, T):
     if T >= 68:
         assert thick >= 1                 # beside full fp16 tiles
     if T == 68:
-        assert T % 64 in range(1, 5)      # the shared expert's last tile is thin, after a full one
+        assert T % 64 in range(1, 5)      # the shared expert's last gate/up tile has 1-4 pairs
 
 
 @pytest.mark.parametrize("gate,down", [(O.Q4_K, O.Q5_K), (O.Q4_K, O.Q8_0), (O.Q5_K, O.Q5_K), (O.Q8_0, O.Q8_0),
