@@ -310,27 +310,31 @@ __global__ __launch_bounds__(256) void k_pf_topk(PrefillArgs a) {
 // shared expert, all T tokens).
 constexpr int kPfGroupLds = 16384;     // E*W words of each table
 
-FO_DEV int block_exclusive_scan(int v, int *buf) {   // 1024 threads, returns exclusive prefix
-    // inclusive scan within each wave by shuffles, then the 16 wave totals
-    // (buf[0..15]) scanned by every thread: two barriers per scan
+// Exclusive prefix over the 1024 threads of 64-bit packed fields: inclusive
+// scan within each wave by shuffles, then the 16 wave totals (buf[0..15])
+// summed by every thread; two barriers per scan.
+FO_DEV uint64_t block_exclusive_scan64(uint64_t v, uint64_t *buf) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    int x = v;
+    uint64_t x = v;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, 64);
+        const uint64_t y = (uint64_t)__shfl_up((long long)x, o, 64);
         if (lane >= o) x += y;
     }
     if (lane == 63) buf[wv] = x;
     __syncthreads();
-    int base = 0;
+    uint64_t base = 0;
     for (int w = 0; w < wv; w++) base += buf[w];
-    __syncthreads();                                 // buf is free for the next scan
+    __syncthreads();
     return base + x - v;
 }
 
+// Bit fields of the packed scans (each field holds its total over all experts:
+// pairs < 2^21, full tiles < 2^16, per-expert-at-most-one classes < 2^12).
+FO_DEV uint32_t fld(uint64_t v, int lo, int bits) { return (uint32_t)((v >> lo) & ((1ull << bits) - 1)); }
+
 __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     extern __shared__ uint32_t lds[];
-    __shared__ int scan_buf[1024];
     const int tid = threadIdx.x;
     const int W = (a.T + 31) / 32, E = a.E, k = a.k, K1 = k + 1;
     uint32_t *bm = lds, *pre = lds + E * W;
@@ -348,29 +352,44 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     } else if (tid == E && sh) {
         cnt = a.T;
     }
-    const int off = block_exclusive_scan(cnt, scan_buf);   // pair offset of expert tid
-    const int nt = (cnt + kPfMT - 1) / kPfMT;
-    const int toff = block_exclusive_scan(nt, scan_buf);   // first tile of expert tid
+    // every prefix the tables need in four scans of packed fields
+    constexpr int DT = 2 * kPfMT;
+    const int nt = (cnt + kPfMT - 1) / kPfMT;                                 // 64-pair tiles
+    const int dn = (cnt + DT - 1) / DT;                                       // 128-pair tiles
     // The GEMMs take tiles in decreasing cost: entry i's fourth word is the
     // i-th tile by token-block count (4, 3, 2, 1; expert order within a
-    // count), so the last work handed out is the cheapest; one-block tiles of
-    // at most kPfThin pairs come last of all (the thin tiles, which the Q6_K
-    // down projection runs on its integer path). Per expert: its full tiles
-    // (count 4) and its last, partial tile (count cb).
+    // count), so the last work handed out is the cheapest; the one tile of an
+    // expert of at most kPfThin pairs comes last of all (the thin experts,
+    // whose Q6_K down projection runs on the integer path). Per expert: its
+    // full tiles (count 4) and its last, partial tile (count cb).
     const int nfull = cnt / kPfMT, rem = cnt - kPfMT * nfull, cb = (rem + 15) >> 4;   // cb = 0: no partial tile
-    const int thin = cnt > 0 && cnt <= kPfThin;   // an expert of at most kPfThin pairs: its one tile
+    const int thin = cnt > 0 && cnt <= kPfThin;
     const int c4 = nfull + (cb == 4), c3 = cb == 3, c2 = cb == 2, c1 = cb == 1 && !thin;
-    const int o43 = block_exclusive_scan(c4 | (c3 << 16), scan_buf);
-    const int o21 = block_exclusive_scan(c2 | (c1 << 16), scan_buf);
-    const int o0 = block_exclusive_scan(thin, scan_buf);
-    __shared__ int s_tot[3];
-    if (tid == 1023) { s_tot[0] = o43 + (c4 | (c3 << 16)); s_tot[1] = o21 + (c2 | (c1 << 16)); s_tot[2] = o0 + thin; }
+    // Double tiles for k_pf_down16: per expert ceil(cnt / 128) tiles of up to
+    // 2 kPfMT pairs (its weights are read and decoded once per 128 pairs), in
+    // decreasing token-block count (8 .. 1), those of thin experts last.
+    const int dfull = cnt / DT, drem = cnt - DT * dfull, dcb = (drem + 15) >> 4;
+    auto cls = [&](int b) { return b == 8 ? dfull + (dcb == 8) : (dcb == b && !thin ? 1 : 0); };
+    __shared__ uint64_t scan64[16];
+    const uint64_t p1 = (uint64_t)cnt | ((uint64_t)nt << 21) | ((uint64_t)dn << 42);
+    const uint64_t p2 = (uint64_t)c4 | ((uint64_t)c3 << 16) | ((uint64_t)c2 << 28) | ((uint64_t)c1 << 40) |
+                        ((uint64_t)thin << 52);
+    const uint64_t p3 = (uint64_t)cls(8) | ((uint64_t)cls(7) << 16) | ((uint64_t)cls(6) << 28) |
+                        ((uint64_t)cls(5) << 40) | ((uint64_t)cls(4) << 52);
+    const uint64_t p4 = (uint64_t)cls(3) | ((uint64_t)cls(2) << 12) | ((uint64_t)cls(1) << 24);
+    const uint64_t s1 = block_exclusive_scan64(p1, scan64), s2 = block_exclusive_scan64(p2, scan64);
+    const uint64_t s3 = block_exclusive_scan64(p3, scan64), s4 = block_exclusive_scan64(p4, scan64);
+    const int off = (int)fld(s1, 0, 21), toff = (int)fld(s1, 21, 21), doff = (int)fld(s1, 42, 21);
+    __shared__ uint64_t s_tot[4];
+    if (tid == 1023) { s_tot[0] = s1 + p1; s_tot[1] = s2 + p2; s_tot[2] = s3 + p3; s_tot[3] = s4 + p4; }
     __syncthreads();
-    const int T4 = s_tot[0] & 0xFFFF, T3 = s_tot[0] >> 16, T2 = s_tot[1] & 0xFFFF, T1 = s_tot[1] >> 16;
-    const int b4 = o43 & 0xFFFF;                                 // this expert's first rank per count
-    const int bpart = cb == 4 ? b4 + nfull : cb == 3 ? T4 + (o43 >> 16)
-                    : cb == 2 ? T4 + T3 + (o21 & 0xFFFF) : thin ? T4 + T3 + T2 + T1 + o0
-                    : T4 + T3 + T2 + (o21 >> 16);
+    const uint64_t t1 = s_tot[0], t2 = s_tot[1], t3 = s_tot[2], t4 = s_tot[3];
+    const int T4 = (int)fld(t2, 0, 16), T3 = (int)fld(t2, 16, 12), T2 = (int)fld(t2, 28, 12), T1 = (int)fld(t2, 40, 12);
+    const int Tthin = (int)fld(t2, 52, 12);
+    const int b4 = (int)fld(s2, 0, 16);                                       // this expert's first rank per count
+    const int bpart = cb == 4 ? b4 + nfull : cb == 3 ? T4 + (int)fld(s2, 16, 12)
+                    : cb == 2 ? T4 + T3 + (int)fld(s2, 28, 12) : thin ? T4 + T3 + T2 + T1 + (int)fld(s2, 52, 12)
+                    : T4 + T3 + T2 + (int)fld(s2, 40, 12);
     if (tid <= E) {
         for (int i = 0; i < nt; i++) {
             int32_t *tp = a.tiles + 4 * (toff + i);
@@ -378,45 +397,26 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
             a.tiles[4 * (i < nfull ? b4 + i : bpart) + 3] = toff + i;
         }
     }
-    // [0]: tiles, [1]: tiles before the thin ones, [2]: k_pf_gateup_f16 work counter
-    if (tid == 1023) { a.n_tiles[0] = toff + nt; a.n_tiles[1] = toff + nt - s_tot[2]; a.n_tiles[2] = 0; }
-    // Double tiles for k_pf_down16: per expert ceil(cnt / 128) tiles of up to
-    // 2 kPfMT pairs (its weights are read and decoded once per 128 pairs), in
-    // decreasing token-block count (8 .. 1), those of thin experts last.
+    // [0]: tiles, [1]: tiles before the thin ones, [2]: k_pf_gateup_f16 work
+    // counter, [3]: double tiles, [4]: double tiles before the thin experts'
+    const int NT = (int)fld(t1, 21, 21), ND = (int)fld(t1, 42, 21);
+    if (tid == 1023) { a.n_tiles[0] = NT; a.n_tiles[1] = NT - Tthin; a.n_tiles[2] = 0; a.n_tiles[3] = ND; a.n_tiles[4] = ND - Tthin; }
     {
-        constexpr int DT = 2 * kPfMT;
-        const int dn = (cnt + DT - 1) / DT, dfull = cnt / DT, drem = cnt - DT * dfull, dcb = (drem + 15) >> 4;
-        const int doff = block_exclusive_scan(dn, scan_buf);   // storage index of the expert's first
-        // count per class: c[8] = full double tiles (+ a partial one of 8 blocks), c[1..7] = the partial one
-        auto cls = [&](int b) { return b == 8 ? dfull + (dcb == 8) : (dcb == b && !thin ? 1 : 0); };
-        const int o87 = block_exclusive_scan(cls(8) | (cls(7) << 16), scan_buf);
-        const int o65 = block_exclusive_scan(cls(6) | (cls(5) << 16), scan_buf);
-        const int o43 = block_exclusive_scan(cls(4) | (cls(3) << 16), scan_buf);
-        const int o21 = block_exclusive_scan(cls(2) | (cls(1) << 16), scan_buf);
-        const int oth = block_exclusive_scan(thin, scan_buf);
-        __shared__ int s_dt[5];
-        if (tid == 1023) {
-            s_dt[0] = o87 + (cls(8) | (cls(7) << 16)); s_dt[1] = o65 + (cls(6) | (cls(5) << 16));
-            s_dt[2] = o43 + (cls(4) | (cls(3) << 16)); s_dt[3] = o21 + (cls(2) | (cls(1) << 16));
-            s_dt[4] = oth + thin;
-            a.n_tiles[3] = doff + dn;
-            a.n_tiles[4] = doff + dn - (oth + thin);
-        }
-        __syncthreads();
         int tot[9], base[9];   // per class count and first rank, classes in order 8, 7, .., 1
-        tot[8] = s_dt[0] & 0xFFFF; tot[7] = s_dt[0] >> 16; tot[6] = s_dt[1] & 0xFFFF; tot[5] = s_dt[1] >> 16;
-        tot[4] = s_dt[2] & 0xFFFF; tot[3] = s_dt[2] >> 16; tot[2] = s_dt[3] & 0xFFFF; tot[1] = s_dt[3] >> 16;
+        tot[8] = (int)fld(t3, 0, 16); tot[7] = (int)fld(t3, 16, 12); tot[6] = (int)fld(t3, 28, 12);
+        tot[5] = (int)fld(t3, 40, 12); tot[4] = (int)fld(t3, 52, 12);
+        tot[3] = (int)fld(t4, 0, 12); tot[2] = (int)fld(t4, 12, 12); tot[1] = (int)fld(t4, 24, 12);
         base[8] = 0;
         for (int b = 7; b >= 1; b--) base[b] = base[b + 1] + tot[b + 1];
         const int thin_base = base[1] + tot[1];
-        const int mine[9] = {0, o21 >> 16, o21 & 0xFFFF, o43 >> 16, o43 & 0xFFFF, o65 >> 16, o65 & 0xFFFF,
-                             o87 >> 16, o87 & 0xFFFF};
+        const int mine[9] = {0, (int)fld(s4, 24, 12), (int)fld(s4, 12, 12), (int)fld(s4, 0, 12), (int)fld(s3, 52, 12),
+                             (int)fld(s3, 40, 12), (int)fld(s3, 28, 12), (int)fld(s3, 16, 12), (int)fld(s3, 0, 16)};
         if (tid <= E) {
             for (int i = 0; i < dn; i++) {
                 int32_t *tp = a.dtiles + 4 * (doff + i);
                 tp[0] = tid; tp[1] = off + DT * i; tp[2] = min(DT, cnt - DT * i);
                 int rank;
-                if (thin) rank = thin_base + oth;
+                if (thin) rank = thin_base + (int)fld(s2, 52, 12);
                 else if (i < dfull) rank = base[8] + mine[8] + i;
                 else rank = dcb == 8 ? base[8] + mine[8] + dfull : base[dcb] + mine[dcb];
                 a.dtiles[4 * rank + 3] = doff + i;
