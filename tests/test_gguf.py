@@ -396,6 +396,58 @@ def test_load_moe_layer_runs_against_oracle(gpu, tmp_path, case):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("case", ["q6k_down_f32_router", "q4k_down_f16_router_no_shared"] + list(SHEXP_CASES))
+def test_load_moe_layer_prefill(gpu, tmp_path, case):
+    """The GGUF-loaded layer of the cases above through gpu_moe_prefill
+    (no RMSNorm; bf16 tokens): routing equal to the oracle's and every token
+    against the oracle's composition with each expert's own operand rounding
+    (bf16_mask 16); a shared expert whose gate and up are Q5_K and Q8_0 is a
+    type mix the prefill does not run (-1)."""
+    E, H, F, k, T = 12, 512, 256, 4, 40
+    dt, rt, shared = (FA.Q6_K, FA.F32, True) if case.startswith("q6k") else (FA.Q4_K, FA.F16, False)
+    st, Fs = (FA.Q4_K, FA.Q4_K, dt), F
+    if case in SHEXP_CASES:
+        (st, Fs), dt, rt, shared = SHEXP_CASES[case], FA.Q4_K, FA.F32, True
+    kvs, tensors, blobs, gs, ds, stride, router, norm, gvec = moe_model(
+        E, H, F, k, 94, dt, rt, shared, shared_types=st, Fs=Fs, fs_key=Fs if case in SHEXP_CASES else None)
+    sgs, sus = O.row_bytes(st[0], H) * Fs, O.row_bytes(st[1], H) * Fs
+    p = str(tmp_path / "moe.gguf")
+    write_gguf(p, kvs, tensors)
+    with FA.Gguf(p) as g:
+        L = gpu.gguf_load_moe_layer(g, 0)
+    try:
+        x = O.to_bf16(O.synth_f32(96, 0, 1.0, T * H)).reshape(T, H)
+        dx, dout = gpu.upload(x), gpu.alloc(4 * T * H)
+        if shared and st[0] != st[1] and FA.Q4_K not in st[:2]:
+            with pytest.raises(FA.GpuError):
+                gpu.moe_prefill(L, dx, T, dout, FA.MOE_RESIDUAL)
+            return
+        gpu.moe_prefill(L, dx, T, dout, FA.MOE_RESIDUAL)
+        got = gpu.download(dout, np.float32, T * H).reshape(T, H)
+        ids, w = gpu.prefill_routing(T, k)
+        d = O.MoeDesc()
+        d.n_embd, d.inter, d.n_experts, d.k = H, F, E, k
+        d.gate_type, d.up_type, d.down_type = O.Q4_K, O.Q4_K, dt
+        d.gate_size, d.up_size, d.expert_stride = gs, gs, stride
+        d.router, d.experts = router.ctypes.data, blobs.ctypes.data
+        if shared:
+            d.shared = blobs.ctypes.data + E * stride
+            d.shared_inter, d.shared_gate_size, d.shared_up_size = Fs, sgs, sus
+            d.shared_gate_type, d.shared_up_type, d.shared_down_type = st
+            d.shared_gate_vec = gvec.ctypes.data
+        want, oids, ow = O.moe_prefill(d, x, 0, T, O.MOE_RESIDUAL, bf16_mask=16)
+        assert np.array_equal(ids, oids)
+        xf = O.bf16_to_f32(x).reshape(T, H)
+        e1 = max(inf_rel(got[t] - xf[t], want[t] - xf[t]) for t in range(T))
+        print(f"  gguf prefill {case}: worst token inf_rel (ffn) vs same rounding {e1:.3e}")
+        # the prefill's same-rounding bar for its fp16 paths (measured 6.8e-5 with a
+        # Q6_K down projection, 5e-6 on the bf16 paths)
+        assert e1 <= 3e-4
+    finally:
+        gpu.gguf_free_moe_layer(L)
+
+
+@pytest.mark.gpu
 def test_load_moe_layer_rejects_bad_models(gpu, tmp_path):
     E, H, F, k = 4, 256, 256, 2
     kvs, tensors, *_ = moe_model(E, H, F, k, 96)
