@@ -1137,6 +1137,50 @@ def test_prefill_chunked_batch(gpu):
         pf_check(got[t:t + 1], d, x, t, shape, flags=O.MOE_RESIDUAL)
 
 
+def test_prefill_chunked_shared_own_types(gpu):
+    """The chunked batch (512 experts x 1300 tokens: chunks of 1024 + 276)
+    with the shared expert in its own types and intermediate size (Q4_K gate
+    and up, Q8_0 down, F_s = 512): the shared pass runs per chunk;
+    bit-identical to the two calls made separately, and tokens on both sides
+    of the chunk boundary against the oracle with each expert's own operand
+    rounding."""
+    from fomoe_amd import synthetic as S
+    T, E, Fs = 1300, 512, 512
+    say(f"prefill chunked, shared expert in its own types T={T} E={E} Fs={Fs}")
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=E, k=4, shared=True)
+    H, k = shape.n_embd, shape.k
+    L = S.build_layer(gpu, shape, 0, seed=25, zipf_s=1.1, norm=False)
+    sh = [O.synth_quant(O.Q4_K, 27, 0, 0.02, Fs, H), O.synth_quant(O.Q4_K, 27, 1, 0.02, Fs, H),
+          O.synth_quant(O.Q8_0, 27, 2, 0.02, H, Fs)]
+    sblob = np.concatenate(sh)
+    dS = gpu.upload(sblob)
+    L.desc.shared, L.desc.shared_inter = dS.ptr, Fs
+    L.desc.shared_gate_size, L.desc.shared_up_size = sh[0].size, sh[1].size
+    L.desc.shared_gate_type, L.desc.shared_up_type, L.desc.shared_down_type = O.Q4_K, O.Q4_K, O.Q8_0
+    dx = S.tokens_bf16(gpu, T, H, seed=26)
+    dout = gpu.alloc(4 * T * H)
+    gpu.moe_prefill(L.desc, dx, T, dout, FA.MOE_RESIDUAL)
+    got = gpu.download(dout, np.float32, T * H).reshape(T, H)
+    ids, _ = gpu.prefill_routing(T, k)
+    d2 = gpu.alloc(4 * T * H)
+    gpu.moe_prefill(L.desc, dx, 1024, d2, FA.MOE_RESIDUAL)
+    gpu.moe_prefill(L.desc, dx.offset(2 * 1024 * H), T - 1024, d2.offset(4 * 1024 * H), FA.MOE_RESIDUAL)
+    sep = gpu.download(d2, np.float32, T * H).reshape(T, H)
+    assert np.array_equal(got.view(np.uint32), sep.view(np.uint32))
+    x = gpu.download(dx, np.uint16, T * H).reshape(T, H)
+    d, keep = _prefill_host_layer(shape, 0, 25, True)
+    d.shared = sblob.ctypes.data
+    d.shared_inter, d.shared_gate_size, d.shared_up_size = Fs, sh[0].size, sh[1].size
+    d.shared_gate_type, d.shared_up_type, d.shared_down_type = O.Q4_K, O.Q4_K, O.Q8_0
+    xf = O.bf16_to_f32(x).reshape(T, H)
+    for t in (0, 1023, 1024, 1299):
+        want, oids, _ = O.moe_prefill(d, x, t, 1, O.MOE_RESIDUAL, bf16_mask=16)
+        assert np.array_equal(ids[t], oids[0]), t
+        e = inf_rel(got[t] - xf[t], want[0] - xf[t])
+        say(f"  token {t}: inf_rel (ffn) vs same rounding {e:.3e}")
+        assert e <= 3e-4
+
+
 def test_prefill_config5_sampled(gpu):
     """Config 5 at full size (512 tokens, 512 experts, top-10, H 4096, F 1024,
     Zipf(1.1) router bias): routing of every token against the oracle's fp32
