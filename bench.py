@@ -1,7 +1,7 @@
 """Benchmark of the quantized MoE expert hot path on one MI355X.
 
-Headline (BASELINE.json metric "Q4_K/Q6_K expert matvec GB/s (% of HBM peak);
-us per MoE layer at top-10/512"), measured on BASELINE config 2 — the
+Headline (the benchmark metric "Q4_K/Q6_K expert matvec GB/s (% of HBM peak);
+us per MoE layer at top-10/512"), measured on benchmark config 2 — the
 expert down-projection shape, Q6_K 4096 x 1024, x ~ N(0,1) — as a rotation
 over 512 distinct expert matrices (1.76 GB, far beyond the 256 MB Infinity
 Cache) in one batched launch per step. A step is one pass over the 512
@@ -63,7 +63,7 @@ def spread_of(gpu, fn, n, scale=1.0, prefix=""):
 
 class Rotation:
     """n_mats distinct [M x K] matrices of type t (matrix m from stream m of
-    wseed; matrix 0 is the BASELINE config's W) times one x, one launch per
+    wseed; matrix 0 is the benchmark config's W) times one x, one launch per
     step. setup() generates the weights in HBM, timed() runs W warmup and K
     timed steps back to back, spread() times >= 100 launches one by one."""
 

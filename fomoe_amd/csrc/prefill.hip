@@ -1,4 +1,4 @@
-// prefill.hip — the multi-token MoE path (512 tokens,
+// prefill.hip — the multi-token MoE path (benchmark config 5: 512 tokens,
 // top-10 of 512 experts, Q4_K gate/up and Q6_K down).
 //
 //   P1 k_pf_router3  logits[T x E] = x . W_r^T (+ bias): bf16 MFMA on x (bf16)

@@ -1,4 +1,4 @@
-"""Device-resident synthetic workloads of the BASELINE configurations.
+"""Device-resident synthetic workloads of the benchmark configurations.
 
 Stream numbering (this build's own definition; the reference has no
 synthetic data): stream(layer, expert, kind) = ((layer + 1) << 24) |

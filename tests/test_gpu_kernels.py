@@ -621,9 +621,9 @@ def test_moe_layer_shared_rejects_bad_shapes(gpu):
 
 @pytest.mark.parametrize("seed", [4, 5, 6])
 def test_moe_layer_config3_full(gpu, seed):
-    """BASELINE config 3 at full size: 512 experts (Q4_K gate/up 1024x4096, Q6_K
+    """Benchmark config 3 at full size: 512 experts (Q4_K gate/up 1024x4096, Q6_K
     down 4096x1024) + shared, top-10, generated in HBM; the oracle rebuilds the
-    router and only the selected experts on the CPU. Seed 4 is the BASELINE
+    router and only the selected experts on the CPU. Seed 4 is the benchmark
     one; 5 and 6 are further samples of the same workload."""
     from fomoe_amd import synthetic as S
     say("moe config3 full, seed", seed)

@@ -1,4 +1,4 @@
-"""GPU parity of BASELINE config 4 at its real size: the 60-layer, 512-expert,
+"""GPU parity of benchmark config 4 at its real size: the 60-layer, 512-expert,
 top-10, Zipf(1.1)-routed Q4_K/Q6_K stack, fully HBM-resident (251.6 GB),
 decoded from the captured HIP graph of gpu_moe_stack_decode.
 
