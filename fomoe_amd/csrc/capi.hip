@@ -676,11 +676,14 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     if (!fo::prefill_types_ok(L->gate_type, L->up_type, L->down_type))
         return fail(ctx, -1, "moe prefill: types gate %d up %d down %d (gate/up Q4_K/Q6_K, or both Q5_K or "
                              "both Q8_0; down Q4_K, Q5_K, Q6_K or Q8_0)", L->gate_type, L->up_type, L->down_type);
-    // a shared expert in other types or F_s runs as a one-expert pass of its
-    // own (every token routed to it), whose output the routed pass combines
+    // a shared expert whose gate/up types or F_s differ runs as a one-expert
+    // pass of its own (every token routed to it), whose output the routed
+    // pass combines; one that differs in its down type only (the usual GGUF
+    // mix) shares the routed gate/up GEMM and gets a down launch of its own
     const bool own = L->shared && (L->shared_inter != L->inter || L->shared_gate_type != L->gate_type ||
-                                   L->shared_up_type != L->up_type || L->shared_down_type != L->down_type);
-    if (own && !fo::prefill_types_ok(L->shared_gate_type, L->shared_up_type, L->shared_down_type))
+                                   L->shared_up_type != L->up_type);
+    const bool down_own = L->shared && !own && L->shared_down_type != L->down_type;
+    if ((own || down_own) && !fo::prefill_types_ok(L->shared_gate_type, L->shared_up_type, L->shared_down_type))
         return fail(ctx, -1, "moe prefill: shared-expert types gate %d up %d down %d", L->shared_gate_type,
                     L->shared_up_type, L->shared_down_type);
     const int T = n_tokens, E = L->n_experts, k = L->k, H = L->n_embd, F = L->inter;
@@ -734,6 +737,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     a.shared = sh ? (const uint8_t *)L->shared : nullptr;
     a.sh_gate_size = L->shared_gate_size; a.sh_up_size = L->shared_up_size;
     a.ys = own ? ctx->pf_ys : nullptr;
+    a.sh_down_type = down_own ? L->shared_down_type : -1;
     a.shared_gate_vec = L->shared_gate_vec;
     a.residual = (flags & GPU_MOE_RESIDUAL) ? 1 : 0;
     a.logits = ctx->pf_logits; a.pairpos = ctx->pf_pairpos;
@@ -762,7 +766,7 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
             const uint64_t sds = fomoe_row_bytes(L->shared_down_type, Fs) * (uint64_t)H;
             b.stride = (L->shared_gate_size + L->shared_up_size + sds + 15) & ~(uint64_t)15;
             b.gate_size = L->shared_gate_size; b.up_size = L->shared_up_size;
-            b.shared = nullptr; b.shared_gate_vec = nullptr; b.ys = nullptr;
+            b.shared = nullptr; b.shared_gate_vec = nullptr; b.ys = nullptr; b.sh_down_type = -1;
             b.residual = 0; b.out = ctx->pf_ys;
             b.ids = ctx->pf_ids2; b.w = (float *)(ctx->pf_ids2 + Tc);
             b.max_tiles = fo::prefill_max_tiles(n, 1, 1, false);

@@ -42,8 +42,9 @@ struct PrefillArgs {
     int32_t *pair_tok;           // [P] token of each pair slot, grouped by expert
     int32_t *tiles;              // [max_tiles x 4] {expert (E = shared), first pair, n, order}
     int32_t *dtiles;             // [max_tiles x 4] the same in tiles of up to 2 kPfMT pairs (k_pf_down16)
-    int32_t *n_tiles;            // [5]: tiles, tiles before the thin ones, work counter of the gate/up
-                                 // kernel, double tiles, double tiles before those of thin experts
+    int32_t *n_tiles;            // [6]: tiles, tiles before the thin ones, work counter of the gate/up
+                                 // kernel, double tiles, double tiles before those of thin experts,
+                                 // the shared expert's first tile
     int max_tiles;
     uint16_t *act_hi, *act_lo;   // [P x F] SwiGLU activation as bf16 hi + lo terms (a Q6_K
                                  // down projection rewrites act_hi as fp16 rows, scale in pexp)
@@ -54,6 +55,11 @@ struct PrefillArgs {
     int32_t *pexp;               // [P] power-of-two scale of the fp16 activation rows (Q6_K down)
     uint16_t *rsplit;            // bf16 router GEMM operands (prefill_router_ws_elems)
     int thin_down;               // set by launch_prefill: thin tiles take k_pf_down_thin
+    int sh_down_type;            // -1: the shared down projection has down_type; else its own type
+                                 // (gate/up and F as the routed experts), run by a launch of its own
+    int down_sel;                // set by launch_prefill: 0 every expert's down projection, 1 the
+                                 // routed experts' only, 2 the shared expert's only
+    int dt_sel;                  // set by launch_prefill: the same choice for k_pf_down16's tiles
 };
 
 // Number of pair slots and an upper bound on the GEMM tiles for T tokens.

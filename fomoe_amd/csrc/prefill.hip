@@ -355,7 +355,9 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     // every prefix the tables need in four scans of packed fields
     constexpr int DT = 2 * kPfMT;
     const int nt = (cnt + kPfMT - 1) / kPfMT;                                 // 64-pair tiles
-    const int dn = (cnt + DT - 1) / DT;                                       // 128-pair tiles
+    // 128-pair tiles of the experts k_pf_down16 runs (dt_sel: all, routed, shared)
+    const bool in_dt = a.dt_sel == 0 || (a.dt_sel == 1 ? tid != E : tid == E);
+    const int dn = in_dt ? (cnt + DT - 1) / DT : 0;
     // The GEMMs take tiles in decreasing cost: entry i's fourth word is the
     // i-th tile by token-block count (4, 3, 2, 1; expert order within a
     // count), so the last work handed out is the cheapest; the one tile of an
@@ -363,29 +365,34 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     // whose Q6_K down projection runs on the integer path). Per expert: its
     // full tiles (count 4) and its last, partial tile (count cb).
     const int nfull = cnt / kPfMT, rem = cnt - kPfMT * nfull, cb = (rem + 15) >> 4;   // cb = 0: no partial tile
-    const int thin = cnt > 0 && cnt <= kPfThin;
+    // (a shared expert whose down projection runs in its own type is never thin)
+    const int thin = cnt > 0 && cnt <= kPfThin && !(tid == E && a.sh_down_type >= 0);
     const int c4 = nfull + (cb == 4), c3 = cb == 3, c2 = cb == 2, c1 = cb == 1 && !thin;
     // Double tiles for k_pf_down16: per expert ceil(cnt / 128) tiles of up to
     // 2 kPfMT pairs (its weights are read and decoded once per 128 pairs), in
     // decreasing token-block count (8 .. 1), those of thin experts last.
-    const int dfull = cnt / DT, drem = cnt - DT * dfull, dcb = (drem + 15) >> 4;
-    auto cls = [&](int b) { return b == 8 ? dfull + (dcb == 8) : (dcb == b && !thin ? 1 : 0); };
+    const int dcnt = in_dt ? cnt : 0;
+    const int dfull = dcnt / DT, drem = dcnt - DT * dfull, dcb = (drem + 15) >> 4;
+    const int dthin = thin && in_dt;
+    auto cls = [&](int b) { return b == 8 ? dfull + (dcb == 8) : (dcb == b && !dthin ? 1 : 0); };
     __shared__ uint64_t scan64[16];
     const uint64_t p1 = (uint64_t)cnt | ((uint64_t)nt << 21) | ((uint64_t)dn << 42);
     const uint64_t p2 = (uint64_t)c4 | ((uint64_t)c3 << 16) | ((uint64_t)c2 << 28) | ((uint64_t)c1 << 40) |
                         ((uint64_t)thin << 52);
+    const uint64_t p5 = (uint64_t)dthin;   // thin experts among the double tiles
     const uint64_t p3 = (uint64_t)cls(8) | ((uint64_t)cls(7) << 16) | ((uint64_t)cls(6) << 28) |
                         ((uint64_t)cls(5) << 40) | ((uint64_t)cls(4) << 52);
     const uint64_t p4 = (uint64_t)cls(3) | ((uint64_t)cls(2) << 12) | ((uint64_t)cls(1) << 24);
     const uint64_t s1 = block_exclusive_scan64(p1, scan64), s2 = block_exclusive_scan64(p2, scan64);
-    const uint64_t s3 = block_exclusive_scan64(p3, scan64), s4 = block_exclusive_scan64(p4, scan64);
+    const uint64_t s3 = block_exclusive_scan64(p3, scan64), s4 = block_exclusive_scan64(p4 | (p5 << 36), scan64);
     const int off = (int)fld(s1, 0, 21), toff = (int)fld(s1, 21, 21), doff = (int)fld(s1, 42, 21);
     __shared__ uint64_t s_tot[4];
-    if (tid == 1023) { s_tot[0] = s1 + p1; s_tot[1] = s2 + p2; s_tot[2] = s3 + p3; s_tot[3] = s4 + p4; }
+    if (tid == 1023) { s_tot[0] = s1 + p1; s_tot[1] = s2 + p2; s_tot[2] = s3 + p3; s_tot[3] = s4 + (p4 | (p5 << 36)); }
+    if (tid == E && sh) a.n_tiles[5] = toff;   // the shared expert's first 64-pair tile
     __syncthreads();
     const uint64_t t1 = s_tot[0], t2 = s_tot[1], t3 = s_tot[2], t4 = s_tot[3];
     const int T4 = (int)fld(t2, 0, 16), T3 = (int)fld(t2, 16, 12), T2 = (int)fld(t2, 28, 12), T1 = (int)fld(t2, 40, 12);
-    const int Tthin = (int)fld(t2, 52, 12);
+    const int Tthin = (int)fld(t2, 52, 12), Tdthin = (int)fld(t4, 36, 12);
     const int b4 = (int)fld(s2, 0, 16);                                       // this expert's first rank per count
     const int bpart = cb == 4 ? b4 + nfull : cb == 3 ? T4 + (int)fld(s2, 16, 12)
                     : cb == 2 ? T4 + T3 + (int)fld(s2, 28, 12) : thin ? T4 + T3 + T2 + T1 + (int)fld(s2, 52, 12)
@@ -400,7 +407,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     // [0]: tiles, [1]: tiles before the thin ones, [2]: k_pf_gateup_f16 work
     // counter, [3]: double tiles, [4]: double tiles before the thin experts'
     const int NT = (int)fld(t1, 21, 21), ND = (int)fld(t1, 42, 21);
-    if (tid == 1023) { a.n_tiles[0] = NT; a.n_tiles[1] = NT - Tthin; a.n_tiles[2] = 0; a.n_tiles[3] = ND; a.n_tiles[4] = ND - Tthin; }
+    if (tid == 1023) { a.n_tiles[0] = NT; a.n_tiles[1] = NT - Tthin; a.n_tiles[2] = 0; a.n_tiles[3] = ND; a.n_tiles[4] = ND - Tdthin; }
     {
         int tot[9], base[9];   // per class count and first rank, classes in order 8, 7, .., 1
         tot[8] = (int)fld(t3, 0, 16); tot[7] = (int)fld(t3, 16, 12); tot[6] = (int)fld(t3, 28, 12);
@@ -416,7 +423,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
                 int32_t *tp = a.dtiles + 4 * (doff + i);
                 tp[0] = tid; tp[1] = off + DT * i; tp[2] = min(DT, cnt - DT * i);
                 int rank;
-                if (thin) rank = thin_base + (int)fld(s2, 52, 12);
+                if (dthin) rank = thin_base + (int)fld(s4, 36, 12);
                 else if (i < dfull) rank = base[8] + mine[8] + i;
                 else rank = dcb == 8 ? base[8] + mine[8] + dfull : base[dcb] + mine[dcb];
                 a.dtiles[4 * rank + 3] = doff + i;
@@ -1060,9 +1067,15 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t dxs[];   // 2 buffers x {hi, lo} tiles
     int tile, rbk;
     pf_tile_of(a.H / (32 * kPfDownWaves), tile, rbk);
-    if (tile >= *a.n_tiles) return;
+    if (a.down_sel == 2) {   // the shared expert's tiles only: a grid over ceil(T / kPfMT) of them
+        if (tile >= (a.T + kPfMT - 1) / kPfMT) return;
+        tile += a.n_tiles[5];
+    } else if (tile >= *a.n_tiles) {
+        return;
+    }
     const int4 tl = *(const int4 *)(a.tiles + 4 * tile);
     const int e = tl.x, p0 = tl.y, n = tl.z;
+    if (a.down_sel == 1 && e == a.E) return;                // the routed experts only
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, kg = lane >> 4;
     const bool shared = e == a.E;
     const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
@@ -1532,6 +1545,15 @@ static hipError_t launch_gateup_t(const PrefillArgs &a, hipStream_t s) {
 
 hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
     PrefillArgs a = a_;
+    // A shared expert whose down projection has a type of its own (gate/up
+    // and F as the routed experts) shares the routed gate/up GEMM as expert
+    // E; the down projections run per type: bf16-operand launches first
+    // (they read the hi/lo activation planes), then the fp16 Q6_K path.
+    auto fp16_down = [&](int t) { return t == GGML_TYPE_Q6_K && a.F <= 4096; };
+    const int RT = a.down_type, ST = a.sh_down_type;
+    const bool sep = a.shared && ST >= 0 && ST != RT;
+    a.down_sel = 0;
+    a.dt_sel = !sep ? 0 : fp16_down(RT) ? 1 : fp16_down(ST) ? 2 : 0;
     const bool okt = prefill_types_ok(a.gate_type, a.up_type, a.down_type);
     const int W = (a.T + 31) / 32;
     if (!okt || a.T <= 0 || a.E <= 0 || a.E > 1023 || a.k <= 0 || a.k > a.E || a.k > kMaxK ||
@@ -1609,7 +1631,18 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             }
             down_attr = true;
         }
-        if (a.down_type == GGML_TYPE_Q6_K && a.F <= 4096) {   // fp16 operands, one activation plane
+        auto down_bf16 = [&](int type, int sel) {
+            PrefillArgs d = a;
+            d.down_sel = sel;
+            const unsigned g = sel == 2 ? pf_grid(a.H / (32 * kPfDownWaves), (a.T + kPfMT - 1) / kPfMT) : grid;
+            if (type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<g, kPfDownWaves * 64, lds, s>>>(d);
+            else if (type == GGML_TYPE_Q5_K) k_pf_down<GGML_TYPE_Q5_K><<<g, kPfDownWaves * 64, lds, s>>>(d);
+            else if (type == GGML_TYPE_Q8_0) k_pf_down<GGML_TYPE_Q8_0><<<g, kPfDownWaves * 64, lds, s>>>(d);
+            else k_pf_down<GGML_TYPE_Q6_K><<<g, kPfDownWaves * 64, lds, s>>>(d);
+        };
+        if (!fp16_down(RT)) down_bf16(RT, sep ? 1 : 0);
+        if (sep && !fp16_down(ST)) down_bf16(ST, 2);
+        if (fp16_down(RT) || (sep && fp16_down(ST))) {   // fp16 operands, one activation plane
             const size_t lds16 = 2 * (size_t)kPfD16Tile * sizeof(uint16_t);   // 128 KiB
             static bool d16_attr = false;
             if (!d16_attr) {
@@ -1623,15 +1656,12 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             }
             const int np = prefill_pairs(a.T, a.k, a.shared != nullptr);
             k_pf_actprep_w<<<(np + kApWaves - 1) / kApWaves, 64 * kApWaves, 0, s>>>(a, np);
-            a.thin_down = pf_thin_down(a);
+            a.thin_down = fp16_down(RT) && pf_thin_down(a);   // thin routed experts (never the shared one here)
             int dev = 0, n_cu = 256;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
             k_pf_down16<<<(kPfD16PerCU * n_cu + 7) & ~7, kPfD16Waves * 64, lds16, s>>>(a);   // persistent
             if (a.thin_down) k_pf_down_thin<<<2 * n_cu, 64 * kPfThinWaves, kPfThinLds, s>>>(a);
-        } else if (a.down_type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
-        else if (a.down_type == GGML_TYPE_Q5_K) k_pf_down<GGML_TYPE_Q5_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
-        else if (a.down_type == GGML_TYPE_Q8_0) k_pf_down<GGML_TYPE_Q8_0><<<grid, kPfDownWaves * 64, lds, s>>>(a);
-        else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(a);
+        }
     }
     k_pf_combine<<<dim3(a.T, (a.H + kCombCols - 1) / kCombCols), 256, 0, s>>>(a);
     return hipGetLastError();

@@ -298,9 +298,10 @@ void gpu_gguf_free_moe_layer(gpu_ctx_t *ctx, gpu_moe_layer_t *L);
  * two bf16 terms (hi + lo, within 2^-18). Types: gate/up Q4_K or Q6_K (any
  * mix), or both Q5_K or both Q8_0; down Q4_K, Q5_K, Q6_K or Q8_0; the same
  * sets for the shared expert: with the routed types and
- * intermediate size it is one more pair per token in the routed pass, in
- * types or an intermediate size of its own it runs first as a one-expert
- * pass whose output the routed pass adds at the shared weight;
+ * intermediate size it is one more pair per token in the routed pass (with
+ * only its down type differing, its down projection is a launch of its
+ * own), with gate/up types or an intermediate size of its own it runs first
+ * as a one-expert pass whose output the routed pass adds at the shared weight;
  * n_experts <= 1023; with Q4_K gate/up, the experts and shared pointers,
  * expert_stride and the gate sizes must be multiples of 16 bytes (-1 else). A batch larger than the grouping table (n_experts *
  * ceil(n_tokens/32) > 16384) runs as consecutive chunks of
