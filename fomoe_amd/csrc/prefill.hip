@@ -1062,11 +1062,11 @@ __global__ __launch_bounds__(64 * kWsWaves, 4) void k_pf_gateup_f16(PrefillArgs 
 
 constexpr int kPfDownWaves = 8;                   // 8 waves x 32 rows = 256 weight rows per work-group
 
-template <int DT>
-__global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
+template <int DT, int NW = kPfDownWaves>
+__global__ __launch_bounds__(NW * 64) void k_pf_down(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t dxs[];   // 2 buffers x {hi, lo} tiles
     int tile, rbk;
-    pf_tile_of(a.H / (32 * kPfDownWaves), tile, rbk);
+    pf_tile_of(a.H / (32 * NW), tile, rbk);
     if (a.down_sel == 2) {   // the shared expert's tiles only: a grid over ceil(T / kPfMT) of them
         if (tile >= (a.T + kPfMT - 1) / kPfMT) return;
         tile += a.n_tiles[5];
@@ -1080,7 +1080,7 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
     const bool shared = e == a.E;
     const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)e * a.stride;
     const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
-    const int row = rbk * (32 * kPfDownWaves) + 32 * wave + col;   // rows row, row + 16
+    const int row = rbk * (32 * NW) + 32 * wave + col;   // rows row, row + 16
     const uint64_t db = (uint64_t)(a.F / 256) * PfDec<DT>::BLOCK;
     const uint8_t *drow = blob + down_off + (uint64_t)row * db, *drow1 = drow + 16 * db;
     const int nb = (n + 15) >> 4, NK = a.F / 256;
@@ -1090,7 +1090,7 @@ __global__ __launch_bounds__(kPfDownWaves * 64) void k_pf_down(PrefillArgs a) {
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[h][b] = (f32x4){0, 0, 0, 0};
     auto stage = [&](int kb) {   // first half of the waves stages hi, second half lo
-        constexpr int HW = kPfDownWaves / 2;
+        constexpr int HW = NW / 2;
         uint16_t *buf = dxs + (kb & 1) * 2 * kPfTile + (wave / HW) * kPfTile;
         const uint16_t *plane = (wave / HW) ? a.act_lo : a.act_hi;
         const int lane_ = threadIdx.x & 63, w4 = wave % HW;
@@ -1623,8 +1623,10 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         const unsigned grid = pf_grid(a.H / (32 * kPfDownWaves), a.max_tiles);
         static bool down_attr = false;
         if (!down_attr) {
-            const void *fns[4] = {(const void *)k_pf_down<GGML_TYPE_Q4_K>, (const void *)k_pf_down<GGML_TYPE_Q5_K>,
-                                  (const void *)k_pf_down<GGML_TYPE_Q6_K>, (const void *)k_pf_down<GGML_TYPE_Q8_0>};
+            const void *fns[8] = {(const void *)k_pf_down<GGML_TYPE_Q4_K>, (const void *)k_pf_down<GGML_TYPE_Q5_K>,
+                                  (const void *)k_pf_down<GGML_TYPE_Q6_K>, (const void *)k_pf_down<GGML_TYPE_Q8_0>,
+                                  (const void *)k_pf_down<GGML_TYPE_Q4_K, 4>, (const void *)k_pf_down<GGML_TYPE_Q5_K, 4>,
+                                  (const void *)k_pf_down<GGML_TYPE_Q6_K, 4>, (const void *)k_pf_down<GGML_TYPE_Q8_0, 4>};
             for (const void *f : fns) {
                 const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
                 if (e != hipSuccess) return e;
@@ -1634,11 +1636,18 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         auto down_bf16 = [&](int type, int sel) {
             PrefillArgs d = a;
             d.down_sel = sel;
-            const unsigned g = sel == 2 ? pf_grid(a.H / (32 * kPfDownWaves), (a.T + kPfMT - 1) / kPfMT) : grid;
-            if (type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<g, kPfDownWaves * 64, lds, s>>>(d);
-            else if (type == GGML_TYPE_Q5_K) k_pf_down<GGML_TYPE_Q5_K><<<g, kPfDownWaves * 64, lds, s>>>(d);
-            else if (type == GGML_TYPE_Q8_0) k_pf_down<GGML_TYPE_Q8_0><<<g, kPfDownWaves * 64, lds, s>>>(d);
-            else k_pf_down<GGML_TYPE_Q6_K><<<g, kPfDownWaves * 64, lds, s>>>(d);
+            if (sel == 2) {   // one expert's tiles: 4-wave work-groups of 128 rows, so that they fill the CUs
+                const unsigned g = pf_grid(a.H / (32 * 4), (a.T + kPfMT - 1) / kPfMT);
+                if (type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K, 4><<<g, 256, lds, s>>>(d);
+                else if (type == GGML_TYPE_Q5_K) k_pf_down<GGML_TYPE_Q5_K, 4><<<g, 256, lds, s>>>(d);
+                else if (type == GGML_TYPE_Q8_0) k_pf_down<GGML_TYPE_Q8_0, 4><<<g, 256, lds, s>>>(d);
+                else k_pf_down<GGML_TYPE_Q6_K, 4><<<g, 256, lds, s>>>(d);
+                return;
+            }
+            if (type == GGML_TYPE_Q4_K) k_pf_down<GGML_TYPE_Q4_K><<<grid, kPfDownWaves * 64, lds, s>>>(d);
+            else if (type == GGML_TYPE_Q5_K) k_pf_down<GGML_TYPE_Q5_K><<<grid, kPfDownWaves * 64, lds, s>>>(d);
+            else if (type == GGML_TYPE_Q8_0) k_pf_down<GGML_TYPE_Q8_0><<<grid, kPfDownWaves * 64, lds, s>>>(d);
+            else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(d);
         };
         if (!fp16_down(RT)) down_bf16(RT, sep ? 1 : 0);
         if (sep && !fp16_down(ST)) down_bf16(ST, 2);
