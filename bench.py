@@ -432,24 +432,29 @@ def prefill_config5(gpu, layer, shape, reps):
     pairs = T * (k + 1)
     flops = pairs * 6.0 * H * F + 2.0 * T * E * H
     wbytes = n_unique * shape.expert_bytes() + 4 * E * H   # each touched weight byte once
-    # the same prefill with ffn_down_shexp in its own type (Q8_0), as GGUF
-    # models carry the shared expert: it runs as a one-expert pass of its own
-    gs, us, ds = shape.gate_size, shape.gate_size, FA.row_bytes(FA.Q8_0, F) * H
-    bl = gpu.alloc(gs + us + ds)
-    for t, off, M, K, kind in ((FA.Q4_K, 0, F, H, 0), (FA.Q4_K, gs, F, H, 1), (FA.Q8_0, gs + us, H, F, 2)):
-        gpu.synth_quant(t, 9, kind, 0, 0.02, M, K, 1, bl.offset(off), 0)
-    d = FA.MoeLayer.from_buffer_copy(layer.desc)
-    d.shared, d.shared_inter, d.shared_gate_size, d.shared_up_size = bl.ptr, F, gs, us
-    d.shared_gate_type, d.shared_up_type, d.shared_down_type = FA.Q4_K, FA.Q4_K, FA.Q8_0
-    for _ in range(10):
-        gpu.moe_prefill(d, x, T, out, 0)
-    gpu.sync()
-    gpu.timer_start()
-    for _ in range(reps):
-        gpu.moe_prefill(d, x, T, out, 0)
-    ms_sh = gpu.timer_stop() / reps
-    del bl
-    return {**sp5, "config5_ms": round(ms, 4), "config5_shexp_q8_0_down_ms": round(ms_sh, 4),
+    # the same prefill with the shared expert in its own types, as GGUF models
+    # carry it: only ffn_down_shexp differs (Q8_0: the routed gate/up GEMM
+    # takes it, its down projection a launch of its own), or also its
+    # intermediate size (F_s = 512: a one-expert pass of its own first)
+    shexp = {}
+    for name, Fs in (("q8_0_down", F), ("q8_0_down_fs512", 512)):
+        gs = FA.row_bytes(FA.Q4_K, H) * Fs
+        ds = FA.row_bytes(FA.Q8_0, Fs) * H
+        bl = gpu.alloc(2 * gs + ds)
+        for t, off, M, K, kind in ((FA.Q4_K, 0, Fs, H, 0), (FA.Q4_K, gs, Fs, H, 1), (FA.Q8_0, 2 * gs, H, Fs, 2)):
+            gpu.synth_quant(t, 9, kind, 0, 0.02, M, K, 1, bl.offset(off), 0)
+        d = FA.MoeLayer.from_buffer_copy(layer.desc)
+        d.shared, d.shared_inter, d.shared_gate_size, d.shared_up_size = bl.ptr, Fs, gs, gs
+        d.shared_gate_type, d.shared_up_type, d.shared_down_type = FA.Q4_K, FA.Q4_K, FA.Q8_0
+        for _ in range(10):
+            gpu.moe_prefill(d, x, T, out, 0)
+        gpu.sync()
+        gpu.timer_start()
+        for _ in range(reps):
+            gpu.moe_prefill(d, x, T, out, 0)
+        shexp[f"config5_shexp_{name}_ms"] = round(gpu.timer_stop() / reps, 4)
+        del bl
+    return {**sp5, **shexp, "config5_ms": round(ms, 4),
             "config5_tok_per_s": round(T / (ms / 1e3), 1),
             "config5_experts_touched": n_unique, "config5_weight_bytes": wbytes,
             "config5_GB/s": round(wbytes / (ms * 1e6), 1),

@@ -91,7 +91,7 @@ void gpu_free(gpu_ctx_t *c) {
                     c->act2, c->vec_in, c->vec_out, c->staging, c->pf_logits, c->pf_ids,
                     c->pf_w, c->pf_pairpos, c->pf_pairtok, c->pf_tiles, c->pf_ntiles,
                     c->pf_act, c->pf_outp, c->pf_xsum, c->pf_rsplit, c->sh_act, c->sh_ys,
-                    c->pf_ys, c->pf_ids2, c->pf_zrouter};
+                    c->pf_ys};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     for (int b = 0; b < 2; b++) {
@@ -715,14 +715,8 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
     HIPC(ensure(ctx->pf_ntiles, ctx->pf_ntiles_cap, 256));
     const size_t Pact = std::max(P * F, (size_t)Tc * Fs);   // activation elements of either pass
     HIPC(ensure(ctx->pf_act, ctx->pf_act_cap, 2 * sizeof(uint16_t) * Pact));
-    if (own) {   // the shared pass: its output [Tc x H], routing [Tc] / [Tc x 2], a zero router row
+    if (own)   // the shared pass's output [Tc x H] (its down rows, pairs in token order)
         HIPC(ensure(ctx->pf_ys, ctx->pf_ys_cap, sizeof(float) * (size_t)Tc * H));
-        HIPC(ensure(ctx->pf_ids2, ctx->pf_ids2_cap, sizeof(int32_t) * (size_t)Tc * 3));
-        if (ctx->pf_zrouter_cap < sizeof(float) * (size_t)H) {
-            HIPC(ensure(ctx->pf_zrouter, ctx->pf_zrouter_cap, sizeof(float) * (size_t)H));
-            HIPC(hipMemsetAsync(ctx->pf_zrouter, 0, sizeof(float) * (size_t)H, ctx->stream));
-        }
-    }
     HIPC(ensure(ctx->pf_outp, ctx->pf_outp_cap, sizeof(float) * P * H));
     HIPC(ensure(ctx->pf_rsplit, ctx->pf_rsplit_cap, sizeof(uint16_t) * fo::prefill_router_ws_elems(E, Tc, H)));
     // xsum [Tc x H/32] fp32, then x16 [Tc x H] fp16, then xexp [Tc] int32, then pexp [P] int32
@@ -761,17 +755,20 @@ int gpu_moe_prefill(gpu_ctx_t *ctx, const gpu_moe_layer_t *L, const uint16_t *d_
             fo::PrefillArgs b = a;
             b.E = 1; b.k = 1; b.F = Fs;
             b.gate_type = L->shared_gate_type; b.up_type = L->shared_up_type; b.down_type = L->shared_down_type;
-            b.router = ctx->pf_zrouter; b.router_bias = nullptr;   // every logit 0: one expert, weight 1
+            b.one_expert = 1;             // no router or combine: the down rows are ys in token order
+            b.xprep_ready = 0;            // this chunk's tokens are prepared here
+            b.router = nullptr; b.router_bias = nullptr;
             b.experts = (const uint8_t *)L->shared;
             const uint64_t sds = fomoe_row_bytes(L->shared_down_type, Fs) * (uint64_t)H;
             b.stride = (L->shared_gate_size + L->shared_up_size + sds + 15) & ~(uint64_t)15;
             b.gate_size = L->shared_gate_size; b.up_size = L->shared_up_size;
             b.shared = nullptr; b.shared_gate_vec = nullptr; b.ys = nullptr; b.sh_down_type = -1;
-            b.residual = 0; b.out = ctx->pf_ys;
-            b.ids = ctx->pf_ids2; b.w = (float *)(ctx->pf_ids2 + Tc);
+            b.residual = 0; b.out = nullptr; b.outp = ctx->pf_ys;
             b.max_tiles = fo::prefill_max_tiles(n, 1, 1, false);
             HIPC(fo::launch_prefill(b, ctx->stream));
         }
+        // the shared pass prepared these tokens' fp16 rows for Q4_K gate/up
+        a.xprep_ready = own && L->shared_gate_type == GGML_TYPE_Q4_K && L->shared_up_type == GGML_TYPE_Q4_K;
         HIPC(fo::launch_prefill(a, ctx->stream));
     }
     ctx->pf_T = T;

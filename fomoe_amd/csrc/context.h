@@ -53,8 +53,6 @@ struct gpu_ctx {
     float *pf_xsum = nullptr;      size_t pf_xsum_cap = 0;
     uint16_t *pf_rsplit = nullptr; size_t pf_rsplit_cap = 0;   // bf16 router GEMM operands
     float *pf_ys = nullptr;        size_t pf_ys_cap = 0;       // shared-expert pass output (own types)
-    int32_t *pf_ids2 = nullptr;    size_t pf_ids2_cap = 0;     // its routing (ids, then weights)
-    float *pf_zrouter = nullptr;   size_t pf_zrouter_cap = 0;  // its router: one zero row
     int pf_T = 0, pf_k = 0;
 
     // pinned staging for host->device uploads of expert stores

@@ -60,6 +60,10 @@ struct PrefillArgs {
     int down_sel;                // set by launch_prefill: 0 every expert's down projection, 1 the
                                  // routed experts' only, 2 the shared expert's only
     int dt_sel;                  // set by launch_prefill: the same choice for k_pf_down16's tiles
+    int one_expert;              // every token to expert 0 at weight 1 (E = k = 1, no shared expert):
+                                 // no router, top-k or combine; the down projection writes outp rows
+                                 // in token order, which are then the output
+    int xprep_ready;             // x16 / xsum / xexp already hold these tokens (a pass before this one)
 };
 
 // Number of pair slots and an upper bound on the GEMM tiles for T tokens.

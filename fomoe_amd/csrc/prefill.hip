@@ -341,7 +341,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     for (int i = tid; i < E * W; i += 1024) bm[i] = 0;
     __syncthreads();
     for (int i = tid; i < a.T * k; i += 1024) {
-        const int t = i / k, e = a.ids[i];
+        const int t = i / k, e = a.one_expert ? 0 : a.ids[i];
         atomicOr(&bm[e * W + (t >> 5)], 1u << (t & 31));
     }
     __syncthreads();
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     if (tid <= E) s_off[tid] = off;
     __syncthreads();
     for (int i = tid; i < a.T * k; i += 1024) {
-        const int t = i / k, r = i - t * k, e = a.ids[i];
+        const int t = i / k, r = i - t * k, e = a.one_expert ? 0 : a.ids[i];
         const uint32_t word = bm[e * W + (t >> 5)];
         const int pos = s_off[e] + (int)pre[e * W + (t >> 5)] + __popc(word & ((1u << (t & 31)) - 1u));
         a.pair_tok[pos] = t;
@@ -1561,11 +1561,14 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         a.max_tiles < prefill_max_tiles(a.T, a.k, a.E, a.shared != nullptr))
         return hipErrorInvalidValue;
     const bool fp16_gateup = a.gate_type == GGML_TYPE_Q4_K && a.up_type == GGML_TYPE_Q4_K;
-    bool xprep_done = false;
-    if (a.H % (64 * kR3Waves) == 0 && a.rsplit) {
+    if (a.one_expert && (a.E != 1 || a.k != 1 || a.shared)) return hipErrorInvalidValue;
+    bool xprep_done = a.xprep_ready != 0;
+    if (a.one_expert) {
+        // no router: the grouping places every token on expert 0
+    } else if (a.H % (64 * kR3Waves) == 0 && a.rsplit) {
         const uint64_t pieces = prefill_router_ws_elems(a.E, a.T, a.H) / 8;   // upper bound
         const unsigned n_rt = (unsigned)std::min<uint64_t>((pieces + 255) / 256, 8192);
-        if (fp16_gateup && a.H % 2048 == 0) {
+        if (fp16_gateup && !xprep_done && a.H % 2048 == 0) {
             k_pf_prep<<<n_rt + (a.T + kXpWaves - 1) / kXpWaves, 256, 0, s>>>(a, n_rt);
             xprep_done = true;
         } else {
@@ -1582,7 +1585,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
         }
         k_pf_router<<<dim3((a.E + kRT - 1) / kRT, (a.T + kRT - 1) / kRT), 256, kRLds, s>>>(a);
     }
-    k_pf_topk<<<(a.T + 3) / 4, 256, 0, s>>>(a);
+    if (!a.one_expert) k_pf_topk<<<(a.T + 3) / 4, 256, 0, s>>>(a);
     static bool lds_attr = false;   // the grouping tables may exceed the 64 KiB default
     if (!lds_attr) {
         hipError_t e = hipFuncSetAttribute((const void *)k_pf_group, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1672,7 +1675,7 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             if (a.thin_down) k_pf_down_thin<<<2 * n_cu, 64 * kPfThinWaves, kPfThinLds, s>>>(a);
         }
     }
-    k_pf_combine<<<dim3(a.T, (a.H + kCombCols - 1) / kCombCols), 256, 0, s>>>(a);
+    if (!a.one_expert) k_pf_combine<<<dim3(a.T, (a.H + kCombCols - 1) / kCombCols), 256, 0, s>>>(a);
     return hipGetLastError();
 }
 
