@@ -356,7 +356,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     constexpr int DT = 2 * kPfMT;
     const int nt = (cnt + kPfMT - 1) / kPfMT;                                 // 64-pair tiles
     // 128-pair tiles of the experts k_pf_down16 runs (dt_sel: all, routed, shared)
-    const bool in_dt = a.dt_sel == 0 || (a.dt_sel == 1 ? tid != E : tid == E);
+    const bool in_dt = a.dt_sel == 0 || tid != E;
     const int dn = in_dt ? (cnt + DT - 1) / DT : 0;
     // The GEMMs take tiles in decreasing cost: entry i's fourth word is the
     // i-th tile by token-block count (4, 3, 2, 1; expert order within a
@@ -1214,8 +1214,25 @@ __global__ __launch_bounds__(64 * kApWaves) void k_pf_actprep_w(PrefillArgs a, i
 // reloads waited for every outstanding load).
 constexpr int kPfD16Waves = 8, kPfD16PerCU = 1;   // waves per work-group (32 rows each), work-groups per CU
 constexpr int kPfD16Tile = 2 * kPfTile;           // activation rows of a double tile (128 pairs) per step
+// A super-block's register image for either down type of a launch (the
+// routed RT, the shared ST), so that one item's loads can be in flight while
+// an item of the other type is multiplied.
+struct PfRaw { uint32_t r[20]; };
+template <int T>
+FO_DEV void pf_load_raw(PfRaw &w, const uint8_t *p, int kg) {
+    const typename PfDec<T>::Sb s = PfDec<T>::load(p, kg);
+    static_assert(sizeof(s) <= sizeof(PfRaw), "super-block image too large");
+    __builtin_memcpy(&w, &s, sizeof(s));
+}
+template <int T>
+FO_DEV typename PfDec<T>::Sb pf_sb(const PfRaw &w) {
+    typename PfDec<T>::Sb s;
+    __builtin_memcpy(&s, &w, sizeof(s));
+    return s;
+}
+
+template <int RT, int ST>   // Q6_K: fp16(q - 32) * fp16(d * sc); Q8_0: fp16(d * q) (one rounding)
 __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) void k_pf_down16(PrefillArgs a) {
-    using D = PfDec<GGML_TYPE_Q6_K>;
     extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x double tile
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), col = lane & 15, kg = lane >> 4;
     // items (double tile of up to 128 pairs of one expert, block of 256
@@ -1228,24 +1245,34 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     // (an expert's tiles are neighbours in that order; down16 HBM reads -15 %
     // against every eighth tile per XCD); its work-groups take its items
     // u = i / 8, + G8, ..., the costliest first
-    const int nt = a.n_tiles[a.thin_down ? 4 : 3], nrb = a.H / (32 * kPfD16Waves);   // thin experts: k_pf_down_thin
+    // thin experts: k_pf_down_thin; the shared expert alone: ceil(T / 128) tiles
+    const int nt = a.d16_shared ? (a.T + 2 * kPfMT - 1) / (2 * kPfMT) : a.n_tiles[a.thin_down ? 4 : 3];
+    const int nrb = a.H / (32 * kPfD16Waves);
     const int x = blockIdx.x & 7, G8 = gridDim.x >> 3;
     const int nrbx = (nrb - x + 7) >> 3, n_u = nt * nrbx;     // row blocks x, x + 8, ... of every tile
-    const uint64_t db = (uint64_t)(a.F / 256) * D::BLOCK;
+    const uint64_t dbR = (uint64_t)(a.F / 256) * PfDec<RT>::BLOCK, dbS = (uint64_t)(a.F / 256) * PfDec<ST>::BLOCK;
     const int NK = a.F / 256;
-    struct Item { int p0, n, row; const uint8_t *drow; bool ok; };
+    struct Item { int p0, n, row; const uint8_t *drow; uint64_t db; bool ok, sh; };
     auto item_at = [&](int u) {
         Item it;
         const int tl = u / nrbx, rbk = x + 8 * (u - tl * nrbx);
         it.ok = u < n_u;
-        const int tile = a.dtiles[4 * (it.ok ? tl : 0) + 3];
-        const int4 t4 = *(const int4 *)(a.dtiles + 4 * tile);
+        int4 t4;
+        if (a.d16_shared) {   // the shared expert's pairs follow the T * k routed ones, in token order
+            const int i = it.ok ? tl : 0;
+            t4 = make_int4(a.E, a.T * a.k + 2 * kPfMT * i, min(2 * kPfMT, a.T - 2 * kPfMT * i), 0);
+        } else {
+            const int tile = a.dtiles[4 * (it.ok ? tl : 0) + 3];
+            t4 = *(const int4 *)(a.dtiles + 4 * tile);
+        }
         const bool shared = t4.x == a.E;
         const uint8_t *blob = shared ? a.shared : a.experts + (uint64_t)t4.x * a.stride;
         const uint64_t down_off = shared ? a.sh_gate_size + a.sh_up_size : a.gate_size + a.up_size;
         it.p0 = t4.y; it.n = t4.z;
         it.row = rbk * (32 * kPfD16Waves) + 32 * wave + col;   // rows row, row + 16
-        it.drow = blob + down_off + (uint64_t)it.row * db;
+        it.sh = shared;
+        it.db = shared ? dbS : dbR;
+        it.drow = blob + down_off + (uint64_t)it.row * it.db;
         return it;
     };
     // a step's activation rows land while the previous step is multiplied:
@@ -1265,7 +1292,26 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     // fp16 operand of chunk ch (values 128n + 32t + 8kg .. +7, scale group
     // 8n + 2t + kg/2) of one super-block
     const f16x2 m1056 = {(_Float16)-1056.f, (_Float16)-1056.f};
-    auto dec = [&](const D::Sb &sb, int ch) {
+    const f16x2 m1152 = {(_Float16)-1152.f, (_Float16)-1152.f};
+    auto dec = [&](auto TC, const auto &sb, int ch) {
+      if constexpr (decltype(TC)::value == GGML_TYPE_Q8_0) {
+        // block ch, codes 8 kg .. 8 kg + 7: byte b ^ 0x80 = q + 128 becomes the
+        // fp16 1024 + q + 128 by a byte permute; minus 1152 is q exactly; times d
+        // (fp16) is the one rounding
+        const uint2 q = sb.q[ch];
+        const uint32_t u0 = q.x ^ 0x80808080u, u1 = q.y ^ 0x80808080u;
+        const uint32_t dh = (sb.d[ch >> 1] >> (16 * (ch & 1))) & 0xFFFFu;
+        const f16x2 d2 = __builtin_bit_cast(f16x2, dh | (dh << 16));
+        const uint32_t pw[4] = {__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u),
+                                __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u),
+                                __builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u),
+                                __builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)};
+        u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            r[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, pw[i]) + m1152) * d2);
+        return __builtin_bit_cast(f16x8, r);
+      } else {
         const int nn = ch >> 2, t = ch & 3;
         const uint2 l = sb.ql[2 * nn + (t & 1)];
         const uint2 h = sb.qh[nn];
@@ -1286,19 +1332,26 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
         for (int i = 0; i < 4; i++)   // (1024 + q) - 1056 = q - 32 exactly, then one rounding
             r[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, pw[i]) + m1056) * ds2);
         return __builtin_bit_cast(f16x8, r);
+      }
     };
     int u = blockIdx.x >> 3;
     Item cur = item_at(u);
     if (!cur.ok) return;
     int gs = 0;                                       // steps done: LDS buffer gs & 1
     stage(cur, 0, 0);
-    D::Sb s0_next = D::load(cur.drow, kg), s1_next = D::load(cur.drow + 16 * db, kg);
+    PfRaw s0_next, s1_next;
+    auto load2 = [&](const Item &it, int kb) {   // the item's two row blocks, super-block kb
+        const uint8_t *p = it.drow + (uint64_t)kb * (it.sh ? PfDec<ST>::BLOCK : PfDec<RT>::BLOCK);
+        if (it.sh) { pf_load_raw<ST>(s0_next, p, kg); pf_load_raw<ST>(s1_next, p + 16 * it.db, kg); }
+        else { pf_load_raw<RT>(s0_next, p, kg); pf_load_raw<RT>(s1_next, p + 16 * it.db, kg); }
+    };
+    load2(cur, 0);
     // the token-block count is a compile-time constant of an item's steps
     // (fewer live registers for small tiles: no spill reloads, whose waits
     // would also wait for the next step's loads); the last step requests the
     // next item's first
-    auto run = [&](auto NBC, const Item &nxt) {
-        constexpr int NB = decltype(NBC)::value;
+    auto run = [&](auto NBC, auto TC, const Item &nxt) {
+        constexpr int NB = decltype(NBC)::value, T = decltype(TC)::value;
         f32x4 acc[2][NB];
 #pragma unroll
         for (int h = 0; h < 2; h++)
@@ -1307,21 +1360,19 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
         for (int kb = 0; kb < NK; kb++) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            const auto s0 = s0_next;
-            const auto s1 = s1_next;
+            const auto s0 = pf_sb<T>(s0_next);
+            const auto s1 = pf_sb<T>(s1_next);
             if (kb + 1 < NK) {
                 stage(cur, kb + 1, (gs + 1) & 1);
-                s0_next = D::load(cur.drow + (uint64_t)(kb + 1) * D::BLOCK, kg);
-                s1_next = D::load(cur.drow + 16 * db + (uint64_t)(kb + 1) * D::BLOCK, kg);
+                load2(cur, kb + 1);
             } else if (nxt.ok) {
                 stage(nxt, 0, (gs + 1) & 1);
-                s0_next = D::load(nxt.drow, kg);
-                s1_next = D::load(nxt.drow + 16 * db, kg);
+                load2(nxt, 0);
             }
             const uint16_t *xh = d16s + (gs & 1) * kPfD16Tile;
 #pragma unroll
             for (int ch = 0; ch < 8; ch++) {
-                const f16x8 b0 = dec(s0, ch), b1 = dec(s1, ch);
+                const f16x8 b0 = dec(TC, s0, ch), b1 = dec(TC, s1, ch);
 #pragma unroll
                 for (int b = 0; b < NB; b++) {
                     const f16x8 av = *(const f16x8 *)(xh + pf_swz(16 * b + col, 4 * ch + kg));
@@ -1348,16 +1399,21 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     for (;;) {
         u += G8;
         const Item nxt = item_at(u);
-        switch ((cur.n + 15) >> 4) {
-            case 1: run(std::integral_constant<int, 1>{}, nxt); break;
-            case 2: run(std::integral_constant<int, 2>{}, nxt); break;
-            case 3: run(std::integral_constant<int, 3>{}, nxt); break;
-            case 4: run(std::integral_constant<int, 4>{}, nxt); break;
-            case 5: run(std::integral_constant<int, 5>{}, nxt); break;
-            case 6: run(std::integral_constant<int, 6>{}, nxt); break;
-            case 7: run(std::integral_constant<int, 7>{}, nxt); break;
-            default: run(std::integral_constant<int, 8>{}, nxt); break;
-        }
+        auto by_nb = [&](auto TC) {
+            switch ((cur.n + 15) >> 4) {
+                case 1: run(std::integral_constant<int, 1>{}, TC, nxt); break;
+                case 2: run(std::integral_constant<int, 2>{}, TC, nxt); break;
+                case 3: run(std::integral_constant<int, 3>{}, TC, nxt); break;
+                case 4: run(std::integral_constant<int, 4>{}, TC, nxt); break;
+                case 5: run(std::integral_constant<int, 5>{}, TC, nxt); break;
+                case 6: run(std::integral_constant<int, 6>{}, TC, nxt); break;
+                case 7: run(std::integral_constant<int, 7>{}, TC, nxt); break;
+                default: run(std::integral_constant<int, 8>{}, TC, nxt); break;
+            }
+        };
+        if constexpr (RT == ST) by_nb(std::integral_constant<int, RT>{});
+        else if (cur.sh) by_nb(std::integral_constant<int, ST>{});
+        else by_nb(std::integral_constant<int, RT>{});
         if (!nxt.ok) break;
         cur = nxt;
     }
@@ -1549,11 +1605,16 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
     // and F as the routed experts) shares the routed gate/up GEMM as expert
     // E; the down projections run per type: bf16-operand launches first
     // (they read the hi/lo activation planes), then the fp16 Q6_K path.
-    auto fp16_down = [&](int t) { return t == GGML_TYPE_Q6_K && a.F <= 4096; };
+    auto fp16_down = [&](int t) { return (t == GGML_TYPE_Q6_K || t == GGML_TYPE_Q8_0) && a.F <= 4096; };
     const int RT = a.down_type, ST = a.sh_down_type;
     const bool sep = a.shared && ST >= 0 && ST != RT;
+    // k_pf_down16 runs one type per launch: the routed experts' (its tile
+    // table, the shared expert left out when its type differs) and then the
+    // shared expert's pairs when its own type takes the fp16 path too
+    const bool rt16 = fp16_down(RT), st16 = sep && fp16_down(ST);
     a.down_sel = 0;
-    a.dt_sel = !sep ? 0 : fp16_down(RT) ? 1 : fp16_down(ST) ? 2 : 0;
+    a.d16_shared = 0;
+    a.dt_sel = sep && !(rt16 && st16) ? 1 : 0;   // both fp16: one launch takes routed and shared tiles
     const bool okt = prefill_types_ok(a.gate_type, a.up_type, a.down_type);
     const int W = (a.T + 31) / 32;
     if (!okt || a.T <= 0 || a.E <= 0 || a.E > 1023 || a.k <= 0 || a.k > a.E || a.k > kMaxK ||
@@ -1652,26 +1713,41 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             else if (type == GGML_TYPE_Q8_0) k_pf_down<GGML_TYPE_Q8_0><<<grid, kPfDownWaves * 64, lds, s>>>(d);
             else k_pf_down<GGML_TYPE_Q6_K><<<grid, kPfDownWaves * 64, lds, s>>>(d);
         };
-        if (!fp16_down(RT)) down_bf16(RT, sep ? 1 : 0);
-        if (sep && !fp16_down(ST)) down_bf16(ST, 2);
-        if (fp16_down(RT) || (sep && fp16_down(ST))) {   // fp16 operands, one activation plane
+        if (!rt16) down_bf16(RT, sep ? 1 : 0);
+        if (sep && !st16) down_bf16(ST, 2);
+        if (rt16 || st16) {   // fp16 operands, one activation plane
             const size_t lds16 = 2 * (size_t)kPfD16Tile * sizeof(uint16_t);   // 128 KiB
             static bool d16_attr = false;
             if (!d16_attr) {
-                hipError_t e = hipFuncSetAttribute((const void *)k_pf_down16,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds16);
-                if (e != hipSuccess) return e;
-                e = hipFuncSetAttribute((const void *)k_pf_down_thin, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)kPfThinLds);
-                if (e != hipSuccess) return e;
+                const void *fns[5] = {(const void *)k_pf_down16<GGML_TYPE_Q6_K, GGML_TYPE_Q6_K>,
+                                      (const void *)k_pf_down16<GGML_TYPE_Q6_K, GGML_TYPE_Q8_0>,
+                                      (const void *)k_pf_down16<GGML_TYPE_Q8_0, GGML_TYPE_Q6_K>,
+                                      (const void *)k_pf_down16<GGML_TYPE_Q8_0, GGML_TYPE_Q8_0>,
+                                      (const void *)k_pf_down_thin};
+                const int sz[5] = {(int)lds16, (int)lds16, (int)lds16, (int)lds16, (int)kPfThinLds};
+                for (int i = 0; i < 5; i++) {
+                    const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, sz[i]);
+                    if (e != hipSuccess) return e;
+                }
                 d16_attr = true;
             }
             const int np = prefill_pairs(a.T, a.k, a.shared != nullptr);
             k_pf_actprep_w<<<(np + kApWaves - 1) / kApWaves, 64 * kApWaves, 0, s>>>(a, np);
-            a.thin_down = fp16_down(RT) && pf_thin_down(a);   // thin routed experts (never the shared one here)
+            a.thin_down = rt16 && pf_thin_down(a);   // thin routed Q6_K experts (never the shared one here)
             int dev = 0, n_cu = 256;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-            k_pf_down16<<<(kPfD16PerCU * n_cu + 7) & ~7, kPfD16Waves * 64, lds16, s>>>(a);   // persistent
+            const unsigned g16 = (kPfD16PerCU * n_cu + 7) & ~7;   // persistent
+            constexpr int Q6 = GGML_TYPE_Q6_K, Q8 = GGML_TYPE_Q8_0;
+            auto down16 = [&](int rt, int st, int shared_only) {
+                PrefillArgs d = a;
+                d.d16_shared = shared_only;
+                if (rt == Q6 && st == Q6) k_pf_down16<Q6, Q6><<<g16, kPfD16Waves * 64, lds16, s>>>(d);
+                else if (rt == Q6) k_pf_down16<Q6, Q8><<<g16, kPfD16Waves * 64, lds16, s>>>(d);
+                else if (st == Q6) k_pf_down16<Q8, Q6><<<g16, kPfD16Waves * 64, lds16, s>>>(d);
+                else k_pf_down16<Q8, Q8><<<g16, kPfD16Waves * 64, lds16, s>>>(d);
+            };
+            if (rt16) down16(RT, st16 ? ST : RT, 0);   // with the shared tiles when their type is fp16 too
+            else if (st16) down16(ST, ST, 1);           // the shared expert alone
             if (a.thin_down) k_pf_down_thin<<<2 * n_cu, 64 * kPfThinWaves, kPfThinLds, s>>>(a);
         }
     }

@@ -573,8 +573,18 @@ static void deq_q6_K_f16ops(const block_q6_K *x, float *y, int64_t nb) {
     }
 }
 
+/* A Q8_0 row as the fp16 operands of the GPU prefill's down projection:
+ * fp16(d * q) (the product exact in fp32, one nearest-even rounding). Value
+ * order as dequantize_row_q8_0 (reference src/quant.c:266-274). */
+static void deq_q8_0_f16ops(const block_q8_0 *x, float *y, int64_t nb) {
+    for (int64_t i = 0; i < nb; i++, y += 32) {
+        const float d = fo_fp16_to_fp32(x[i].d);
+        for (int e = 0; e < 32; e++) y[e] = f16_round(d * (float)x[i].qs[e]);
+    }
+}
+
 /* rows x cols matrix of `type` dequantized exactly, then rounded to bf16
- * when `round` is 1; round 2 (Q6_K only): the fp16 operands above */
+ * when `round` is 1; round 2 (Q6_K, Q8_0): the fp16 operands above */
 static float *deq_bf16(const uint8_t *w, int type, int rows, int cols, int round) {
     float *m = (float *)malloc(sizeof(float) * (size_t)rows * cols);
     const uint64_t rb = fomoe_row_bytes(type, cols);
@@ -583,6 +593,10 @@ static float *deq_bf16(const uint8_t *w, int type, int rows, int cols, int round
         float *y = m + (size_t)r * cols;
         if (round == 2 && type == GGML_TYPE_Q6_K) {
             deq_q6_K_f16ops((const block_q6_K *)(w + (uint64_t)r * rb), y, cols / QK_K);
+            continue;
+        }
+        if (round == 2 && type == GGML_TYPE_Q8_0) {
+            deq_q8_0_f16ops((const block_q8_0 *)(w + (uint64_t)r * rb), y, cols / 32);
             continue;
         }
         fo_dequantize_row(type, w + (uint64_t)r * rb, y, cols);
@@ -620,15 +634,16 @@ static void matvec_f64(float *out, const float *m, const float *v, int rows, int
 }
 
 /* bf16_mask: bit 0 gate, bit 1 up, bit 2 down weights rounded to bf16;
- * bit 3: a Q6_K down projection on fp16 operands (deq_q6_K_f16ops weights,
- * act_f16 activation) instead; bit 4: bits 0-3 chosen per expert from its
- * types as the GPU prefill does (exact Q4_K/Q4_K gate/up, else bf16; fp16
- * operands for a Q6_K down projection with F <= 4096, else bf16) */
+ * bit 3: a Q6_K or Q8_0 down projection on fp16 operands (deq_*_f16ops
+ * weights, act_f16 activation) instead; bit 4: bits 0-3 chosen per expert
+ * from its types as the GPU prefill does (exact Q4_K/Q4_K gate/up, else
+ * bf16; fp16 operands for a Q6_K or Q8_0 down projection with F <= 4096,
+ * else bf16) */
 static void expert_ffn_bf16(const uint8_t *blob, int gt, int ut, int dt, int H, int F, uint64_t gs, uint64_t us,
                             const float *x, float *out, int bf16_mask) {
     if (bf16_mask & 16)
         bf16_mask = ((gt == GGML_TYPE_Q4_K && ut == GGML_TYPE_Q4_K) ? 0 : 3) |
-                    ((dt == GGML_TYPE_Q6_K && F <= 4096) ? 8 : 4);
+                    (((dt == GGML_TYPE_Q6_K || dt == GGML_TYPE_Q8_0) && F <= 4096) ? 8 : 4);
     float *g = (float *)malloc(sizeof(float) * (size_t)F * 2), *u = g + F;
     float *wg = deq_bf16(blob, gt, F, H, (bf16_mask & 1) ? 1 : 0);
     matvec_f64(g, wg, x, F, H);
@@ -637,7 +652,7 @@ static void expert_ffn_bf16(const uint8_t *blob, int gt, int ut, int dt, int H, 
     matvec_f64(u, wu, x, F, H);
     free(wu);
     for (int i = 0; i < F; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
-    const int f16 = (bf16_mask & 8) && dt == GGML_TYPE_Q6_K;
+    const int f16 = (bf16_mask & 8) && (dt == GGML_TYPE_Q6_K || dt == GGML_TYPE_Q8_0);
     const int s = f16 ? act_f16(g, F) : 0;
     float *wd = deq_bf16(blob + gs + us, dt, H, F, f16 ? 2 : (bf16_mask & 4) ? 1 : 0);
     matvec_f64(out, wd, g, H, F);
