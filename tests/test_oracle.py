@@ -487,6 +487,49 @@ def test_prefill_oracle_fp64_recomposition(mask):
         assert parity_err(out[i], xt + ref) < (1e-4 if mask & 8 else 1e-5)
 
 
+def _q8_0_f16_operands(blob, rows, cols):
+    """Q8_0 rows as the fp16 down operands: fp16(d * q), the product rounded
+    once; block layout of reference src/quant.c:266-274 (fp16 d, 32 int8),
+    parsed here independently of the oracle's C code."""
+    b = np.frombuffer(blob, np.uint8).reshape(-1, 34)
+    d = b[:, :2].copy().view(np.float16).astype(np.float32)[:, 0]
+    q = b[:, 2:].view(np.int8).astype(np.float32)
+    return (d[:, None] * q).astype(np.float16).astype(np.float32).reshape(rows, cols)
+
+
+def test_prefill_oracle_q8_0_fp16_down():
+    """Prefill oracle with a Q8_0 down projection on fp16 operands (mask 8,
+    and the per-expert rule of mask 16) = numpy recomposition: exact Q4_K
+    gate/up, fp16(d * q) down weights, the activation as fp16 under its row's
+    power of two; one token's rows by hand."""
+    E, k, H, F, T = 6, 2, 256, 256, 3
+    router = O.synth_f32(44, 0, 0.02, E * H)
+    gs, ds = O.row_bytes(O.Q4_K, H) * F, O.row_bytes(O.Q8_0, F) * H
+    stride = 2 * gs + ds
+    experts = np.concatenate([np.concatenate([O.synth_quant(O.Q4_K, 45, 3 * e, 0.02, F, H),
+                                              O.synth_quant(O.Q4_K, 45, 3 * e + 1, 0.02, F, H),
+                                              O.synth_quant(O.Q8_0, 45, 3 * e + 2, 0.02, H, F)]) for e in range(E)])
+    x = O.to_bf16(O.synth_f32(46, 0, 1.0, T * H)).reshape(T, H)
+    d = moe_desc(E, k, H, F, router, experts, gs, ds)
+    d.down_type = O.Q8_0
+    for mask in (8, 16):
+        out, ids, w = O.moe_prefill(d, x, 0, T, 0, bf16_mask=mask)
+        for t in range(T):
+            xt = O.bf16_to_f32(x[t]).astype(np.float64)
+            ref = np.zeros(H)
+            for j in range(k):
+                e = experts[int(ids[t, j]) * stride:(int(ids[t, j]) + 1) * stride]
+                G = O.dequantize(O.Q4_K, e[:gs], F * H).reshape(F, H).astype(np.float64)
+                U = O.dequantize(O.Q4_K, e[gs:2 * gs], F * H).reshape(F, H).astype(np.float64)
+                g, u = (G @ xt).astype(np.float32), (U @ xt).astype(np.float32)
+                a16, sx = _act_f16((g / (1 + np.exp(-g))) * u)
+                D = _q8_0_f16_operands(e[2 * gs:], H, F).astype(np.float64)
+                ref += float(w[t, j]) * np.ldexp(D @ a16, sx)
+            # an fp32 SwiGLU value one ulp apart (numpy vs C expf) can round to
+            # the neighbouring fp16, 2^-11 of one term
+            assert parity_err(out[t], ref) < 1e-4, (mask, t)
+
+
 def test_prefill_oracle_close_to_fp32_layer():
     """bf16 weights/activations move the prefill output by ~1e-3 of its scale
     from the fp32 decode oracle on the same (bf16) input; routing identical."""
