@@ -1245,8 +1245,10 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     // (an expert's tiles are neighbours in that order; down16 HBM reads -15 %
     // against every eighth tile per XCD); its work-groups take its items
     // u = i / 8, + G8, ..., the costliest first
-    // thin experts: k_pf_down_thin; the shared expert alone: ceil(T / 128) tiles
-    const int nt = a.d16_shared ? (a.T + 2 * kPfMT - 1) / (2 * kPfMT) : a.n_tiles[a.thin_down ? 4 : 3];
+    // thin experts: k_pf_down_thin; the shared expert alone: tiles of 32
+    // pairs, so that its items (16 row blocks each) reach every work-group
+    constexpr int kShTile = 32;
+    const int nt = a.d16_shared ? (a.T + kShTile - 1) / kShTile : a.n_tiles[a.thin_down ? 4 : 3];
     const int nrb = a.H / (32 * kPfD16Waves);
     const int x = blockIdx.x & 7, G8 = gridDim.x >> 3;
     const int nrbx = (nrb - x + 7) >> 3, n_u = nt * nrbx;     // row blocks x, x + 8, ... of every tile
@@ -1260,7 +1262,7 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
         int4 t4;
         if (a.d16_shared) {   // the shared expert's pairs follow the T * k routed ones, in token order
             const int i = it.ok ? tl : 0;
-            t4 = make_int4(a.E, a.T * a.k + 2 * kPfMT * i, min(2 * kPfMT, a.T - 2 * kPfMT * i), 0);
+            t4 = make_int4(a.E, a.T * a.k + kShTile * i, min(kShTile, a.T - kShTile * i), 0);
         } else {
             const int tile = a.dtiles[4 * (it.ok ? tl : 0) + 3];
             t4 = *(const int4 *)(a.dtiles + 4 * tile);
