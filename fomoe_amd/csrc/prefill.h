@@ -60,8 +60,9 @@ struct PrefillArgs {
     int down_sel;                // set by launch_prefill: 0 every expert's down projection, 1 the
                                  // routed experts' only, 2 the shared expert's only
     int dt_sel;                  // set by launch_prefill: 1 leaves the shared expert out of dtiles
-    int d16_shared;              // set by launch_prefill: k_pf_down16 runs the shared expert's pairs
-                                 // (T*k .. T*k + T, in token order) instead of dtiles
+    int d16_shared;              // set by launch_prefill: k_pf_down16 runs one expert's T pairs in
+                                 // token order (the shared expert's, T*k .. T*k + T, or a one-expert
+                                 // pass's) in 32-pair tiles instead of dtiles
     int one_expert;              // every token to expert 0 at weight 1 (E = k = 1, no shared expert):
                                  // no router, top-k or combine; the down projection writes outp rows
                                  // in token order, which are then the output

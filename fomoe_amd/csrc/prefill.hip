@@ -48,6 +48,8 @@
 namespace fo {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -589,6 +591,37 @@ template <> struct PfDec<GGML_TYPE_Q8_0> {
     }
 };
 
+// Eight values of chunk ch (lane group kg) of a Q4_K or Q5_K super-block as
+// fp16 operands: the exact fp32 dequantized value d1 * q - m1 (the product is
+// exact, one rounding for the difference, as the reference's dequantization)
+// rounded once more to fp16 (nearest even).
+template <int T>
+FO_DEV f16x8 pf_decode_f16_k(const typename PfDec<T>::Sb &s, int ch) {
+    const uint32_t sc4[3] = {s.hdr.y, s.hdr.z, s.hdr.w};
+    const int j = ch;
+    auto byte = [&](int i) -> uint32_t { return (sc4[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
+    uint32_t sc, mn;
+    if (j < 4) { sc = byte(j) & 63; mn = byte(j + 4) & 63; }
+    else {
+        sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
+        mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+    const float d1 = h2f(s.hdr.x) * (float)sc, m1 = h2f(s.hdr.x >> 16) * (float)mn;
+    const uint2 q = s.q[ch >> 1];
+    const int sh = 4 * (ch & 1);
+    uint32_t w0 = (q.x >> sh) & 0x0F0F0F0Fu, w1 = (q.y >> sh) & 0x0F0F0F0Fu;
+    if constexpr (T == GGML_TYPE_Q5_K) {
+        w0 |= ((s.qh.x >> ch) & 0x01010101u) << 4;
+        w1 |= ((s.qh.y >> ch) & 0x01010101u) << 4;
+    }
+    f16x8 r;
+    r[0] = (_Float16)fmaf(d1, ub0(w0), -m1); r[1] = (_Float16)fmaf(d1, ub1(w0), -m1);
+    r[2] = (_Float16)fmaf(d1, ub2(w0), -m1); r[3] = (_Float16)fmaf(d1, ub3(w0), -m1);
+    r[4] = (_Float16)fmaf(d1, ub0(w1), -m1); r[5] = (_Float16)fmaf(d1, ub1(w1), -m1);
+    r[6] = (_Float16)fmaf(d1, ub2(w1), -m1); r[7] = (_Float16)fmaf(d1, ub3(w1), -m1);
+    return r;
+}
+
 template <int T>
 FO_DEV u32x4 pf_decode(const typename PfDec<T>::Sb &s, int ch, int kg) {
     if constexpr (T == GGML_TYPE_Q4_K) return PfDec<T>::decode(s, ch);
@@ -781,8 +814,6 @@ __global__ __launch_bounds__(kPfGateWaves * 64, 4) void k_pf_gateup(PrefillArgs 
 // 74 KiB of LDS and <= 128 VGPRs: two work-groups share a CU, and the loads
 // of one overlap the arithmetic of the other. Work-groups take items from a
 // counter (reset by k_pf_group).
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 constexpr int kWsWaves = 8;
 constexpr int kWsRows = 16 * kWsWaves;                // F rows per item
 
@@ -1231,7 +1262,7 @@ FO_DEV typename PfDec<T>::Sb pf_sb(const PfRaw &w) {
     return s;
 }
 
-template <int RT, int ST>   // Q6_K: fp16(q - 32) * fp16(d * sc); Q8_0: fp16(d * q) (one rounding)
+template <int RT, int ST>   // Q6_K: fp16(q - 32) * fp16(d * sc); Q8_0: fp16(d * q); Q4_K / Q5_K: fp16(exact value)
 __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) void k_pf_down16(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t d16s[];   // 2 buffers x double tile
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), col = lane & 15, kg = lane >> 4;
@@ -1260,9 +1291,11 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
         const int tl = u / nrbx, rbk = x + 8 * (u - tl * nrbx);
         it.ok = u < n_u;
         int4 t4;
-        if (a.d16_shared) {   // the shared expert's pairs follow the T * k routed ones, in token order
+        if (a.d16_shared) {   // one expert's T pairs in token order: the shared expert's follow the
+                              // T * k routed ones; a one-expert pass's are all of them
             const int i = it.ok ? tl : 0;
-            t4 = make_int4(a.E, a.T * a.k + kShTile * i, min(kShTile, a.T - kShTile * i), 0);
+            const int e0 = a.one_expert ? 0 : a.E, base = a.one_expert ? 0 : a.T * a.k;
+            t4 = make_int4(e0, base + kShTile * i, min(kShTile, a.T - kShTile * i), 0);
         } else {
             const int tile = a.dtiles[4 * (it.ok ? tl : 0) + 3];
             t4 = *(const int4 *)(a.dtiles + 4 * tile);
@@ -1296,7 +1329,9 @@ __global__ __launch_bounds__(kPfD16Waves * 64, kPfD16PerCU * kPfD16Waves / 4) vo
     const f16x2 m1056 = {(_Float16)-1056.f, (_Float16)-1056.f};
     const f16x2 m1152 = {(_Float16)-1152.f, (_Float16)-1152.f};
     auto dec = [&](auto TC, const auto &sb, int ch) {
-      if constexpr (decltype(TC)::value == GGML_TYPE_Q8_0) {
+      if constexpr (decltype(TC)::value == GGML_TYPE_Q4_K || decltype(TC)::value == GGML_TYPE_Q5_K) {
+        return pf_decode_f16_k<decltype(TC)::value>(sb, ch);
+      } else if constexpr (decltype(TC)::value == GGML_TYPE_Q8_0) {
         // block ch, codes 8 kg .. 8 kg + 7: byte b ^ 0x80 = q + 128 becomes the
         // fp16 1024 + q + 128 by a byte permute; minus 1152 is q exactly; times d
         // (fp16) is the one rounding
@@ -1601,22 +1636,34 @@ static hipError_t launch_gateup_t(const PrefillArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// The k_pf_down16 type pairs built: each down type alone, and a shared Q6_K
+// or Q8_0 down projection beside any routed type.
+#define FO_D16_ALL \
+    FO_D16(GGML_TYPE_Q4_K, GGML_TYPE_Q4_K) FO_D16(GGML_TYPE_Q5_K, GGML_TYPE_Q5_K) \
+    FO_D16(GGML_TYPE_Q6_K, GGML_TYPE_Q6_K) FO_D16(GGML_TYPE_Q8_0, GGML_TYPE_Q8_0) \
+    FO_D16(GGML_TYPE_Q4_K, GGML_TYPE_Q6_K) FO_D16(GGML_TYPE_Q4_K, GGML_TYPE_Q8_0) \
+    FO_D16(GGML_TYPE_Q5_K, GGML_TYPE_Q6_K) FO_D16(GGML_TYPE_Q5_K, GGML_TYPE_Q8_0) \
+    FO_D16(GGML_TYPE_Q6_K, GGML_TYPE_Q8_0) FO_D16(GGML_TYPE_Q8_0, GGML_TYPE_Q6_K)
+
 hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
     PrefillArgs a = a_;
     // A shared expert whose down projection has a type of its own (gate/up
     // and F as the routed experts) shares the routed gate/up GEMM as expert
     // E; the down projections run per type: bf16-operand launches first
     // (they read the hi/lo activation planes), then the fp16 Q6_K path.
-    auto fp16_down = [&](int t) { return (t == GGML_TYPE_Q6_K || t == GGML_TYPE_Q8_0) && a.F <= 4096; };
+    auto fp16_down = [&](int t) { (void)t; return a.F <= 4096; };   // every down type of the prefill
     const int RT = a.down_type, ST = a.sh_down_type;
     const bool sep = a.shared && ST >= 0 && ST != RT;
     // k_pf_down16 runs one type per launch: the routed experts' (its tile
     // table, the shared expert left out when its type differs) and then the
     // shared expert's pairs when its own type takes the fp16 path too
     const bool rt16 = fp16_down(RT), st16 = sep && fp16_down(ST);
+    // one launch takes routed and shared tiles when its type pair is built
+    // (a shared Q6_K or Q8_0 down beside any routed type)
+    const bool joint = rt16 && st16 && (ST == GGML_TYPE_Q6_K || ST == GGML_TYPE_Q8_0);
     a.down_sel = 0;
     a.d16_shared = 0;
-    a.dt_sel = sep && !(rt16 && st16) ? 1 : 0;   // both fp16: one launch takes routed and shared tiles
+    a.dt_sel = sep && !joint ? 1 : 0;
     const bool okt = prefill_types_ok(a.gate_type, a.up_type, a.down_type);
     const int W = (a.T + 31) / 32;
     if (!okt || a.T <= 0 || a.E <= 0 || a.E > 1023 || a.k <= 0 || a.k > a.E || a.k > kMaxK ||
@@ -1721,16 +1768,13 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             const size_t lds16 = 2 * (size_t)kPfD16Tile * sizeof(uint16_t);   // 128 KiB
             static bool d16_attr = false;
             if (!d16_attr) {
-                const void *fns[5] = {(const void *)k_pf_down16<GGML_TYPE_Q6_K, GGML_TYPE_Q6_K>,
-                                      (const void *)k_pf_down16<GGML_TYPE_Q6_K, GGML_TYPE_Q8_0>,
-                                      (const void *)k_pf_down16<GGML_TYPE_Q8_0, GGML_TYPE_Q6_K>,
-                                      (const void *)k_pf_down16<GGML_TYPE_Q8_0, GGML_TYPE_Q8_0>,
-                                      (const void *)k_pf_down_thin};
-                const int sz[5] = {(int)lds16, (int)lds16, (int)lds16, (int)lds16, (int)kPfThinLds};
-                for (int i = 0; i < 5; i++) {
-                    const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, sz[i]);
-                    if (e != hipSuccess) return e;
-                }
+#define FO_D16(R, S) \
+                if (hipFuncSetAttribute((const void *)k_pf_down16<R, S>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                        (int)lds16) != hipSuccess) return hipErrorInvalidValue;
+                FO_D16_ALL
+#undef FO_D16
+                if (hipFuncSetAttribute((const void *)k_pf_down_thin, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)kPfThinLds) != hipSuccess) return hipErrorInvalidValue;
                 d16_attr = true;
             }
             const int np = prefill_pairs(a.T, a.k, a.shared != nullptr);
@@ -1739,17 +1783,15 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
             int dev = 0, n_cu = 256;
             if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
             const unsigned g16 = (kPfD16PerCU * n_cu + 7) & ~7;   // persistent
-            constexpr int Q6 = GGML_TYPE_Q6_K, Q8 = GGML_TYPE_Q8_0;
             auto down16 = [&](int rt, int st, int shared_only) {
                 PrefillArgs d = a;
                 d.d16_shared = shared_only;
-                if (rt == Q6 && st == Q6) k_pf_down16<Q6, Q6><<<g16, kPfD16Waves * 64, lds16, s>>>(d);
-                else if (rt == Q6) k_pf_down16<Q6, Q8><<<g16, kPfD16Waves * 64, lds16, s>>>(d);
-                else if (st == Q6) k_pf_down16<Q8, Q6><<<g16, kPfD16Waves * 64, lds16, s>>>(d);
-                else k_pf_down16<Q8, Q8><<<g16, kPfD16Waves * 64, lds16, s>>>(d);
+#define FO_D16(R, S) if (rt == R && st == S) { k_pf_down16<R, S><<<g16, kPfD16Waves * 64, lds16, s>>>(d); return; }
+                FO_D16_ALL
+#undef FO_D16
             };
-            if (rt16) down16(RT, st16 ? ST : RT, 0);   // with the shared tiles when their type is fp16 too
-            else if (st16) down16(ST, ST, 1);           // the shared expert alone
+            if (rt16) down16(RT, joint ? ST : RT, a.one_expert);   // (one expert: its pairs in 32-pair tiles)
+            if (st16 && !joint) down16(ST, ST, 1);      // the shared expert alone
             if (a.thin_down) k_pf_down_thin<<<2 * n_cu, 64 * kPfThinWaves, kPfThinLds, s>>>(a);
         }
     }

@@ -195,7 +195,9 @@ def bf16_to_f32(b: np.ndarray) -> np.ndarray:
 
 def moe_prefill(desc: MoeDesc, x_bf16: np.ndarray, t0: int, nt: int, flags: int = 0, bf16_mask: int = 7):
     """Oracle prefill for tokens t0..t0+nt-1 of x_bf16 [T x H] (uint16 bits);
-    bf16_mask picks the weight matrices rounded to bf16 (1 gate, 2 up, 4 down)."""
+    bf16_mask picks the weight matrices rounded to bf16 (1 gate, 2 up, 4 down);
+    8: the down projection on the GPU prefill's fp16 operands instead; 16: the
+    choice per expert from its own types, as the GPU prefill makes it."""
     x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
     H, k = desc.n_embd, desc.k
     out = np.empty((nt, H), np.float32)

@@ -584,7 +584,9 @@ static void deq_q8_0_f16ops(const block_q8_0 *x, float *y, int64_t nb) {
 }
 
 /* rows x cols matrix of `type` dequantized exactly, then rounded to bf16
- * when `round` is 1; round 2 (Q6_K, Q8_0): the fp16 operands above */
+ * when `round` is 1; round 2: the fp16 operands of the GPU prefill's down
+ * projection (Q6_K, Q8_0 as above; other types the exact value rounded to
+ * fp16) */
 static float *deq_bf16(const uint8_t *w, int type, int rows, int cols, int round) {
     float *m = (float *)malloc(sizeof(float) * (size_t)rows * cols);
     const uint64_t rb = fomoe_row_bytes(type, cols);
@@ -600,7 +602,9 @@ static float *deq_bf16(const uint8_t *w, int type, int rows, int cols, int round
             continue;
         }
         fo_dequantize_row(type, w + (uint64_t)r * rb, y, cols);
-        if (round)
+        if (round == 2)   /* Q4_K, Q5_K: the exact value rounded once to fp16 */
+            for (int c = 0; c < cols; c++) y[c] = f16_round(y[c]);
+        else if (round)
             for (int c = 0; c < cols; c++) y[c] = fo_bf16_to_fp32(fo_fp32_to_bf16(y[c]));
     }
     return m;
@@ -634,16 +638,15 @@ static void matvec_f64(float *out, const float *m, const float *v, int rows, int
 }
 
 /* bf16_mask: bit 0 gate, bit 1 up, bit 2 down weights rounded to bf16;
- * bit 3: a Q6_K or Q8_0 down projection on fp16 operands (deq_*_f16ops
- * weights, act_f16 activation) instead; bit 4: bits 0-3 chosen per expert
- * from its types as the GPU prefill does (exact Q4_K/Q4_K gate/up, else
- * bf16; fp16 operands for a Q6_K or Q8_0 down projection with F <= 4096,
- * else bf16) */
+ * bit 3: the down projection on fp16 operands (deq_bf16 round 2 weights,
+ * act_f16 activation) instead; bit 4: bits 0-3 chosen per expert from its
+ * types as the GPU prefill does (exact Q4_K/Q4_K gate/up, else bf16; fp16
+ * operands for the down projection with F <= 4096, else bf16) */
 static void expert_ffn_bf16(const uint8_t *blob, int gt, int ut, int dt, int H, int F, uint64_t gs, uint64_t us,
                             const float *x, float *out, int bf16_mask) {
     if (bf16_mask & 16)
         bf16_mask = ((gt == GGML_TYPE_Q4_K && ut == GGML_TYPE_Q4_K) ? 0 : 3) |
-                    (((dt == GGML_TYPE_Q6_K || dt == GGML_TYPE_Q8_0) && F <= 4096) ? 8 : 4);
+                    (F <= 4096 ? 8 : 4);
     float *g = (float *)malloc(sizeof(float) * (size_t)F * 2), *u = g + F;
     float *wg = deq_bf16(blob, gt, F, H, (bf16_mask & 1) ? 1 : 0);
     matvec_f64(g, wg, x, F, H);
@@ -652,7 +655,7 @@ static void expert_ffn_bf16(const uint8_t *blob, int gt, int ut, int dt, int H, 
     matvec_f64(u, wu, x, F, H);
     free(wu);
     for (int i = 0; i < F; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
-    const int f16 = (bf16_mask & 8) && (dt == GGML_TYPE_Q6_K || dt == GGML_TYPE_Q8_0);
+    const int f16 = (bf16_mask & 8) != 0;
     const int s = f16 ? act_f16(g, F) : 0;
     float *wd = deq_bf16(blob + gs + us, dt, H, F, f16 ? 2 : (bf16_mask & 4) ? 1 : 0);
     matvec_f64(out, wd, g, H, F);

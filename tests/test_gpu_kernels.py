@@ -887,11 +887,10 @@ def pf_check(got, d, x, t0, shape, flags=0, tokens=None):
 def pf_bf16_mask(shape):
     """The prefill path's operand rounding, as the oracle's bf16_mask: Q4_K
     gate/up run with exact weights, other gate/up types are dequantized to
-    bf16; a Q6_K or Q8_0 down projection runs on fp16 operands (8), other
-    down types on bf16 weights (4)."""
+    bf16; the down projection runs on fp16 operands (8) for F <= 4096, on
+    bf16 weights (4) above."""
     q4 = shape.gate_type == O.Q4_K
-    f16 = shape.down_type in (O.Q6_K, O.Q8_0) and shape.inter <= 4096
-    return (0 if q4 else 3) | (8 if f16 else 4)
+    return (0 if q4 else 3) | (8 if shape.inter <= 4096 else 4)
 
 
 @pytest.mark.parametrize("T,shared,gate_vec,resid,H", [(200, True, True, True, 512), (1, True, False, False, 512),

@@ -497,21 +497,23 @@ def _q8_0_f16_operands(blob, rows, cols):
     return (d[:, None] * q).astype(np.float16).astype(np.float32).reshape(rows, cols)
 
 
-def test_prefill_oracle_q8_0_fp16_down():
-    """Prefill oracle with a Q8_0 down projection on fp16 operands (mask 8,
-    and the per-expert rule of mask 16) = numpy recomposition: exact Q4_K
-    gate/up, fp16(d * q) down weights, the activation as fp16 under its row's
-    power of two; one token's rows by hand."""
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_K, O.Q5_K])
+def test_prefill_oracle_fp16_down_types(dt):
+    """Prefill oracle with a Q8_0 / Q4_K / Q5_K down projection on fp16
+    operands (mask 8, and the per-expert rule of mask 16) = numpy
+    recomposition: exact Q4_K gate/up; down weights fp16(d * q) (Q8_0, parsed
+    here) or the exact dequantized value rounded to fp16 (Q4_K, Q5_K); the
+    activation as fp16 under its row's power of two."""
     E, k, H, F, T = 6, 2, 256, 256, 3
     router = O.synth_f32(44, 0, 0.02, E * H)
-    gs, ds = O.row_bytes(O.Q4_K, H) * F, O.row_bytes(O.Q8_0, F) * H
+    gs, ds = O.row_bytes(O.Q4_K, H) * F, O.row_bytes(dt, F) * H
     stride = 2 * gs + ds
     experts = np.concatenate([np.concatenate([O.synth_quant(O.Q4_K, 45, 3 * e, 0.02, F, H),
                                               O.synth_quant(O.Q4_K, 45, 3 * e + 1, 0.02, F, H),
-                                              O.synth_quant(O.Q8_0, 45, 3 * e + 2, 0.02, H, F)]) for e in range(E)])
+                                              O.synth_quant(dt, 45, 3 * e + 2, 0.02, H, F)]) for e in range(E)])
     x = O.to_bf16(O.synth_f32(46, 0, 1.0, T * H)).reshape(T, H)
     d = moe_desc(E, k, H, F, router, experts, gs, ds)
-    d.down_type = O.Q8_0
+    d.down_type = dt
     for mask in (8, 16):
         out, ids, w = O.moe_prefill(d, x, 0, T, 0, bf16_mask=mask)
         for t in range(T):
@@ -523,7 +525,10 @@ def test_prefill_oracle_q8_0_fp16_down():
                 U = O.dequantize(O.Q4_K, e[gs:2 * gs], F * H).reshape(F, H).astype(np.float64)
                 g, u = (G @ xt).astype(np.float32), (U @ xt).astype(np.float32)
                 a16, sx = _act_f16((g / (1 + np.exp(-g))) * u)
-                D = _q8_0_f16_operands(e[2 * gs:], H, F).astype(np.float64)
+                if dt == O.Q8_0:
+                    D = _q8_0_f16_operands(e[2 * gs:], H, F).astype(np.float64)
+                else:
+                    D = O.dequantize(dt, e[2 * gs:], H * F).reshape(H, F).astype(np.float16).astype(np.float64)
                 ref += float(w[t, j]) * np.ldexp(D @ a16, sx)
             # an fp32 SwiGLU value one ulp apart (numpy vs C expf) can round to
             # the neighbouring fp16, 2^-11 of one term
