@@ -454,6 +454,18 @@ def prefill_config5(gpu, layer, shape, reps):
             gpu.moe_prefill(d, x, T, out, 0)
         shexp[f"config5_shexp_{name}_ms"] = round(gpu.timer_stop() / reps, 4)
         del bl
+    # the same tokens through a layer whose routed down projections are Q5_K
+    # (as in part of the real model's layers)
+    s5 = S.LayerShape(down_type=FA.Q5_K)
+    L5 = S.build_layer(gpu, s5, 1, seed=4, zipf_s=1.1, norm=False)
+    for _ in range(10):
+        gpu.moe_prefill(L5.desc, x, T, out, 0)
+    gpu.sync()
+    gpu.timer_start()
+    for _ in range(reps):
+        gpu.moe_prefill(L5.desc, x, T, out, 0)
+    shexp["config5_q5k_down_ms"] = round(gpu.timer_stop() / reps, 4)
+    del L5
     return {**sp5, **shexp, "config5_ms": round(ms, 4),
             "config5_tok_per_s": round(T / (ms / 1e3), 1),
             "config5_experts_touched": n_unique, "config5_weight_bytes": wbytes,
