@@ -343,16 +343,23 @@ static int enqueue_layer_fast(gpu_ctx_t *ctx, const LayerScratch &sc, const gpu_
                  sc.xq_h, gsz_of(L->gate_type), L->shared_gate_vec, L->shared ? shared_w : nullptr};
     HIPC(launch_route(ra, ctx->stream));
     if (mode == kSharedOwn) HIPC(launch_shared(shared_args(sc, L, nullptr), in, norm_w, L->eps, ctx->stream));
-    ExpandArgs ea{sc.logits, L->n_experts, L->k, sc.ids, sc.weights, base, L->expert_stride,
-                  L->gate_size, sh2, L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H),
-                  sc.xq_h, sc.xq_act, xs, dg, mode == kSharedDownOnly ? sc.act : nullptr};
-    HIPC(launch_expand(L->gate_type, ea, ctx->stream, ctx->n_cu));
     const bool fused = mode == kSharedFused;
     ReduceArgs da{sc.ids, sc.weights, L->shared ? shared_w : nullptr, L->k, base, L->expert_stride,
                   L->gate_size + L->up_size, fused ? sh : nullptr, L->shared_gate_size + L->shared_up_size, F, H,
                   fomoe_row_bytes(L->down_type, F), sc.xq_act, xs,
                   (flags & GPU_MOE_RESIDUAL) ? in : nullptr, out, mode == kSharedOwn ? sc.sh_ys : nullptr,
-                  -1, nullptr};
+                  -1, nullptr, nullptr};
+    // a down projection with activation groups of 32 (Q4_K, Q5_K) beside Q4_K
+    // gate/up at H = 4096: the 16-row gate/up kernel leaves fp32 activations
+    // and the down kernel prepares its groups from them
+    const bool f32act = dg == 32 && L->gate_type == GGML_TYPE_Q4_K && H == 4096 &&
+                        reduce_takes_tile(L->down_type, da);
+    ExpandArgs ea{sc.logits, L->n_experts, L->k, sc.ids, sc.weights, base, L->expert_stride,
+                  L->gate_size, sh2, L->shared_gate_size, F, H, fomoe_row_bytes(L->gate_type, H),
+                  sc.xq_h, sc.xq_act, xs, dg, (mode == kSharedDownOnly || f32act) ? sc.act : nullptr,
+                  f32act ? 1 : 0};
+    HIPC(launch_expand(L->gate_type, ea, ctx->stream, ctx->n_cu));
+    if (f32act) da.act_f32 = sc.act;
     if (mode == kSharedDownOnly) {
         const int sdt = L->shared_down_type;
         if (reduce_takes_shared_type(L->down_type, da, sdt)) {   // one more block in k_reduce_tile

@@ -44,6 +44,8 @@ struct ExpandArgs {
     uint64_t xq_vstride;
     int down_gsz;
     float *act;
+    int act_only;           // 1: leave xq_act unwritten, act (non-NULL) is the down
+                            // kernel's input (ReduceArgs::act_f32)
 };
 
 // K3: out[i] = (resid ? resid[i] : 0) + sum_e w_e * down_e[i,:] . act_e over
@@ -70,11 +72,16 @@ struct ReduceArgs {
     int sh_type;            // -1: the shared block has the routed down type; else its own
                             // type (F = 1024, reduce_takes_shared_type), from sh_act
     const float *sh_act;    // [F] fp32 shared activation (sh_type >= 0)
+    const float *act_f32;   // NULL, or [n_tot x F] fp32 activations, each wave preparing its slot from
+                            // them (bit-identical to xq_act's form; the LDS-staged kernel only)
 };
 
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
 hipError_t launch_expand(int gate_type, const ExpandArgs &a, hipStream_t s, int n_cu);
 hipError_t launch_reduce(int down_type, const ReduceArgs &a, hipStream_t s, int n_cu);
+// Whether launch_reduce takes the LDS-staged kernel (the one that can
+// prepare its slots from fp32 activations) for this shape.
+bool reduce_takes_tile(int down_type, const ReduceArgs &a);
 // Whether launch_reduce runs a shared block of type sh_type beside routed
 // down projections of down_type for this shape.
 bool reduce_takes_shared_type(int down_type, const ReduceArgs &a, int sh_type);

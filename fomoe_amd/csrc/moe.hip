@@ -384,8 +384,10 @@ __global__ __launch_bounds__(256, 3) void k_expand_q4t(ExpandArgs a) {
     __syncthreads();
     if (wv == 0) {
         const float val = lane < TR ? s_act[lane] : 0.f;
-        uint8_t *dst = a.xq_act + (uint64_t)e * a.xq_vstride;
-        prep_group_lanes<TR>(val, rb, dst, dst + xq_limb_bytes(F_));
+        if (!a.act_only) {   // else the down kernel prepares its groups from act
+            uint8_t *dst = a.xq_act + (uint64_t)e * a.xq_vstride;
+            prep_group_lanes<TR>(val, rb, dst, dst + xq_limb_bytes(F_));
+        }
         if (a.act && lane < TR) a.act[(uint64_t)e * F_ + rb * TR + lane] = val;
     }
 }
@@ -405,8 +407,10 @@ hipError_t launch_expand(int type, const ExpandArgs &a, hipStream_t s, int n_cu)
     const int n_tot = a.k + (a.shared ? 1 : 0);
     const size_t lds = lds_round(xq_bytes(a.H, type == GGML_TYPE_Q6_K ? 16 : 32));
     const int grid = a.F / TR * n_tot;
-    if (type == GGML_TYPE_Q4_K && TR == 16 && G == 64 && U == 1) {   // gate/up at H = 4096: row spans through LDS
-        k_expand_q4t<<<grid, 256, lds + 512 + 4 * 16 * 576, s>>>(a);
+    // gate/up at H = 4096: row spans through LDS, 16 rows per work-group; a
+    // down projection with groups of 32 takes the fp32 activations instead
+    if (type == GGML_TYPE_Q4_K && (TR == 16 || (a.act_only && a.act)) && G == 64 && U == 1) {
+        k_expand_q4t<<<a.F / 16 * n_tot, 256, lds + 512 + 4 * 16 * 576, s>>>(a);
         return hipGetLastError();
     }
 #define FO_K2(TT, RR, GG, UU) \
@@ -560,7 +564,13 @@ __global__ __launch_bounds__(64 * kTileMaxWaves) void k_reduce_tile(ReduceArgs a
         typename F::X X;
         int gi[F::NG];
         F::groups(slot, gi);
-        load_xslot(X, a.xq_act + (uint64_t)wv * a.xq_vstride, a.F, gi);
+        if (a.act_f32) {   // the slot prepared here from the fp32 activation (as prep_group_lanes would)
+#pragma unroll
+            for (int g = 0; g < F::NG; g++)
+                prep_group_regs<F::GSZ>(a.act_f32 + (uint64_t)wv * a.F + gi[g] * F::GSZ, X.l[g], X.sc[g], X.sum[g]);
+        } else {
+            load_xslot(X, a.xq_act + (uint64_t)wv * a.xq_vstride, a.F, gi);
+        }
         tile_block_dots<T, G, RBYTES>(m, X, tiles + wv * TSTRIDE, part[wv], row0, a.H, slot, live);
     } else if (own && wv == a.k) {
         uint8_t *dst = tiles + a.k * TSTRIDE;
@@ -585,6 +595,13 @@ __global__ __launch_bounds__(64 * kTileMaxWaves) void k_reduce_tile(ReduceArgs a
 // expert's block (its own type's size when sh_type >= 0).
 static uint32_t reduce_tile_lds(const ReduceArgs &a, uint32_t tstride) {
     return a.k * tstride + (a.shared ? (a.sh_type >= 0 ? tile_stride_1024(a.sh_type) : tstride) : 0);
+}
+
+bool reduce_takes_tile(int type, const ReduceArgs &a) {
+    const int n_tot = a.k + (a.shared ? 1 : 0);
+    return (type == GGML_TYPE_Q6_K || type == GGML_TYPE_Q4_K || type == GGML_TYPE_Q5_K) && n_tot <= kTileMaxWaves &&
+           reduce_tile_lds(a, (uint32_t)(kTileRows * a.row_bytes + 15) & ~15u) <= kTileLdsMax &&
+           a.H >= kTileRows && a.F == 1024;
 }
 
 bool reduce_takes_shared_type(int down_type, const ReduceArgs &a, int sh_type) {
@@ -624,12 +641,12 @@ hipError_t launch_reduce(int type, const ReduceArgs &a, hipStream_t s, int n_cu)
     // the LDS-staged variant when all n_tot 16-row blocks fit at once (and
     // the only one that takes a shared block in its own type)
     if (a.shared && a.sh_type >= 0 && !reduce_takes_shared_type(type, a, a.sh_type)) return hipErrorInvalidValue;
-    if (n_tot <= kTileMaxWaves && reduce_tile_lds(a, (uint32_t)(kTileRows * a.row_bytes + 15) & ~15u) <= kTileLdsMax &&
-        a.H >= kTileRows && a.F == 1024) {
+    if (reduce_takes_tile(type, a)) {
         if (type == GGML_TYPE_Q6_K) return reduce_tile<GGML_TYPE_Q6_K, 16, 840>(a, s);
         if (type == GGML_TYPE_Q4_K) return reduce_tile<GGML_TYPE_Q4_K, 16, 576>(a, s);
         if (type == GGML_TYPE_Q5_K) return reduce_tile<GGML_TYPE_Q5_K, 16, 704>(a, s);
     }
+    if (a.act_f32) return hipErrorInvalidValue;   // only the LDS-staged kernel prepares from fp32
     constexpr int RP = 4;
     const int RB = (64 / G) * RP;
     const int grid = (a.H + RB - 1) / RB;

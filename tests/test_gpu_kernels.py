@@ -619,6 +619,49 @@ def test_moe_layer_shared_rejects_bad_shapes(gpu):
     gpu.moe_layer(L, dh, dout, 0)
 
 
+@pytest.mark.parametrize("down,k,shared,sdown", [(O.Q5_K, 10, True, None), (O.Q4_K, 10, True, None),
+                                                   (O.Q5_K, 4, False, None), (O.Q4_K, 7, False, None),
+                                                   # shared down in its own type (gate/up as routed)
+                                                   (O.Q5_K, 10, True, O.Q6_K), (O.Q5_K, 8, True, O.Q8_0),
+                                                   (O.Q4_K, 10, True, O.Q6_K)])
+def test_moe_layer_down_groups_of_32(gpu, down, k, shared, sdown):
+    """The config shape (Q4_K gate/up 1024x4096) with Q4_K / Q5_K down
+    projections, whose activation groups are 32 values: the 16-row gate/up
+    kernel leaves fp32 activations and the down kernel prepares its groups
+    from them. Routing, weights and outputs against the fp32 oracle on the
+    same weights (reference src/inference.c:481-606)."""
+    from fomoe_amd import synthetic as S
+    from test_oracle import moe_desc
+    say(f"moe layer down={down} k={k} shared={shared} shared down={sdown}")
+    shape = S.LayerShape(n_experts=16, k=k, shared=shared, down_type=down)
+    E, H, F = shape.n_experts, shape.n_embd, shape.inter
+    L = S.build_layer(gpu, shape, 0, seed=41, norm=False)
+    d, keep = _prefill_host_layer(shape, 0, 41, False)
+    bl = None
+    if sdown is not None:
+        gs, ds = shape.gate_size, O.row_bytes(sdown, F) * H
+        bl = gpu.alloc(2 * gs + ds)
+        host = []
+        for t, off, M, K, kind in ((O.Q4_K, 0, F, H, 0), (O.Q4_K, gs, F, H, 1), (sdown, 2 * gs, H, F, 2)):
+            gpu.synth_quant(t, 42, kind, 0, 0.02, M, K, 1, bl.offset(off), 0)
+            host.append(O.synth_quant(t, 42, kind, 0.02, M, K))
+        sblob = np.concatenate(host)
+        assert np.array_equal(gpu.download(bl.ptr, np.uint8, sblob.size), sblob)
+        L.desc.shared, L.desc.shared_down_type = bl.ptr, sdown
+        d.shared, d.shared_down_type = sblob.ctypes.data, sdown
+    h = O.synth_f32(43, 0, 1.0, H)
+    dh, dout = gpu.upload(h), gpu.alloc(4 * H)
+    gpu.moe_layer(L.desc, dh, dout, FA.MOE_RESIDUAL)
+    got = gpu.download(dout, np.float32, H)
+    ids, w, sw = gpu.last_routing(k)
+    want, oi, ow = O.moe_layer(d, h, O.MOE_RESIDUAL)
+    assert np.array_equal(ids, oi)
+    assert inf_rel(w, ow) < 1e-5
+    e = inf_rel(got - h, want - h)
+    say(f"  inf_rel(ffn, fp32 oracle) {e:.3e} parity_err {parity_err(got, want):.3e}")
+    assert e < 1e-5 and parity_err(got, want) < 1e-3
+
+
 @pytest.mark.parametrize("seed", [4, 5, 6])
 def test_moe_layer_config3_full(gpu, seed):
     """Benchmark config 3 at full size: 512 experts (Q4_K gate/up 1024x4096, Q6_K
