@@ -1496,6 +1496,9 @@ constexpr uint32_t kPfThinLds = kPfThin * kPfThinX + kPfThinZero + kPfThinWaves 
 
 __global__ __launch_bounds__(64 * kPfThinWaves) void k_pf_down_thin(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sx[];
+    // the pairs' 2^s, read with the activations: a global load inside the
+    // tile loop would wait for the next tile's loads (issued before it)
+    __shared__ int s_pe[kPfThin];
     constexpr int NV = (kPfThinTile + 1023) / 1024;
     constexpr uint32_t rb = kPfThinRow, limb_bytes = 3 * kPfThinF;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -1542,6 +1545,7 @@ __global__ __launch_bounds__(64 * kPfThinWaves) void k_pf_down_thin(PrefillArgs 
             for (int Lq = 0; Lq < kLimbs; Lq++)
                 *(uint4 *)(xm + lane * 48 + 16 * Lq) = make_uint4(limb[Lq][0], limb[Lq][1], limb[Lq][2], limb[Lq][3]);
             *(float2 *)(xm + limb_bytes + lane * 8) = make_float2(scale, -32.f * sum);
+            if (lane == 0) s_pe[wv] = a.pexp[p0 + wv];
         }
         __syncthreads();
         for (int tt = 0; tt < kPfThinTPW; tt++) {
@@ -1561,7 +1565,7 @@ __global__ __launch_bounds__(64 * kPfThinWaves) void k_pf_down_thin(PrefillArgs 
                 acc += __shfl_xor(acc, 16);
                 acc += __shfl_xor(acc, 32);
                 if (g == 0)
-                    a.outp[(uint64_t)(p0 + m) * a.H + row0 + 16 * tt + r] = ldexpf(acc, a.pexp[p0 + m]);
+                    a.outp[(uint64_t)(p0 + m) * a.H + row0 + 16 * tt + r] = ldexpf(acc, s_pe[m]);
             }
         }
     }
