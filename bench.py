@@ -9,8 +9,9 @@ matrices; value = algorithmic bytes per step / time per step, with the
 weights already resident in HBM.
 
 Also measured in the same run (reported under "extra"): the config-1 Q4_K
-rotation, the Q8_0 and Q5_K variants of config 2, one MoE layer (config 3) per call,
-and the 60-layer HBM-resident decode stack (config 4) replayed from a HIP
+rotation, the Q8_0 and Q5_K variants of config 2, one MoE layer (config 3) per call
+(also with Q5_K / Q4_K routed down projections and with shared-expert tensors
+in their own types), and the 60-layer HBM-resident decode stack (config 4) replayed from a HIP
 graph, which gives the us-per-MoE-layer figure; the config-5 prefill (512
 bf16 tokens through one Zipf-routed layer on grouped bf16-MFMA GEMMs); plus
 the reference CPU path
@@ -280,8 +281,33 @@ def cpu_layer_baseline(gpu, layers, shape, seconds, n_sample=4):
                               f"{len(sample)} sampled layers (reference cpu_expert engine)"}
 
 
+def down_type_legs(gpu, calls, n=10):
+    """Config 3 with the routed down projections in Q5_K or Q4_K instead of
+    Q6_K (the real models' ffn_down_exps are partly Q5_K): n layers of
+    their own (rotated, so no call finds its experts in the Infinity Cache),
+    generated, timed over `calls` layer calls and freed before the 60-layer
+    stack is generated."""
+    res = {}
+    for name, dt in (("q5k", FA.Q5_K), ("q4k", FA.Q4_K)):
+        shape = S.LayerShape(down_type=dt)
+        layers = [S.build_layer(gpu, shape, l, seed=4, zipf_s=1.1) for l in range(n)]
+        h = S.hidden(gpu, shape.n_embd)
+        out = gpu.alloc(4 * shape.n_embd)
+        for i in range(3):
+            gpu.moe_layer(layers[i % n].desc, h, out, 0)
+        gpu.sync()
+        gpu.timer_start()
+        for i in range(calls):
+            gpu.moe_layer(layers[i % n].desc, h, out, 0)
+        res[f"config3_{name}_down_us_per_layer_call"] = round(gpu.timer_stop() * 1e3 / calls, 2)
+        gpu.sync()
+        del layers, h, out
+    return res
+
+
 def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0, cpu_seconds=0.0, probes=False):
     shape = S.LayerShape()
+    down_legs = down_type_legs(gpu, layer_calls)
     t0 = time.perf_counter()
     layers = []
     for l in range(n_layers):
@@ -335,7 +361,7 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
         if cl:
             res.update(cl)
             res["config3_speedup_vs_cpu_layer"] = round(cl["cpu_layer_us"] / us_layer_call, 1)
-    return {**res, **sp3, **sp4, **shexp,
+    return {**res, **sp3, **sp4, **shexp, **down_legs,
         "config3_us_per_layer_call": round(us_layer_call, 2),
         "config4_layers": n_layers, "config4_steps": stack_steps,
         "config4_tok_per_s": round(tok_s, 2),
