@@ -311,24 +311,39 @@ __global__ __launch_bounds__(256) void k_pf_topk(PrefillArgs a) {
 // W = ceil(T/32) words; counts and offsets over E+1 entries (entry E is the
 // shared expert, all T tokens).
 constexpr int kPfGroupLds = 16384;     // E*W words of each table
+// Row stride of k_pf_group's tables: W rounded up to odd
+__host__ __device__ constexpr int pf_group_stride(int W) { return W | 1; }
 
-// Exclusive prefix over the 1024 threads of 64-bit packed fields: inclusive
-// scan within each wave by shuffles, then the 16 wave totals (buf[0..15])
-// summed by every thread; two barriers per scan.
-FO_DEV uint64_t block_exclusive_scan64(uint64_t v, uint64_t *buf) {
+// Exclusive prefixes over the 1024 threads of 64-bit packed fields:
+// inclusive scans within each wave by shuffles, then the 16 wave totals
+// summed by every thread.
+// Four of them at once (two barriers for all four); buf holds 4 x 16 wave
+// totals.
+FO_DEV void block_exclusive_scan64x4(uint64_t v0, uint64_t v1, uint64_t v2, uint64_t v3, uint64_t &e0,
+                                     uint64_t &e1, uint64_t &e2, uint64_t &e3, uint64_t *buf) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    uint64_t x = v;
+    uint64_t x[4] = {v0, v1, v2, v3};
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t y = (uint64_t)__shfl_up((long long)x, o, 64);
-        if (lane >= o) x += y;
+        uint64_t y[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) y[q] = (uint64_t)__shfl_up((long long)x[q], o, 64);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (lane >= o) x[q] += y[q];
     }
-    if (lane == 63) buf[wv] = x;
+    if (lane == 63) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) buf[16 * q + wv] = x[q];
+    }
     __syncthreads();
-    uint64_t base = 0;
-    for (int w = 0; w < wv; w++) base += buf[w];
+    uint64_t base[4] = {0, 0, 0, 0};
+    for (int w = 0; w < wv; w++) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) base[q] += buf[16 * q + w];
+    }
     __syncthreads();
-    return base + x - v;
+    e0 = base[0] + x[0] - v0; e1 = base[1] + x[1] - v1; e2 = base[2] + x[2] - v2; e3 = base[3] + x[3] - v3;
 }
 
 // Bit fields of the packed scans (each field holds its total over all experts:
@@ -339,18 +354,19 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     extern __shared__ uint32_t lds[];
     const int tid = threadIdx.x;
     const int W = (a.T + 31) / 32, E = a.E, k = a.k, K1 = k + 1;
-    uint32_t *bm = lds, *pre = lds + E * W;
-    for (int i = tid; i < E * W; i += 1024) bm[i] = 0;
+    const int Ws = pf_group_stride(W);   // odd: thread e's row walk below is free of bank conflicts
+    uint32_t *bm = lds, *pre = lds + E * Ws;
+    for (int i = tid; i < E * Ws; i += 1024) bm[i] = 0;
     __syncthreads();
     for (int i = tid; i < a.T * k; i += 1024) {
         const int t = i / k, e = a.one_expert ? 0 : a.ids[i];
-        atomicOr(&bm[e * W + (t >> 5)], 1u << (t & 31));
+        atomicOr(&bm[e * Ws + (t >> 5)], 1u << (t & 31));
     }
     __syncthreads();
     const bool sh = a.shared != nullptr;
     int cnt = 0;
     if (tid < E) {
-        for (int w = 0; w < W; w++) { pre[tid * W + w] = cnt; cnt += __popc(bm[tid * W + w]); }
+        for (int w = 0; w < W; w++) { pre[tid * Ws + w] = cnt; cnt += __popc(bm[tid * Ws + w]); }
     } else if (tid == E && sh) {
         cnt = a.T;
     }
@@ -377,7 +393,7 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     const int dfull = dcnt / DT, drem = dcnt - DT * dfull, dcb = (drem + 15) >> 4;
     const int dthin = thin && in_dt;
     auto cls = [&](int b) { return b == 8 ? dfull + (dcb == 8) : (dcb == b && !dthin ? 1 : 0); };
-    __shared__ uint64_t scan64[16];
+    __shared__ uint64_t scan64[4 * 16];
     const uint64_t p1 = (uint64_t)cnt | ((uint64_t)nt << 21) | ((uint64_t)dn << 42);
     const uint64_t p2 = (uint64_t)c4 | ((uint64_t)c3 << 16) | ((uint64_t)c2 << 28) | ((uint64_t)c1 << 40) |
                         ((uint64_t)thin << 52);
@@ -385,8 +401,8 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     const uint64_t p3 = (uint64_t)cls(8) | ((uint64_t)cls(7) << 16) | ((uint64_t)cls(6) << 28) |
                         ((uint64_t)cls(5) << 40) | ((uint64_t)cls(4) << 52);
     const uint64_t p4 = (uint64_t)cls(3) | ((uint64_t)cls(2) << 12) | ((uint64_t)cls(1) << 24);
-    const uint64_t s1 = block_exclusive_scan64(p1, scan64), s2 = block_exclusive_scan64(p2, scan64);
-    const uint64_t s3 = block_exclusive_scan64(p3, scan64), s4 = block_exclusive_scan64(p4 | (p5 << 36), scan64);
+    uint64_t s1, s2, s3, s4;
+    block_exclusive_scan64x4(p1, p2, p3, p4 | (p5 << 36), s1, s2, s3, s4, scan64);
     const int off = (int)fld(s1, 0, 21), toff = (int)fld(s1, 21, 21), doff = (int)fld(s1, 42, 21);
     __shared__ uint64_t s_tot[4];
     if (tid == 1023) { s_tot[0] = s1 + p1; s_tot[1] = s2 + p2; s_tot[2] = s3 + p3; s_tot[3] = s4 + (p4 | (p5 << 36)); }
@@ -438,8 +454,8 @@ __global__ __launch_bounds__(1024) void k_pf_group(PrefillArgs a) {
     __syncthreads();
     for (int i = tid; i < a.T * k; i += 1024) {
         const int t = i / k, r = i - t * k, e = a.one_expert ? 0 : a.ids[i];
-        const uint32_t word = bm[e * W + (t >> 5)];
-        const int pos = s_off[e] + (int)pre[e * W + (t >> 5)] + __popc(word & ((1u << (t & 31)) - 1u));
+        const uint32_t word = bm[e * Ws + (t >> 5)];
+        const int pos = s_off[e] + (int)pre[e * Ws + (t >> 5)] + __popc(word & ((1u << (t & 31)) - 1u));
         a.pair_tok[pos] = t;
         a.pairpos[t * K1 + r] = pos;
     }
@@ -1703,11 +1719,11 @@ hipError_t launch_prefill(const PrefillArgs &a_, hipStream_t s) {
     static bool lds_attr = false;   // the grouping tables may exceed the 64 KiB default
     if (!lds_attr) {
         hipError_t e = hipFuncSetAttribute((const void *)k_pf_group, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           2 * kPfGroupLds * (int)sizeof(uint32_t));
+                                           2 * (kPfGroupLds + kMaxE) * (int)sizeof(uint32_t));
         if (e != hipSuccess) return e;
         lds_attr = true;
     }
-    k_pf_group<<<1, 1024, 2 * (size_t)a.E * W * sizeof(uint32_t), s>>>(a);
+    k_pf_group<<<1, 1024, 2 * (size_t)a.E * pf_group_stride(W) * sizeof(uint32_t), s>>>(a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     if (fp16_gateup) {   // exact fp16 operands
