@@ -96,6 +96,21 @@ def test_noalloc_shared_expert_own_types(gpu, st):
         _layer_pair(gpu, shape, seed, FA.MOE_NORM | FA.MOE_RESIDUAL, shared_types=(*st[0], st[1]))
 
 
+@pytest.mark.parametrize("down,st", [(FA.Q5_K, None), (FA.Q4_K, None),
+                                     (FA.Q5_K, ((FA.Q4_K, FA.Q4_K, FA.Q6_K), 1024))])
+def test_noalloc_down_groups_of_32(gpu, down, st):
+    """Q5_K / Q4_K routed down projections at the config shape (the gate/up
+    kernel leaves fp32 activations in the area, the down kernel prepares its
+    32-value groups from them), alone and with a Q6_K shared down block:
+    bit-identical to gpu_moe_layer, twice in a row."""
+    from fomoe_amd import synthetic as S
+    shape = S.LayerShape(n_embd=4096, inter=1024, n_experts=32, k=8, down_type=down)
+    say("noalloc down groups of 32", down, st)
+    for seed in (83, 84):
+        _layer_pair(gpu, shape, seed, FA.MOE_NORM | FA.MOE_RESIDUAL,
+                    shared_types=None if st is None else (*st[0], st[1]))
+
+
 def test_noalloc_rejects_layers_beyond_the_area(gpu):
     """H = F = 8192 with 16 + 1 experts needs ~1.1 MB of scratch: -1 and a
     message, before any device work (the descriptor's pointers are never read)."""
