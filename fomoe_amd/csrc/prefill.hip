@@ -1250,7 +1250,7 @@ __global__ __launch_bounds__(64 * kApWaves) void k_pf_actprep_w(PrefillArgs a, i
 // nearest-even, 2^-11 relative at most) against the fp16 activation rows of
 // k_pf_actprep, one MFMA per operand; the epilogue applies the pair's 2^s.
 // One activation plane halves the LDS of k_pf_down (64 KiB for two buffers).
-// One persistent work-group per CU (205 VGPRs, no spills) loops over the
+// One persistent work-group per CU (up to 256 VGPRs, two waves per SIMD) loops over the
 // items (tile, 256 rows) of its XCD: the next step's activation rows and
 // weights are requested before the current step is multiplied — the last
 // step of an item requests the next item's first, so no item starts on an
