@@ -1224,6 +1224,34 @@ def test_prefill_chunked_shared_own_types(gpu):
         assert e <= 3e-4
 
 
+@pytest.mark.parametrize("down", [O.Q6_K, O.Q5_K])
+def test_prefill_repeatable(gpu, down):
+    """Work-groups take their items from atomic counters, so which work-group
+    computes which output changes from call to call; every output is still
+    produced by one fixed sequence of operations: two calls on the same
+    input (config-3 expert shape, 300 tokens, Zipf routing, thin and thick
+    experts, a Q6_K or Q5_K down projection) are bit-identical, and so is a
+    call after a different batch has run in between."""
+    from fomoe_amd import synthetic as S
+    say(f"prefill repeatable down={down}")
+    shape = S.LayerShape(n_experts=64, k=8, down_type=down)
+    L = S.build_layer(gpu, shape, 0, seed=61, zipf_s=1.1, norm=False)
+    T, H = 300, shape.n_embd
+    dx = S.tokens_bf16(gpu, T, H, seed=62)
+    dy = S.tokens_bf16(gpu, 77, H, seed=63)
+    outs = []
+    for i in range(3):
+        dout = gpu.alloc(4 * T * H)
+        if i == 2:
+            dtmp = gpu.alloc(4 * 77 * H)
+            gpu.moe_prefill(L.desc, dy, 77, dtmp, 0)
+        gpu.moe_prefill(L.desc, dx, T, dout, 0)
+        outs.append(gpu.download(dout, np.float32, T * H))
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+
+
 def test_prefill_config5_sampled(gpu):
     """Config 5 at full size (512 tokens, 512 experts, top-10, H 4096, F 1024,
     Zipf(1.1) router bias): routing of every token against the oracle's fp32
