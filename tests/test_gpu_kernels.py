@@ -305,6 +305,65 @@ def test_moe_layer_norm_residual_gate(gpu):
     assert np.array_equal(got, (x + ffn).astype(np.float32))
 
 
+@pytest.mark.parametrize("E,k,shared", [(1024, 16, True), (1024, 16, False), (1024, 1, True), (17, 16, True)])
+def test_moe_layer_limits(gpu, E, k, shared):
+    """The largest expert count and top-k the layer takes (E <= 1024,
+    k <= 16; with the shared expert 17 slots, past the LDS-staged down
+    kernel's 12), and k = 1: routing and outputs against the fp32 oracle;
+    one expert or one more slot than that is refused with -1."""
+    from fomoe_amd import synthetic as S
+    say(f"layer limits E={E} k={k} shared={shared}")
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=E, k=k, shared=shared)
+    L = S.build_layer(gpu, shape, 0, seed=71, zipf_s=1.1, norm=False)
+    d, keep = _prefill_host_layer(shape, 0, 71, True)
+    h = O.synth_f32(72, 0, 1.0, shape.n_embd)
+    dh, dout = gpu.upload(h), gpu.alloc(4 * shape.n_embd)
+    gpu.moe_layer(L.desc, dh, dout, FA.MOE_RESIDUAL)
+    got = gpu.download(dout, np.float32, shape.n_embd)
+    ids, w, sw = gpu.last_routing(k)
+    want, oi, ow = O.moe_layer(d, h, O.MOE_RESIDUAL)
+    assert np.array_equal(ids, oi)
+    assert inf_rel(w, ow) < 1e-5
+    say(f"  inf_rel {inf_rel(got - h, want - h):.3e}")
+    assert inf_rel(got - h, want - h) < 1e-5
+    if E == 1024:
+        bad = FA.MoeLayer.from_buffer_copy(L.desc)
+        bad.n_experts = 1025
+        with pytest.raises(FA.GpuError):
+            gpu.moe_layer(bad, dh, dout, 0)
+    if k == 16:
+        bad = FA.MoeLayer.from_buffer_copy(L.desc)
+        bad.k = 17
+        with pytest.raises(FA.GpuError):
+            gpu.moe_layer(bad, dh, dout, 0)
+
+
+@pytest.mark.parametrize("E,k", [(1023, 16), (1023, 1)])
+def test_prefill_limits(gpu, E, k):
+    """Prefill at its largest expert count (E <= 1023) and top-k (k <= 16),
+    and k = 1: every token against the oracle's per-token composition;
+    E = 1024 or k = 17 is refused with -1."""
+    from fomoe_amd import synthetic as S
+    say(f"prefill limits E={E} k={k}")
+    T = 40
+    shape = S.LayerShape(n_embd=512, inter=256, n_experts=E, k=k, shared=True)
+    L = S.build_layer(gpu, shape, 0, seed=73, zipf_s=1.1, norm=False)
+    dx = S.tokens_bf16(gpu, T, shape.n_embd, seed=74)
+    dout = gpu.alloc(4 * T * shape.n_embd)
+    gpu.moe_prefill(L.desc, dx, T, dout, 0)
+    got = gpu.download(dout, np.float32, T * shape.n_embd).reshape(T, -1)
+    ids, w = gpu.prefill_routing(T, k)
+    x = O.to_bf16(O.synth_f32(74, S.stream(0, 0, S.TOKENS), 1.0, T * shape.n_embd)).reshape(T, -1)
+    d, keep = _prefill_host_layer(shape, 0, 73, True)
+    want, oids, ow = pf_check(got, d, x, 0, shape)
+    assert np.array_equal(ids, oids)
+    for field, v in (("n_experts", 1024), ("k", 17)):
+        bad = FA.MoeLayer.from_buffer_copy(L.desc)
+        setattr(bad, field, v)
+        with pytest.raises(FA.GpuError):
+            gpu.moe_prefill(bad, dx, T, dout, 0)
+
+
 @pytest.mark.parametrize("case", ["ties", "ties40", "E300_k15", "k3", "saturated", "saturated_k3"])
 def test_moe_layer_topk_ties_and_fallback(gpu, case):
     """Expert selection inside the layer (one or two arg-max rounds per
