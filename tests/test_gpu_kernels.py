@@ -1374,6 +1374,30 @@ def test_prefill_config5_sampled(gpu):
         assert parity_err(got[t], exact[0]) < CONFIG5_PARITY_BAR
 
 
+@pytest.mark.parametrize("down", [O.Q5_K, O.Q4_K])
+def test_stack_decode_down_groups_of_32(gpu, down):
+    """The graph-replayed stack with Q5_K / Q4_K routed down projections at
+    the config shape (the gate/up kernel's fp32 activation hand-off inside
+    the captured graph): bit-identical to the same layer calls issued one by
+    one, three layers, three steps."""
+    from fomoe_amd import synthetic as S
+    say(f"stack down={down}")
+    shape = S.LayerShape(n_experts=16, k=4, down_type=down)
+    layers = [S.build_layer(gpu, shape, l, seed=91, zipf_s=1.1) for l in range(3)]
+    descs = [L.desc for L in layers]
+    x0 = O.synth_f32(92, 0, 1.0, shape.n_embd)
+    dx, dy = gpu.upload(x0), gpu.upload(x0)
+    gpu.stack_decode(descs, dx, 3)
+    gpu.sync()
+    for _ in range(3):
+        for d in descs:
+            gpu.moe_layer(d, dy, dy, O.MOE_NORM | O.MOE_RESIDUAL)
+    a = gpu.download(dx, np.float32, shape.n_embd)
+    b = gpu.download(dy, np.float32, shape.n_embd)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_stack_decode_norm_and_shared_gate(gpu):
     """Stack decode with random RMSNorm weights and a shared-expert sigmoid
     gate on every layer: four layers with F = 1024 (the LDS-staged down
