@@ -305,7 +305,8 @@ def down_type_legs(gpu, calls, n=10):
     return res
 
 
-def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0, cpu_seconds=0.0, probes=False):
+def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0, cpu_seconds=0.0, probes=False,
+                        variants=True):
     shape = S.LayerShape()
     down_legs = down_type_legs(gpu, layer_calls)
     t0 = time.perf_counter()
@@ -355,7 +356,7 @@ def moe_layer_and_stack(gpu, n_layers, stack_steps, layer_calls, prefill_reps=0,
     layer_bytes = 4 * shape.n_experts * shape.n_embd + (shape.k + 1) * shape.expert_bytes()
     tok_s = stack_steps / (ms / 1e3)
     us_layer = ms * 1e3 / (stack_steps * n_layers)
-    res = prefill_config5(gpu, layers[0], shape, prefill_reps) if prefill_reps > 0 else {}
+    res = prefill_config5(gpu, layers[0], shape, prefill_reps, variants) if prefill_reps > 0 else {}
     if cpu_seconds > 0:
         cl = cpu_layer_baseline(gpu, layers, shape, cpu_seconds)
         if cl:
@@ -436,8 +437,9 @@ def shared_own_type_legs(gpu, layers, shape, h, out, n, calls):
     return res
 
 
-def prefill_config5(gpu, layer, shape, reps):
-    """Config 5: 512 bf16 tokens through one Zipf-routed layer (grouped GEMMs)."""
+def prefill_config5(gpu, layer, shape, reps, variants=True):
+    """Config 5: 512 bf16 tokens through one Zipf-routed layer (grouped GEMMs);
+    with `variants`, also the shared-expert own-type and Q5_K-down layers."""
     T, H, F, E, k = 512, shape.n_embd, shape.inter, shape.n_experts, shape.k
     x = S.tokens_bf16(gpu, T, H, seed=4)
     out = gpu.alloc(4 * T * H)
@@ -463,7 +465,7 @@ def prefill_config5(gpu, layer, shape, reps):
     # takes it, its down projection a launch of its own), or also its
     # intermediate size (F_s = 512: a one-expert pass of its own first)
     shexp = {}
-    for name, Fs in (("q8_0_down", F), ("q8_0_down_fs512", 512)):
+    for name, Fs in (("q8_0_down", F), ("q8_0_down_fs512", 512)) if variants else ():
         gs = FA.row_bytes(FA.Q4_K, H) * Fs
         ds = FA.row_bytes(FA.Q8_0, Fs) * H
         bl = gpu.alloc(2 * gs + ds)
@@ -482,16 +484,17 @@ def prefill_config5(gpu, layer, shape, reps):
         del bl
     # the same tokens through a layer whose routed down projections are Q5_K
     # (as in part of the real model's layers)
-    s5 = S.LayerShape(down_type=FA.Q5_K)
-    L5 = S.build_layer(gpu, s5, 1, seed=4, zipf_s=1.1, norm=False)
-    for _ in range(10):
-        gpu.moe_prefill(L5.desc, x, T, out, 0)
-    gpu.sync()
-    gpu.timer_start()
-    for _ in range(reps):
-        gpu.moe_prefill(L5.desc, x, T, out, 0)
-    shexp["config5_q5k_down_ms"] = round(gpu.timer_stop() / reps, 4)
-    del L5
+    if variants:
+        s5 = S.LayerShape(down_type=FA.Q5_K)
+        L5 = S.build_layer(gpu, s5, 1, seed=4, zipf_s=1.1, norm=False)
+        for _ in range(10):
+            gpu.moe_prefill(L5.desc, x, T, out, 0)
+        gpu.sync()
+        gpu.timer_start()
+        for _ in range(reps):
+            gpu.moe_prefill(L5.desc, x, T, out, 0)
+        shexp["config5_q5k_down_ms"] = round(gpu.timer_stop() / reps, 4)
+        del L5
     return {**sp5, **shexp, "config5_ms": round(ms, 4),
             "config5_tok_per_s": round(T / (ms / 1e3), 1),
             "config5_experts_touched": n_unique, "config5_weight_bytes": wbytes,
@@ -513,7 +516,7 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=20)
     ap.add_argument("--no-floor-probes", dest="floor_probes", action="store_false",
                     help="skip the load-only twins of the layer kernels (libfomoe_probe_gfx950.so)")
-    ap.add_argument("--skip", default="", help="comma list: q4k,q8_0,q5k,stack,cpu,prefill")
+    ap.add_argument("--skip", default="", help="comma list: q4k,q8_0,q5k,stack,cpu,prefill,pfvariants (the config-5 variant layers)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -571,7 +574,8 @@ def main():
     if "stack" not in skip and args.stack_layers > 0:
         extra.update(moe_layer_and_stack(gpu, args.stack_layers, args.stack_steps, args.layer_calls,
                                          0 if "prefill" in skip else args.prefill_reps,
-                                         0.0 if "cpu" in skip else args.cpu_seconds / 2, args.floor_probes))
+                                         0.0 if "cpu" in skip else args.cpu_seconds / 2, args.floor_probes,
+                                         "pfvariants" not in skip))
         log(f"stack: {extra['config4_tok_per_s']} tok/s, {extra['config4_us_per_layer']} us/layer")
         if "config5_ms" in extra:
             log(f"prefill: {extra['config5_ms']} ms per 512 tokens, {extra['config5_TFLOP/s']} TFLOP/s, "
